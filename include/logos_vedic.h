@@ -1,0 +1,201 @@
+/*
+ * logos_vedic.h -- C ABI of the MI355X-native (gfx950) LOGOS Vedic GEMM.
+ *
+ * Drop-in boundary for the GEMM hot path of LOGOS
+ * (reference: cuda/VedicGEMM.cuh, cuda/MixedPrecision.cuh).  Plain pointers
+ * and sizes only; device pointers are HIP device memory; `stream` is a
+ * hipStream_t (NULL = the null stream).  Every call is asynchronous on its
+ * stream unless stated otherwise, and returns a vedic_status_t.
+ *
+ * Layout: all matrices are row-major with an explicit leading dimension in
+ * elements.  Sizes are int (the reference uses int everywhere); element
+ * offsets are computed in 64 bits.
+ *
+ * Semantics of one GEMM (every entry point below is a special case of
+ * vedic_gemm):
+ *     acc   = op(A) . op(B)                      (fp32 accumulation)
+ *     t     = alpha * acc + beta * C_old         (C_old not read if beta == 0)
+ *     t     = t + bias[j]                        (if the epilogue has a bias)
+ *     pre   = t                                  (stored if preact != NULL)
+ *     C     = gelu_tanh(t) or t                  (per the epilogue)
+ * where gelu_tanh(x) = 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3)))
+ * (include/FeedForward.hpp:11-13).  For alpha = 1, beta = 0 the bias is added
+ * after the full dot product, as vedic_gemm_bias does
+ * (include/VedicGEMM.hpp:56-65).
+ *
+ * Errors follow the reference's conventions: shape errors are
+ * VEDIC_STATUS_BAD_DIM (the reference throws std::invalid_argument,
+ * include/VedicGEMM.hpp:27-30), device errors VEDIC_STATUS_HIP_ERROR (the
+ * reference throws std::runtime_error from CUDA_CHECK, cuda/VedicGEMM.cuh:111-133).
+ * The C++ header VedicGEMM_hip.hpp rethrows them as those exceptions.
+ */
+#ifndef LOGOS_VEDIC_H
+#define LOGOS_VEDIC_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    VEDIC_STATUS_OK = 0,
+    VEDIC_STATUS_BAD_DIM = 1,      /* non-positive or inconsistent M/N/K */
+    VEDIC_STATUS_BAD_LAYOUT = 2,   /* unknown op */
+    VEDIC_STATUS_NULL_POINTER = 3, /* required pointer is NULL */
+    VEDIC_STATUS_BAD_LD = 4,       /* leading dimension smaller than the row */
+    VEDIC_STATUS_BAD_EPILOGUE = 5, /* unknown epilogue / bias missing */
+    VEDIC_STATUS_BAD_DTYPE = 6,    /* unsupported dtype combination */
+    VEDIC_STATUS_HIP_ERROR = 7,    /* HIP runtime or launch error */
+    VEDIC_STATUS_TOO_LARGE = 8     /* size beyond a documented limit */
+} vedic_status_t;
+
+typedef enum {
+    VEDIC_OP_NN = 0, /* C[MxN] = A[MxK] . B[KxN]                       */
+    VEDIC_OP_NT = 1, /* C[MxN] = A[MxK] . B^T,  B stored [NxK]          */
+    VEDIC_OP_TN = 2  /* C[MxN] = A^T . B,       A stored [KxM], B [KxN] */
+} vedic_op_t;
+
+typedef enum {
+    VEDIC_EPI_NONE = 0,
+    VEDIC_EPI_BIAS = 1,      /* + bias[j]                 */
+    VEDIC_EPI_BIAS_GELU = 2, /* gelu_tanh(t + bias[j])    */
+    VEDIC_EPI_GELU = 3       /* gelu_tanh(t)              */
+} vedic_epilogue_t;
+
+typedef enum {
+    VEDIC_DT_F32 = 0, /* IEEE binary32 */
+    VEDIC_DT_F16 = 1  /* IEEE binary16 */
+} vedic_dtype_t;
+
+/* Full descriptor of one GEMM.  A and B share in_dtype; C is out_dtype
+ * (F16 output only with F16 inputs); bias and preact are always fp32. */
+typedef struct {
+    int op;        /* vedic_op_t */
+    int in_dtype;  /* vedic_dtype_t of A and B */
+    int out_dtype; /* vedic_dtype_t of C */
+    int M, N, K;
+    const void* A;
+    int64_t lda;
+    const void* B;
+    int64_t ldb;
+    void* C;
+    int64_t ldc;
+    float alpha;
+    float beta;
+    const float* bias; /* [N], required for *_BIAS* epilogues */
+    int epilogue;      /* vedic_epilogue_t */
+    float* preact;     /* optional [M x ld_preact] pre-activation output */
+    int64_t ld_preact;
+    void* stream;      /* hipStream_t */
+} vedic_gemm_desc_t;
+
+/* The general entry point.  New: the reference has no single descriptor
+ * call; every function below forwards to it. */
+int vedic_gemm(const vedic_gemm_desc_t* desc);
+
+/* ---- reference-compatible entry points ------------------------------- */
+
+/* C[MxN] = A[MxK] . B[KxN], fp32.
+ * Replaces cuda_vedic_gemm (cuda/VedicGEMM.cuh:182, cuda/VedicGEMM.cu:645-673). */
+int vedic_gemm_f32(const float* A, const float* B, float* C, int M, int K, int N, void* stream);
+
+/* C = A . W + bias[j], fp32.
+ * Replaces cuda_vedic_gemm_bias (cuda/VedicGEMM.cuh:184, cuda/VedicGEMM.cu:675-690). */
+int vedic_gemm_bias_f32(const float* A, const float* W, const float* bias, float* C, int M, int K,
+                        int N, void* stream);
+
+/* C[MxN] fp32 = alpha * A[MxK] . B[KxN] + beta * C, fp16 inputs, fp32 accumulate.
+ * Replaces cuda_gemm_fp16_fp32out (cuda/VedicGEMM.cuh:251, cuda/VedicGEMM.cu:1150-1178,
+ * cuda/MixedPrecision.cuh:301-330).  A, B point to binary16 data. */
+int vedic_gemm_f16_f32out(const void* A, int M, int K, const void* B, int N, float* C, float alpha,
+                          float beta, void* stream);
+
+/* Same with a binary16 C (fp32 accumulate, rounded once at the store).
+ * Replaces cuda_gemm_fp16_fp16out (cuda/VedicGEMM.cuh:252, cuda/VedicGEMM.cu:1182-1197). */
+int vedic_gemm_f16_f16out(const void* A, int M, int K, const void* B, int N, void* C, float alpha,
+                          float beta, void* stream);
+
+/* Fused FFN-up: H = gelu_tanh(X . W + bias), fp16 X/W, fp32 accumulate and
+ * output; preact (nullable) receives X . W + bias.
+ * Replaces the amp_gemm_bias + D2D copy + cuda_gelu sequence
+ * (cuda/ModelGPU.cu:1023-1028, cuda/VedicGEMM.cu:96-102,202-208,707-711). */
+int vedic_gemm_bias_gelu_f16(const void* X, const void* W, const float* bias, float* H,
+                             float* preact, int M, int K, int N, void* stream);
+
+/* fp32 form of the same fused epilogue (FeedForward::forward,
+ * include/FeedForward.hpp:112-114). */
+int vedic_gemm_bias_gelu_f32(const float* X, const float* W, const float* bias, float* H,
+                             float* preact, int M, int K, int N, void* stream);
+
+/* NT backward: dX[MxN] = dY[MxK] . W^T + beta * dX, W stored [NxK].
+ * Replaces lmhead_grad_dx / ffn_da / ffn_dx / attn_dConcat / attn_dHeadOut
+ * (cuda/train_gpu.cu:221-230,323-332,358-367,536-545,514-523; beta = 0) and
+ * attn_dX_from_QKV (:492-501; beta = 1). */
+int vedic_gemm_nt_f32(const float* dY, const float* W, float* dX, int M, int N, int K, float beta,
+                      void* stream);
+int vedic_gemm_nt_f16(const void* dY, const void* W, float* dX, int M, int N, int K, float beta,
+                      void* stream);
+
+/* TN backward: dW[MxN] = X^T . dY + beta * dW, X stored [KxM], dY [KxN].
+ * Replaces lmhead_grad_dw / ffn_w2_grad / ffn_w1_grad / attn_dWproj /
+ * attn_dWO / attn_dWQKV (cuda/train_gpu.cu:210-219,312-321,347-356,525-534,
+ * 503-512,481-490), which atomicAdd into zeroed, micro-batch-accumulated
+ * buffers: beta = 1 reproduces that accumulation deterministically. */
+int vedic_gemm_tn_f32(const float* X, const float* dY, float* dW, int M, int N, int K, float beta,
+                      void* stream);
+int vedic_gemm_tn_f16(const void* X, const void* dY, float* dW, int M, int N, int K, float beta,
+                      void* stream);
+
+/* ---- elementwise helpers on the path ---------------------------------- */
+
+/* C[i][j] += bias[j] over an MxN matrix.
+ * Replaces add_bias_kernel (cuda/VedicGEMM.cuh:191, cuda/VedicGEMM.cu:96-102). */
+int vedic_add_bias(float* C, const float* bias, int M, int N, void* stream);
+
+/* In-place tanh-GELU over n floats.
+ * Replaces cuda_gelu (cuda/VedicGEMM.cuh:187, cuda/VedicGEMM.cu:707-711). */
+int vedic_gelu(float* x, int64_t n, void* stream);
+
+/* dst = binary16(clamp(src, -65504, 65504)), round to nearest even.
+ * Replaces cuda_cast_fp32_to_fp16 (cuda/MixedPrecision.cuh:149-161,177-190). */
+int vedic_cast_f32_to_f16(const float* src, void* dst, int64_t n, void* stream);
+
+/* dst = float(src).  Replaces cuda_cast_fp16_to_fp32 (cuda/MixedPrecision.cuh:164-172,192-196). */
+int vedic_cast_f16_to_f32(const void* src, float* dst, int64_t n, void* stream);
+
+/* Gunitasamuchayah check of C = A . B (fp32, NN): sum(C) against
+ * colsum(A) . rowsum(B).  Synchronous (it returns host values).
+ * Replaces cuda_vedic_verify (cuda/VedicGEMM.cuh:193, cuda/VedicGEMM.cu:765-814). */
+typedef struct {
+    float checksum_C;
+    float checksum_vedic;
+    float relative_error;
+    int pass;
+} vedic_verify_result_t;
+
+int vedic_verify(const float* A, const float* B, const float* C, int M, int K, int N,
+                 float tolerance, vedic_verify_result_t* out, void* stream);
+
+/* ---- backend queries --------------------------------------------------- */
+
+/* Always 0: no vendor BLAS is linked.
+ * Replaces cuda_vedic_gemm_uses_cublas (cuda/VedicGEMM.cuh:183, cuda/VedicGEMM.cu:637-643). */
+int vedic_uses_vendor_blas(void);
+
+/* "hip-native-gfx950" -- for logs, as the reference logs its GEMM backend
+ * (cuda/train_gpu.cu:1920). */
+const char* vedic_backend_name(void);
+
+/* Human-readable text for a vedic_status_t. */
+const char* vedic_status_string(int status);
+
+/* The last HIP error code seen by this library on the calling thread
+ * (0 if none), for VEDIC_STATUS_HIP_ERROR diagnostics. */
+int vedic_last_hip_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOGOS_VEDIC_H */

@@ -1,0 +1,93 @@
+"""Build recipe for liblogos_vedic.so (the gfx950 HIP library) and the CPU oracle.
+
+Usage:  python -m logos_amd.build [--jobs N]
+
+The library is compiled in-tree with hipcc for gfx950 only.  Every HIP
+translation unit is compiled with packed-fp32 instruction selection disabled
+(``-Xclang -target-feature -Xclang -packed-fp32-ops``); the host pass prints a
+harmless "not a recognized feature" warning for it.
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "logos_amd")
+CSRC = os.path.join(PKG, "csrc")
+OBJ = os.path.join(PKG, "_build")
+LIB = os.path.join(PKG, "liblogos_vedic.so")
+SOURCES = ["vedic_gemm_mfma.hip", "vedic_capi.hip"]
+
+ARCH = "gfx950"
+HIPCC_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-ffp-contract=fast",
+    "-Wall",
+    "-Wno-unused-result",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found: the gfx950 library cannot be built")
+
+
+def _run(cmd: list[str], cwd: str | None = None) -> None:
+    proc = subprocess.run(cmd, cwd=cwd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(
+        line for line in proc.stdout.splitlines() if "packed-fp32-ops" not in line
+    )
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        sys.stderr.write(out + "\n")
+
+
+def build_library(jobs: int = 4) -> str:
+    os.makedirs(OBJ, exist_ok=True)
+    cc = hipcc()
+    objs = []
+    cmds = []
+    for src in SOURCES:
+        obj = os.path.join(OBJ, src.replace(".hip", ".o"))
+        objs.append(obj)
+        cmds.append([cc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+    with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        for f in [ex.submit(_run, c) for c in cmds]:
+            f.result()
+    tmp = LIB + ".tmp"
+    _run([cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp, *objs])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_oracle(with_reference: bool = True) -> None:
+    odir = os.path.join(ROOT, "oracle")
+    _run(["make", "-s", "-B", "liblogos_oracle.so"], cwd=odir)
+    if with_reference and os.path.isdir("/root/reference/include"):
+        _run(["make", "-s", "-B", "ref"], cwd=odir)
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=4)
+    ap.add_argument("--no-oracle", action="store_true")
+    args = ap.parse_args()
+    print(build_library(args.jobs))
+    if not args.no_oracle:
+        build_oracle()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,382 @@
+// vedic_capi.hip -- C ABI of liblogos_vedic.so (declared in include/logos_vedic.h):
+// argument validation, kernel selection, and the elementwise kernels of the
+// Vedic GEMM path (fp16 cast, bias, GELU, checksum verify).
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+
+#include "../../include/logos_vedic.h"
+#include "vedic_common.hpp"
+
+namespace vedic {
+hipError_t launch_gemm_f16(int op, bool vec, const GemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_f32(int op, bool vec, const GemmArgs& a, hipStream_t s);
+}  // namespace vedic
+
+using namespace vedic;
+
+static thread_local int g_last_hip_error = 0;
+
+static int hip_status(hipError_t e) {
+    if (e == hipSuccess) return VEDIC_STATUS_OK;
+    g_last_hip_error = (int)e;
+    return VEDIC_STATUS_HIP_ERROR;
+}
+
+static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// ------------------------------------------------------------------ GEMM
+
+extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
+    if (!d) return VEDIC_STATUS_NULL_POINTER;
+    if (d->M <= 0 || d->N <= 0 || d->K <= 0) return VEDIC_STATUS_BAD_DIM;
+    if (d->op < VEDIC_OP_NN || d->op > VEDIC_OP_TN) return VEDIC_STATUS_BAD_LAYOUT;
+    if (d->in_dtype != VEDIC_DT_F32 && d->in_dtype != VEDIC_DT_F16) return VEDIC_STATUS_BAD_DTYPE;
+    if (d->out_dtype != VEDIC_DT_F32 &&
+        !(d->out_dtype == VEDIC_DT_F16 && d->in_dtype == VEDIC_DT_F16))
+        return VEDIC_STATUS_BAD_DTYPE;
+    if (!d->A || !d->B || !d->C) return VEDIC_STATUS_NULL_POINTER;
+    if (d->epilogue < VEDIC_EPI_NONE || d->epilogue > VEDIC_EPI_GELU) return VEDIC_STATUS_BAD_EPILOGUE;
+    const bool want_bias = d->epilogue == VEDIC_EPI_BIAS || d->epilogue == VEDIC_EPI_BIAS_GELU;
+    if (want_bias && !d->bias) return VEDIC_STATUS_BAD_EPILOGUE;
+
+    const bool a_kc = d->op != VEDIC_OP_TN;
+    const bool b_kc = d->op == VEDIC_OP_NT;
+    const int64_t a_row = a_kc ? d->K : d->M;
+    const int64_t b_row = b_kc ? d->K : d->N;
+    if (d->lda < a_row || d->ldb < b_row || d->ldc < d->N) return VEDIC_STATUS_BAD_LD;
+    if (d->preact && d->ld_preact < d->N) return VEDIC_STATUS_BAD_LD;
+
+    GemmArgs a{};
+    a.A = d->A;
+    a.B = d->B;
+    a.C = d->C;
+    a.bias = want_bias ? d->bias : nullptr;
+    a.preact = d->preact;
+    a.lda = d->lda;
+    a.ldb = d->ldb;
+    a.ldc = d->ldc;
+    a.ldp = d->preact ? d->ld_preact : 0;
+    a.M = d->M;
+    a.N = d->N;
+    a.K = d->K;
+    a.alpha = d->alpha;
+    a.beta = d->beta;
+    a.epi = 0;
+    if (want_bias) a.epi |= EPI_BIAS;
+    if (d->epilogue == VEDIC_EPI_BIAS_GELU || d->epilogue == VEDIC_EPI_GELU) a.epi |= EPI_GELU;
+    if (d->preact) a.epi |= EPI_PREACT;
+    if (d->beta != 0.0f) a.epi |= EPI_BETA;
+    if (d->alpha != 1.0f) a.epi |= EPI_ALPHA;
+    if (d->out_dtype == VEDIC_DT_F16) a.epi |= EPI_F16OUT;
+    a.group_m = 8;
+
+    // 16-byte vector loads need aligned bases, leading dimensions that keep
+    // every row aligned, and contiguous extents that end on a chunk boundary.
+    const int ve = d->in_dtype == VEDIC_DT_F16 ? 8 : 4;
+    const bool vec = aligned16(d->A) && aligned16(d->B) && d->lda % ve == 0 && d->ldb % ve == 0 &&
+                     a_row % ve == 0 && b_row % ve == 0;
+
+    hipStream_t s = static_cast<hipStream_t>(d->stream);
+    hipError_t e = d->in_dtype == VEDIC_DT_F16 ? launch_gemm_f16(d->op, vec, a, s)
+                                               : launch_gemm_f32(d->op, vec, a, s);
+    return hip_status(e);
+}
+
+static vedic_gemm_desc_t make_desc(int op, int dt, int M, int N, int K, const void* A, int64_t lda,
+                                   const void* B, int64_t ldb, float* C, float alpha, float beta,
+                                   void* stream) {
+    vedic_gemm_desc_t d{};
+    d.op = op;
+    d.in_dtype = dt;
+    d.out_dtype = VEDIC_DT_F32;
+    d.M = M;
+    d.N = N;
+    d.K = K;
+    d.A = A;
+    d.lda = lda;
+    d.B = B;
+    d.ldb = ldb;
+    d.C = C;
+    d.ldc = N;
+    d.alpha = alpha;
+    d.beta = beta;
+    d.epilogue = VEDIC_EPI_NONE;
+    d.stream = stream;
+    return d;
+}
+
+extern "C" int vedic_gemm_f32(const float* A, const float* B, float* C, int M, int K, int N,
+                              void* stream) {
+    vedic_gemm_desc_t d = make_desc(VEDIC_OP_NN, VEDIC_DT_F32, M, N, K, A, K, B, N, C, 1.f, 0.f, stream);
+    return vedic_gemm(&d);
+}
+
+extern "C" int vedic_gemm_bias_f32(const float* A, const float* W, const float* bias, float* C,
+                                   int M, int K, int N, void* stream) {
+    vedic_gemm_desc_t d = make_desc(VEDIC_OP_NN, VEDIC_DT_F32, M, N, K, A, K, W, N, C, 1.f, 0.f, stream);
+    d.bias = bias;
+    d.epilogue = VEDIC_EPI_BIAS;
+    return vedic_gemm(&d);
+}
+
+extern "C" int vedic_gemm_f16_f32out(const void* A, int M, int K, const void* B, int N, float* C,
+                                     float alpha, float beta, void* stream) {
+    vedic_gemm_desc_t d = make_desc(VEDIC_OP_NN, VEDIC_DT_F16, M, N, K, A, K, B, N, C, alpha, beta, stream);
+    return vedic_gemm(&d);
+}
+
+extern "C" int vedic_gemm_f16_f16out(const void* A, int M, int K, const void* B, int N, void* C,
+                                     float alpha, float beta, void* stream) {
+    vedic_gemm_desc_t d =
+        make_desc(VEDIC_OP_NN, VEDIC_DT_F16, M, N, K, A, K, B, N, (float*)C, alpha, beta, stream);
+    d.out_dtype = VEDIC_DT_F16;
+    return vedic_gemm(&d);
+}
+
+extern "C" int vedic_gemm_bias_gelu_f16(const void* X, const void* W, const float* bias, float* H,
+                                        float* preact, int M, int K, int N, void* stream) {
+    vedic_gemm_desc_t d = make_desc(VEDIC_OP_NN, VEDIC_DT_F16, M, N, K, X, K, W, N, H, 1.f, 0.f, stream);
+    d.bias = bias;
+    d.epilogue = VEDIC_EPI_BIAS_GELU;
+    d.preact = preact;
+    d.ld_preact = N;
+    return vedic_gemm(&d);
+}
+
+extern "C" int vedic_gemm_bias_gelu_f32(const float* X, const float* W, const float* bias, float* H,
+                                        float* preact, int M, int K, int N, void* stream) {
+    vedic_gemm_desc_t d = make_desc(VEDIC_OP_NN, VEDIC_DT_F32, M, N, K, X, K, W, N, H, 1.f, 0.f, stream);
+    d.bias = bias;
+    d.epilogue = VEDIC_EPI_BIAS_GELU;
+    d.preact = preact;
+    d.ld_preact = N;
+    return vedic_gemm(&d);
+}
+
+extern "C" int vedic_gemm_nt_f32(const float* dY, const float* W, float* dX, int M, int N, int K,
+                                 float beta, void* stream) {
+    vedic_gemm_desc_t d = make_desc(VEDIC_OP_NT, VEDIC_DT_F32, M, N, K, dY, K, W, K, dX, 1.f, beta, stream);
+    return vedic_gemm(&d);
+}
+
+extern "C" int vedic_gemm_nt_f16(const void* dY, const void* W, float* dX, int M, int N, int K,
+                                 float beta, void* stream) {
+    vedic_gemm_desc_t d = make_desc(VEDIC_OP_NT, VEDIC_DT_F16, M, N, K, dY, K, W, K, dX, 1.f, beta, stream);
+    return vedic_gemm(&d);
+}
+
+extern "C" int vedic_gemm_tn_f32(const float* X, const float* dY, float* dW, int M, int N, int K,
+                                 float beta, void* stream) {
+    vedic_gemm_desc_t d = make_desc(VEDIC_OP_TN, VEDIC_DT_F32, M, N, K, X, M, dY, N, dW, 1.f, beta, stream);
+    return vedic_gemm(&d);
+}
+
+extern "C" int vedic_gemm_tn_f16(const void* X, const void* dY, float* dW, int M, int N, int K,
+                                 float beta, void* stream) {
+    vedic_gemm_desc_t d = make_desc(VEDIC_OP_TN, VEDIC_DT_F16, M, N, K, X, M, dY, N, dW, 1.f, beta, stream);
+    return vedic_gemm(&d);
+}
+
+// ----------------------------------------------------------- elementwise
+
+namespace {
+
+constexpr int kEwThreads = 256;
+
+inline unsigned ew_blocks(int64_t n, int per_thread) {
+    int64_t b = (n + (int64_t)kEwThreads * per_thread - 1) / ((int64_t)kEwThreads * per_thread);
+    if (b > 65536) b = 65536;  // grid-stride loops cover the rest
+    if (b < 1) b = 1;
+    return (unsigned)b;
+}
+
+__global__ void add_bias_kernel(float* __restrict__ C, const float* __restrict__ bias, int M, int N) {
+    const int64_t total = (int64_t)M * N;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x)
+        C[i] += bias[i % N];
+}
+
+__global__ void gelu_kernel(float* __restrict__ x, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        x[i] = gelu_tanh(x[i]);
+}
+
+__device__ __forceinline__ _Float16 to_half_clamped(float v) {
+    return (_Float16)fmaxf(fminf(v, 65504.0f), -65504.0f);
+}
+
+// Eight elements per thread per step when the buffers are 16-byte aligned.
+__global__ void cast_f32_f16_kernel(const float* __restrict__ src, _Float16* __restrict__ dst,
+                                    int64_t n, int vec) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (vec) {
+        const int64_t n8 = n / 8;
+        for (int64_t i = t; i < n8; i += stride) {
+            float4_t a = reinterpret_cast<const float4_t*>(src)[2 * i];
+            float4_t b = reinterpret_cast<const float4_t*>(src)[2 * i + 1];
+            half8_t h;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                h[j] = to_half_clamped(a[j]);
+                h[4 + j] = to_half_clamped(b[j]);
+            }
+            reinterpret_cast<half8_t*>(dst)[i] = h;
+        }
+        for (int64_t i = n8 * 8 + t; i < n; i += stride) dst[i] = to_half_clamped(src[i]);
+    } else {
+        for (int64_t i = t; i < n; i += stride) dst[i] = to_half_clamped(src[i]);
+    }
+}
+
+__global__ void cast_f16_f32_kernel(const _Float16* __restrict__ src, float* __restrict__ dst, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        dst[i] = (float)src[i];
+}
+
+// Deterministic reductions for vedic_verify, accumulated in double.
+// colsum[k] = sum_i A[i][k]: one block per 64 columns, 4 row phases, fixed
+// combine order.
+__global__ void colsum_kernel(const float* __restrict__ A, double* __restrict__ out, int M, int K) {
+    __shared__ double part[4][64];
+    const int c = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int ph = threadIdx.x >> 6;
+    double s = 0.0;
+    if (c < K)
+        for (int i = ph; i < M; i += 4) s += (double)A[(int64_t)i * K + c];
+    part[ph][threadIdx.x & 63] = s;
+    __syncthreads();
+    if (ph == 0 && c < K) out[c] = ((part[0][threadIdx.x] + part[1][threadIdx.x]) + part[2][threadIdx.x]) +
+                                   part[3][threadIdx.x];
+}
+
+// Sum of each of `rows` rows of length `cols` (one block per row, fixed tree).
+__global__ void rowsum_kernel(const float* __restrict__ B, double* __restrict__ out, int cols) {
+    __shared__ double red[kEwThreads];
+    const int64_t base = (int64_t)blockIdx.x * cols;
+    double s = 0.0;
+    for (int j = threadIdx.x; j < cols; j += kEwThreads) s += (double)B[base + j];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = kEwThreads / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = red[0];
+}
+
+// Partial sums of a flat array: block b sums elements b, b + G, b + 2G, ...
+// of the 256-strided layout, then a fixed tree.
+__global__ void arraysum_kernel(const float* __restrict__ x, int64_t n, double* __restrict__ out) {
+    __shared__ double red[kEwThreads];
+    double s = 0.0;
+    for (int64_t i = (int64_t)blockIdx.x * kEwThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kEwThreads)
+        s += (double)x[i];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = kEwThreads / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = red[0];
+}
+
+}  // namespace
+
+extern "C" int vedic_add_bias(float* C, const float* bias, int M, int N, void* stream) {
+    if (M <= 0 || N <= 0) return VEDIC_STATUS_BAD_DIM;
+    if (!C || !bias) return VEDIC_STATUS_NULL_POINTER;
+    hipLaunchKernelGGL(add_bias_kernel, dim3(ew_blocks((int64_t)M * N, 4)), dim3(kEwThreads), 0,
+                       static_cast<hipStream_t>(stream), C, bias, M, N);
+    return hip_status(hipGetLastError());
+}
+
+extern "C" int vedic_gelu(float* x, int64_t n, void* stream) {
+    if (n <= 0) return VEDIC_STATUS_BAD_DIM;
+    if (!x) return VEDIC_STATUS_NULL_POINTER;
+    hipLaunchKernelGGL(gelu_kernel, dim3(ew_blocks(n, 4)), dim3(kEwThreads), 0,
+                       static_cast<hipStream_t>(stream), x, n);
+    return hip_status(hipGetLastError());
+}
+
+extern "C" int vedic_cast_f32_to_f16(const float* src, void* dst, int64_t n, void* stream) {
+    if (n <= 0) return VEDIC_STATUS_BAD_DIM;
+    if (!src || !dst) return VEDIC_STATUS_NULL_POINTER;
+    const int vec = aligned16(src) && aligned16(dst);
+    hipLaunchKernelGGL(cast_f32_f16_kernel, dim3(ew_blocks(n, 8)), dim3(kEwThreads), 0,
+                       static_cast<hipStream_t>(stream), src, static_cast<_Float16*>(dst), n, vec);
+    return hip_status(hipGetLastError());
+}
+
+extern "C" int vedic_cast_f16_to_f32(const void* src, float* dst, int64_t n, void* stream) {
+    if (n <= 0) return VEDIC_STATUS_BAD_DIM;
+    if (!src || !dst) return VEDIC_STATUS_NULL_POINTER;
+    hipLaunchKernelGGL(cast_f16_f32_kernel, dim3(ew_blocks(n, 4)), dim3(kEwThreads), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const _Float16*>(src), dst, n);
+    return hip_status(hipGetLastError());
+}
+
+extern "C" int vedic_verify(const float* A, const float* B, const float* C, int M, int K, int N,
+                            float tolerance, vedic_verify_result_t* out, void* stream) {
+    if (M <= 0 || K <= 0 || N <= 0) return VEDIC_STATUS_BAD_DIM;
+    if (!A || !B || !C || !out) return VEDIC_STATUS_NULL_POINTER;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int nparts = 1024;
+    double* ws = nullptr;
+    const size_t bytes = sizeof(double) * ((size_t)K * 2 + nparts);
+    hipError_t e = hipMalloc(&ws, bytes);
+    if (e != hipSuccess) return hip_status(e);
+    double* d_col = ws;
+    double* d_row = ws + K;
+    double* d_part = ws + 2 * (size_t)K;
+    hipLaunchKernelGGL(colsum_kernel, dim3((K + 63) / 64), dim3(kEwThreads), 0, s, A, d_col, M, K);
+    hipLaunchKernelGGL(rowsum_kernel, dim3(K), dim3(kEwThreads), 0, s, B, d_row, N);
+    hipLaunchKernelGGL(arraysum_kernel, dim3(nparts), dim3(kEwThreads), 0, s, C, (int64_t)M * N, d_part);
+    e = hipGetLastError();
+    double* host = (double*)malloc(bytes);
+    if (e == hipSuccess && !host) e = hipErrorOutOfMemory;
+    if (e == hipSuccess) e = hipMemcpyAsync(host, ws, bytes, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(ws);
+    if (e != hipSuccess) {
+        free(host);
+        return hip_status(e);
+    }
+    double pred = 0.0, sum_c = 0.0;
+    for (int k = 0; k < K; ++k) pred += host[k] * host[K + k];
+    for (int p = 0; p < nparts; ++p) sum_c += host[2 * (size_t)K + p];
+    free(host);
+    out->checksum_C = (float)sum_c;
+    out->checksum_vedic = (float)pred;
+    out->relative_error = fabsf(out->checksum_C - out->checksum_vedic) / (fabsf(out->checksum_vedic) + 1e-6f);
+    out->pass = out->relative_error < tolerance;
+    return VEDIC_STATUS_OK;
+}
+
+// --------------------------------------------------------------- queries
+
+extern "C" int vedic_uses_vendor_blas(void) { return 0; }
+
+extern "C" const char* vedic_backend_name(void) { return "hip-native-gfx950"; }
+
+extern "C" int vedic_last_hip_error(void) { return g_last_hip_error; }
+
+extern "C" const char* vedic_status_string(int status) {
+    switch (status) {
+        case VEDIC_STATUS_OK: return "ok";
+        case VEDIC_STATUS_BAD_DIM: return "bad dimension (non-positive or mismatched M/N/K)";
+        case VEDIC_STATUS_BAD_LAYOUT: return "bad layout (op must be NN, NT or TN)";
+        case VEDIC_STATUS_NULL_POINTER: return "null pointer";
+        case VEDIC_STATUS_BAD_LD: return "leading dimension smaller than the row length";
+        case VEDIC_STATUS_BAD_EPILOGUE: return "bad epilogue (unknown, or bias missing)";
+        case VEDIC_STATUS_BAD_DTYPE: return "unsupported dtype combination";
+        case VEDIC_STATUS_HIP_ERROR: return "HIP runtime error";
+        case VEDIC_STATUS_TOO_LARGE: return "size beyond the documented limit";
+    }
+    return "unknown status";
+}

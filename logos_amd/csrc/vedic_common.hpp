@@ -1,0 +1,71 @@
+// vedic_common.hpp -- shared device types and helpers for the gfx950 Vedic
+// GEMM kernels.  Internal to logos_amd/csrc; the public surface is the C ABI
+// in include/logos_vedic.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vedic {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// One LDS tile row holds 128 bytes of the contraction dimension: 64 fp16 or
+// 32 fp32 values.  A row is eight 16-byte chunks.
+constexpr int kRowBytes = 128;
+
+// 16-byte chunk swizzle.  Chunk c of tile row r is stored at chunk position
+// c ^ swz(r).  With swz(r) = (r ^ (r >> 3)) & 7:
+//  - an MFMA operand read (lane l reads row l%32, one chunk) touches eight
+//    distinct 16-byte positions per eight consecutive rows: no bank conflict
+//    for 8-lane (32-bank) or 16-lane (64-bank) service groups;
+//  - the transposed staging writes (rows 8 or 4 apart in consecutive lanes)
+//    also land on distinct positions per eight lanes.
+__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
+
+__device__ __forceinline__ uint32_t lds_offset(int row, int chunk) {
+    return (uint32_t)(row * kRowBytes + ((chunk ^ swz(row)) << 4));
+}
+
+// tanh-GELU, 0.5 x (1 + tanh(c (x + 0.044715 x^3))), c = sqrt(2/pi), written
+// in the algebraically equal logistic form x / (1 + exp(-2u)) with
+// u = c (x + 0.044715 x^3), and exp(-2u) = exp2(x * (k0 + k1 x^2)).
+// Limits: x -> +inf gives exp2 -> 0 and x; x -> -inf gives exp2 -> inf and
+// x * 0 = -0; NaN propagates.  Error is a few ulp of fp32 (one exp2, one
+// reciprocal), well inside the fp32 parity bound.
+__device__ __forceinline__ float gelu_tanh(float x) {
+    constexpr float k0 = -2.0f * 0.7978845608f * 1.4426950408889634f;             // -2c log2(e)
+    constexpr float k1 = -2.0f * 0.7978845608f * 0.044715f * 1.4426950408889634f; // -2c 0.044715 log2(e)
+    float x2 = x * x;
+    float e = __builtin_amdgcn_exp2f(x * __builtin_fmaf(k1, x2, k0));
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// Epilogue flag bits (internal).
+enum : int {
+    EPI_BIAS = 1,
+    EPI_GELU = 2,
+    EPI_PREACT = 4,
+    EPI_BETA = 8,
+    EPI_ALPHA = 16,
+    EPI_F16OUT = 32,
+};
+
+struct GemmArgs {
+    const void* A;
+    const void* B;
+    void* C;
+    const float* bias;
+    float* preact;
+    int64_t lda, ldb, ldc, ldp;
+    int M, N, K;
+    float alpha, beta;
+    int epi;
+    int tiles_m, tiles_n;
+    int group_m;
+};
+
+}  // namespace vedic

@@ -1,0 +1,239 @@
+"""Python mirror of the LOGOS Vedic GEMM API over the gfx950 C ABI.
+
+Names and argument meaning follow the reference:
+  vedic_gemm(A, B)                 include/VedicGEMM.hpp:25-54 / cuda_vedic_gemm
+  vedic_gemm_bias(A, W, bias)      include/VedicGEMM.hpp:56-65 / cuda_vedic_gemm_bias
+  gemm_fp16_fp32out(A, B, ...)     cuda_gemm_fp16_fp32out (cuda/VedicGEMM.cu:1150)
+  gemm_fp16_fp16out(A, B, ...)     cuda_gemm_fp16_fp16out (cuda/VedicGEMM.cu:1182)
+  gemm_nt(dY, W) / gemm_tn(X, dY)  the NT/TN backward products (include/Backprop.hpp:48-63,
+                                   cuda/train_gpu.cu:210-545)
+  gemm_bias_gelu(X, W, b)          FeedForward::forward's first half (include/FeedForward.hpp:112-114)
+  add_bias / gelu_ / cast_*        add_bias_kernel, cuda_gelu, cuda_cast_fp32_to_fp16 ...
+  verify(A, B, C)                  cuda_vedic_verify (cuda/VedicGEMM.cu:765-814)
+
+Operands are torch tensors resident on the GPU (torch is used for device
+memory and streams only); every call runs on torch's current stream.  Shape
+errors raise ValueError (the reference's std::invalid_argument), device
+errors RuntimeError (its std::runtime_error).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import DT_F16, DT_F32, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU, EPI_NONE, OP_NN, OP_NT, OP_TN
+
+__all__ = [
+    "OP_NN", "OP_NT", "OP_TN", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU", "EPI_GELU",
+    "gemm", "vedic_gemm", "vedic_gemm_bias", "gemm_fp16_fp32out", "gemm_fp16_fp16out",
+    "gemm_bias_gelu", "gemm_nt", "gemm_tn", "add_bias", "gelu_", "cast_fp32_to_fp16",
+    "cast_fp16_to_fp32", "verify", "VerifyResult", "uses_vendor_blas", "backend_name",
+]
+
+_DT = {torch.float32: DT_F32, torch.float16: DT_F16}
+
+
+def _check(status: int) -> None:
+    if status == _lib.STATUS_OK:
+        return
+    msg = _lib.status_string(status)
+    if status in (_lib.STATUS_BAD_DIM, _lib.STATUS_BAD_LD, _lib.STATUS_BAD_LAYOUT,
+                  _lib.STATUS_BAD_EPILOGUE, _lib.STATUS_BAD_DTYPE, _lib.STATUS_NULL_POINTER,
+                  _lib.STATUS_TOO_LARGE):
+        raise ValueError(f"VedicGEMM: {msg}")
+    code = _lib.load().vedic_last_hip_error()
+    raise RuntimeError(f"VedicGEMM: {msg} (hipError {code})")
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _mat(t: torch.Tensor, name: str) -> tuple[int, int, int]:
+    """(rows, cols, leading dimension) of a row-major 2-D GPU matrix."""
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be on the GPU")
+    if t.dim() == 1:
+        t = t.view(1, -1)
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be 2-D, got shape {tuple(t.shape)}")
+    r, c = t.shape
+    if c > 1 and t.stride(1) != 1:
+        raise ValueError(f"{name} must be row-major with unit column stride")
+    ld = t.stride(0) if r > 1 else c
+    return r, c, max(ld, c)
+
+
+def gemm(op: int, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor | None = None, *,
+         alpha: float = 1.0, beta: float = 0.0, bias: torch.Tensor | None = None,
+         epilogue: int = EPI_NONE, preact: torch.Tensor | None = None,
+         out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """General GEMM: C = epi(alpha * op(A) op(B) + beta * C + bias) (see include/logos_vedic.h)."""
+    if A.dtype != B.dtype or A.dtype not in _DT:
+        raise ValueError(f"A and B must share dtype float16 or float32 (got {A.dtype}, {B.dtype})")
+    ar, ac, lda = _mat(A, "A")
+    br, bc, ldb = _mat(B, "B")
+    if op == OP_NN:
+        M, K, N, Kb = ar, ac, bc, br
+    elif op == OP_NT:
+        M, K, N, Kb = ar, ac, br, bc
+    elif op == OP_TN:
+        M, K, N, Kb = ac, ar, bc, br
+    else:
+        raise ValueError(f"unknown op {op}")
+    if Kb != K:
+        raise ValueError(f"VedicGEMM: inner dimensions differ (A gives K={K}, B gives K={Kb})")
+    if C is None:
+        if beta != 0.0:
+            raise ValueError("beta != 0 needs an existing C")
+        C = torch.empty((M, N), dtype=out_dtype, device=A.device)
+    cr, cc, ldc = _mat(C, "C")
+    if (cr, cc) != (M, N):
+        raise ValueError(f"C must be {M}x{N}, got {cr}x{cc}")
+    if C.dtype not in _DT:
+        raise ValueError("C must be float32 or float16")
+    if bias is not None:
+        if bias.dtype != torch.float32 or bias.numel() != N or not bias.is_cuda:
+            raise ValueError(f"bias must be {N} float32 values on the GPU")
+        bias = bias.contiguous()
+    ldp = 0
+    if preact is not None:
+        pr, pc, ldp = _mat(preact, "preact")
+        if (pr, pc) != (M, N) or preact.dtype != torch.float32:
+            raise ValueError(f"preact must be float32 {M}x{N}")
+    d = _lib.GemmDesc(
+        op=op, in_dtype=_DT[A.dtype], out_dtype=_DT[C.dtype], M=M, N=N, K=K,
+        A=A.data_ptr(), lda=lda, B=B.data_ptr(), ldb=ldb, C=C.data_ptr(), ldc=ldc,
+        alpha=alpha, beta=beta, bias=bias.data_ptr() if bias is not None else None,
+        epilogue=epilogue, preact=preact.data_ptr() if preact is not None else None,
+        ld_preact=ldp, stream=_stream(),
+    )
+    _check(_lib.load().vedic_gemm(ctypes.byref(d)))
+    return C
+
+
+def vedic_gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """C = A . B in fp32 (vedic_gemm / cuda_vedic_gemm)."""
+    if A.dtype != torch.float32:
+        raise ValueError("vedic_gemm takes float32 operands")
+    return gemm(OP_NN, A, B, out)
+
+
+def vedic_gemm_bias(A: torch.Tensor, W: torch.Tensor, bias: torch.Tensor,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """C = A . W + bias[j] in fp32 (vedic_gemm_bias / cuda_vedic_gemm_bias)."""
+    if A.dtype != torch.float32:
+        raise ValueError("vedic_gemm_bias takes float32 operands")
+    return gemm(OP_NN, A, W, out, bias=bias, epilogue=EPI_BIAS)
+
+
+def gemm_fp16_fp32out(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor | None = None,
+                      alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
+    """fp32 C = alpha A.B + beta C with fp16 A, B (cuda_gemm_fp16_fp32out)."""
+    if A.dtype != torch.float16:
+        raise ValueError("gemm_fp16_fp32out takes float16 operands")
+    return gemm(OP_NN, A, B, C, alpha=alpha, beta=beta)
+
+
+def gemm_fp16_fp16out(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor | None = None,
+                      alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
+    """fp16 C = alpha A.B + beta C, fp32 accumulation (cuda_gemm_fp16_fp16out)."""
+    if A.dtype != torch.float16:
+        raise ValueError("gemm_fp16_fp16out takes float16 operands")
+    return gemm(OP_NN, A, B, C, alpha=alpha, beta=beta, out_dtype=torch.float16)
+
+
+def gemm_bias_gelu(X: torch.Tensor, W: torch.Tensor, bias: torch.Tensor,
+                   out: torch.Tensor | None = None, preact: torch.Tensor | None = None) -> torch.Tensor:
+    """H = gelu_tanh(X . W + bias), fp32 output; preact receives X . W + bias."""
+    return gemm(OP_NN, X, W, out, bias=bias, epilogue=EPI_BIAS_GELU, preact=preact)
+
+
+def gemm_nt(dY: torch.Tensor, W: torch.Tensor, out: torch.Tensor | None = None,
+            beta: float = 0.0) -> torch.Tensor:
+    """dX = dY . W^T (+ beta dX); W stored [N x K]."""
+    return gemm(OP_NT, dY, W, out, beta=beta)
+
+
+def gemm_tn(X: torch.Tensor, dY: torch.Tensor, out: torch.Tensor | None = None,
+            beta: float = 0.0) -> torch.Tensor:
+    """dW = X^T . dY (+ beta dW); X stored [K x M], dY [K x N]."""
+    return gemm(OP_TN, X, dY, out, beta=beta)
+
+
+def add_bias(C: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """C[i][j] += bias[j] in place (add_bias_kernel)."""
+    M, N, ld = _mat(C, "C")
+    if ld != N or C.dtype != torch.float32:
+        raise ValueError("C must be a contiguous float32 matrix")
+    if bias.numel() != N or bias.dtype != torch.float32:
+        raise ValueError("bias size mismatch")
+    _check(_lib.load().vedic_add_bias(C.data_ptr(), bias.contiguous().data_ptr(), M, N, _stream()))
+    return C
+
+
+def gelu_(x: torch.Tensor) -> torch.Tensor:
+    """In-place tanh-GELU (cuda_gelu)."""
+    if not x.is_cuda or x.dtype != torch.float32 or not x.is_contiguous():
+        raise ValueError("gelu_ takes a contiguous float32 GPU tensor")
+    _check(_lib.load().vedic_gelu(x.data_ptr(), x.numel(), _stream()))
+    return x
+
+
+def cast_fp32_to_fp16(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp16 copy with the reference's +-65504 clamp (cuda_cast_fp32_to_fp16)."""
+    if not x.is_cuda or x.dtype != torch.float32 or not x.is_contiguous():
+        raise ValueError("cast_fp32_to_fp16 takes a contiguous float32 GPU tensor")
+    if out is None:
+        out = torch.empty(x.shape, dtype=torch.float16, device=x.device)
+    if out.numel() != x.numel() or out.dtype != torch.float16 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous float16 tensor of the same size")
+    _check(_lib.load().vedic_cast_f32_to_f16(x.data_ptr(), out.data_ptr(), x.numel(), _stream()))
+    return out
+
+
+def cast_fp16_to_fp32(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 copy of an fp16 tensor (cuda_cast_fp16_to_fp32)."""
+    if not x.is_cuda or x.dtype != torch.float16 or not x.is_contiguous():
+        raise ValueError("cast_fp16_to_fp32 takes a contiguous float16 GPU tensor")
+    if out is None:
+        out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    _check(_lib.load().vedic_cast_f16_to_f32(x.data_ptr(), out.data_ptr(), x.numel(), _stream()))
+    return out
+
+
+@dataclass
+class VerifyResult:
+    """Mirror of VedicVerifyResult (cuda/VedicGEMM.cuh:162-167)."""
+
+    checksum_C: float
+    checksum_vedic: float
+    relative_error: float
+    passed: bool
+
+
+def verify(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, tolerance: float = 0.01) -> VerifyResult:
+    """Gunitasamuchayah check: sum(C) against colsum(A) . rowsum(B)."""
+    M, K, lda = _mat(A, "A")
+    Kb, N, ldb = _mat(B, "B")
+    Mc, Nc, ldc = _mat(C, "C")
+    if Kb != K or (Mc, Nc) != (M, N) or lda != K or ldb != N or ldc != N:
+        raise ValueError("verify takes contiguous A[MxK], B[KxN], C[MxN]")
+    r = _lib.VerifyResult()
+    _check(_lib.load().vedic_verify(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, K, N, tolerance,
+                                    ctypes.byref(r), _stream()))
+    return VerifyResult(r.checksum_C, r.checksum_vedic, r.relative_error, bool(r.pass_))
+
+
+def uses_vendor_blas() -> bool:
+    """Always False (cuda_vedic_gemm_uses_cublas's counterpart)."""
+    return bool(_lib.load().vedic_uses_vendor_blas())
+
+
+def backend_name() -> str:
+    return _lib.load().vedic_backend_name().decode()

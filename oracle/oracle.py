@@ -1,0 +1,294 @@
+"""numpy front end of the CPU oracle (liblogos_oracle.so) and of the reference's
+own CPU GEMM built in place (oracle/_ref/libvedic_ref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker.  The product (logos_amd/) never
+imports it.  See vedic_oracle.c for what each function restates and how it is
+pinned.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_LIB = os.path.join(HERE, "liblogos_oracle.so")
+REF_LIB = os.path.join(HERE, "_ref", "libvedic_ref.so")
+
+_fp = ctypes.POINTER(ctypes.c_float)
+_dp = ctypes.POINTER(ctypes.c_double)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+
+_lib = None
+_ref = None
+
+NN, NT, TN = 0, 1, 2
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(ORACLE_LIB):
+            raise RuntimeError(f"{ORACLE_LIB} missing: run `make -C oracle`")
+        lib = ctypes.CDLL(ORACLE_LIB)
+        sig = {
+            "oracle_vedic_gemm": [_fp, _fp, _fp, _i, _i, _i, _i],
+            "oracle_reference_gemm": [_fp, _fp, _fp, _i, _i, _i],
+            "oracle_vedic_gemm_bias": [_fp, _fp, _fp, _fp, _i, _i, _i, _i],
+            "oracle_gelu_inplace": [_fp, _i64],
+            "oracle_transpose": [_fp, _fp, _i, _i],
+            "oracle_gemm_nt": [_fp, _fp, _fp, _i, _i, _i, _i],
+            "oracle_gemm_tn": [_fp, _fp, _fp, _i, _i, _i, _i, _i],
+            "oracle_f32_to_f16": [_fp, _u16p, _i64],
+            "oracle_f16_to_f32": [_u16p, _fp, _i64],
+            "oracle_gemm_f64": [_i, _fp, _fp, _fp, _i, _i, _i, _i, _dp, _dp, _i],
+            "oracle_checksum": [_fp, _fp, _fp, _i, _i, _i, _dp, _dp],
+        }
+        for name, args in sig.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = None if name in ("oracle_gelu_inplace", "oracle_transpose",
+                                          "oracle_f32_to_f16", "oracle_f16_to_f32") else _i
+        _lib = lib
+    return _lib
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_LIB)
+
+
+def _load_ref():
+    global _ref
+    if _ref is None:
+        lib = ctypes.CDLL(REF_LIB)
+        sig = {
+            "ref_vedic_gemm": [_fp, _fp, _fp, _i, _i, _i],
+            "ref_reference_gemm": [_fp, _fp, _fp, _i, _i, _i],
+            "ref_vedic_gemm_bias": [_fp, _fp, _fp, _fp, _i, _i, _i],
+            "ref_gelu_inplace": [_fp, ctypes.c_longlong],
+            "ref_gemm_nt": [_fp, _fp, _fp, _i, _i, _i],
+            "ref_gemm_tn": [_fp, _fp, _fp, _i, _i, _i, _i],
+        }
+        for name, args in sig.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = None if name == "ref_gelu_inplace" else _i
+        _ref = lib
+    return _ref
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(_fp)
+
+
+def _nthreads(n):
+    return n if n is not None else (os.cpu_count() or 1)
+
+
+# ---------------------------------------------------------------- restatement
+
+def vedic_gemm(A, B, nthreads=None) -> np.ndarray:
+    """Bitwise restatement of include/VedicGEMM.hpp:25-54 (fp32, k ascending)."""
+    A, B = _f32(A), _f32(B)
+    M, K = A.shape
+    if B.shape[0] != K:
+        raise ValueError("VedicGEMM: dimension mismatch")
+    N = B.shape[1]
+    C = np.empty((M, N), np.float32)
+    if _load().oracle_vedic_gemm(_p(A), _p(B), _p(C), M, K, N, _nthreads(nthreads)):
+        raise ValueError("VedicGEMM: bad dimension")
+    return C
+
+
+def reference_gemm(A, B) -> np.ndarray:
+    A, B = _f32(A), _f32(B)
+    M, K = A.shape
+    N = B.shape[1]
+    C = np.empty((M, N), np.float32)
+    if _load().oracle_reference_gemm(_p(A), _p(B), _p(C), M, K, N):
+        raise ValueError("reference_gemm: bad dimension")
+    return C
+
+
+def vedic_gemm_bias(A, W, bias, nthreads=None) -> np.ndarray:
+    A, W, bias = _f32(A), _f32(W), _f32(bias).reshape(-1)
+    M, K = A.shape
+    N = W.shape[1]
+    if W.shape[0] != K or bias.size != N:
+        raise ValueError("vedic_gemm_bias: size mismatch")
+    C = np.empty((M, N), np.float32)
+    if _load().oracle_vedic_gemm_bias(_p(A), _p(W), _p(bias), _p(C), M, K, N, _nthreads(nthreads)):
+        raise ValueError("vedic_gemm_bias: bad dimension")
+    return C
+
+
+def gelu(x) -> np.ndarray:
+    y = np.array(x, dtype=np.float32, copy=True, order="C")
+    _load().oracle_gelu_inplace(_p(y), y.size)
+    return y
+
+
+def gemm_nt(dY, W, nthreads=None) -> np.ndarray:
+    dY, W = _f32(dY), _f32(W)
+    M, K = dY.shape
+    N = W.shape[0]
+    out = np.empty((M, N), np.float32)
+    if _load().oracle_gemm_nt(_p(dY), _p(W), _p(out), M, N, K, _nthreads(nthreads)):
+        raise ValueError("gemm_nt: bad dimension")
+    return out
+
+
+def gemm_tn(X, dY, accumulate_into=None, nthreads=None) -> np.ndarray:
+    X, dY = _f32(X), _f32(dY)
+    K, M = X.shape
+    N = dY.shape[1]
+    if accumulate_into is not None:
+        out = np.array(accumulate_into, dtype=np.float32, copy=True, order="C")
+        acc = 1
+    else:
+        out = np.empty((M, N), np.float32)
+        acc = 0
+    if _load().oracle_gemm_tn(_p(X), _p(dY), _p(out), M, N, K, acc, _nthreads(nthreads)):
+        raise ValueError("gemm_tn: bad dimension")
+    return out
+
+
+def f32_to_f16_bits(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty(x.shape, np.uint16)
+    _load().oracle_f32_to_f16(_p(x), out.ctypes.data_as(_u16p), x.size)
+    return out
+
+
+def f16_round(x) -> np.ndarray:
+    """fp32 values rounded through binary16 (clamp + RNE) and widened back."""
+    bits = f32_to_f16_bits(x)
+    out = np.empty(bits.shape, np.float32)
+    _load().oracle_f16_to_f32(bits.ctypes.data_as(_u16p), _p(out), bits.size)
+    return out
+
+
+def gemm_f64(layout, A, B, bias=None, gelu=False, nthreads=None):
+    """(out, absdot) in float64 for op(A) op(B) (+bias) (gelu)."""
+    A, B = _f32(A), _f32(B)
+    if layout == NN:
+        M, K = A.shape
+        N = B.shape[1]
+    elif layout == NT:
+        M, K = A.shape
+        N = B.shape[0]
+    else:
+        K, M = A.shape
+        N = B.shape[1]
+    out = np.empty((M, N), np.float64)
+    absdot = np.empty((M, N), np.float64)
+    bp = None
+    if bias is not None:
+        bias = _f32(bias).reshape(-1)
+        bp = _p(bias)
+    rc = _load().oracle_gemm_f64(layout, _p(A), _p(B), bp, 1 if gelu else 0, M, N, K,
+                                 out.ctypes.data_as(_dp), absdot.ctypes.data_as(_dp),
+                                 _nthreads(nthreads))
+    if rc:
+        raise ValueError("gemm_f64: bad arguments")
+    return out, absdot
+
+
+def checksum(A, B, C):
+    A, B, C = _f32(A), _f32(B), _f32(C)
+    M, K = A.shape
+    N = B.shape[1]
+    s = ctypes.c_double()
+    p = ctypes.c_double()
+    _load().oracle_checksum(_p(A), _p(B), _p(C), M, K, N, ctypes.byref(s), ctypes.byref(p))
+    return s.value, p.value
+
+
+# -------------------------------------------------- the reference, built in place
+
+def ref_vedic_gemm(A, B) -> np.ndarray:
+    A, B = _f32(A), _f32(B)
+    M, K = A.shape
+    N = B.shape[1]
+    C = np.empty((M, N), np.float32)
+    if _load_ref().ref_vedic_gemm(_p(A), _p(B), _p(C), M, K, N):
+        raise ValueError("reference vedic_gemm threw")
+    return C
+
+
+def ref_reference_gemm(A, B) -> np.ndarray:
+    A, B = _f32(A), _f32(B)
+    M, K = A.shape
+    N = B.shape[1]
+    C = np.empty((M, N), np.float32)
+    if _load_ref().ref_reference_gemm(_p(A), _p(B), _p(C), M, K, N):
+        raise ValueError("reference reference_gemm threw")
+    return C
+
+
+def ref_vedic_gemm_bias(A, W, bias) -> np.ndarray:
+    A, W, bias = _f32(A), _f32(W), _f32(bias).reshape(-1)
+    M, K = A.shape
+    N = W.shape[1]
+    C = np.empty((M, N), np.float32)
+    if _load_ref().ref_vedic_gemm_bias(_p(A), _p(W), _p(bias), _p(C), M, K, N):
+        raise ValueError("reference vedic_gemm_bias threw")
+    return C
+
+
+def ref_gelu(x) -> np.ndarray:
+    y = np.array(x, dtype=np.float32, copy=True, order="C")
+    _load_ref().ref_gelu_inplace(_p(y), y.size)
+    return y
+
+
+def ref_gemm_nt(dY, W) -> np.ndarray:
+    dY, W = _f32(dY), _f32(W)
+    M, K = dY.shape
+    N = W.shape[0]
+    out = np.empty((M, N), np.float32)
+    if _load_ref().ref_gemm_nt(_p(dY), _p(W), _p(out), M, N, K):
+        raise ValueError("reference NT threw")
+    return out
+
+
+def ref_gemm_tn(X, dY, accumulate_into=None) -> np.ndarray:
+    X, dY = _f32(X), _f32(dY)
+    K, M = X.shape
+    N = dY.shape[1]
+    if accumulate_into is not None:
+        out = np.array(accumulate_into, dtype=np.float32, copy=True, order="C")
+    else:
+        out = np.empty((M, N), np.float32)
+    if _load_ref().ref_gemm_tn(_p(X), _p(dY), _p(out), M, N, K, 1 if accumulate_into is not None else 0):
+        raise ValueError("reference TN threw")
+    return out
+
+
+# ------------------------------------------------------------ parity metrics
+
+def inf_rel_err(got, want64) -> float:
+    """max |got - want| / max |want| (the infinity-norm relative error)."""
+    got = np.asarray(got, dtype=np.float64)
+    want64 = np.asarray(want64, dtype=np.float64)
+    denom = float(np.max(np.abs(want64))) if want64.size else 0.0
+    num = float(np.max(np.abs(got - want64))) if want64.size else 0.0
+    if denom == 0.0:
+        return num
+    return num / denom
+
+
+def fp32_tolerance(K: int) -> float:
+    """Max relative error bound for the FP32 path: 1e-5 * sqrt(K)."""
+    return 1e-5 * float(np.sqrt(K))
+
+
+FP16_TOLERANCE = 2e-3

@@ -1,0 +1,90 @@
+"""CPU checks of the C ABI: the library loads, exports every function that
+include/logos_vedic.h declares, and rejects bad arguments before any device
+work (the reference throws std::invalid_argument for these,
+include/VedicGEMM.hpp:27-30,59-60).  No kernel is launched here."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from logos_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "logos_vedic.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vedic_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_surface():
+    names = declared_functions()
+    for must in ["vedic_gemm", "vedic_gemm_f32", "vedic_gemm_bias_f32", "vedic_gemm_f16_f32out",
+                 "vedic_gemm_f16_f16out", "vedic_gemm_bias_gelu_f16", "vedic_gemm_nt_f16",
+                 "vedic_gemm_tn_f16", "vedic_cast_f32_to_f16", "vedic_verify"]:
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert set(declared_functions()) == set(_lib.SIGNATURES), "binding table out of date"
+
+
+def test_backend_queries():
+    lib = _lib.load()
+    assert lib.vedic_uses_vendor_blas() == 0
+    assert lib.vedic_backend_name() == b"hip-native-gfx950"
+    assert _lib.status_string(_lib.STATUS_BAD_DIM).startswith("bad dimension")
+
+
+def _desc(**kw):
+    d = dict(op=0, in_dtype=0, out_dtype=0, M=4, N=4, K=4, A=16, lda=4, B=16, ldb=4, C=16, ldc=4,
+             alpha=1.0, beta=0.0, bias=None, epilogue=0, preact=None, ld_preact=0, stream=None)
+    d.update(kw)
+    return _lib.GemmDesc(**d)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(M=0), _lib.STATUS_BAD_DIM),
+    (dict(N=-1), _lib.STATUS_BAD_DIM),
+    (dict(K=0), _lib.STATUS_BAD_DIM),
+    (dict(op=3), _lib.STATUS_BAD_LAYOUT),
+    (dict(in_dtype=2), _lib.STATUS_BAD_DTYPE),
+    (dict(out_dtype=1), _lib.STATUS_BAD_DTYPE),  # fp16 out needs fp16 in
+    (dict(A=None), _lib.STATUS_NULL_POINTER),
+    (dict(C=None), _lib.STATUS_NULL_POINTER),
+    (dict(lda=3), _lib.STATUS_BAD_LD),
+    (dict(op=2, lda=3), _lib.STATUS_BAD_LD),
+    (dict(ldc=2), _lib.STATUS_BAD_LD),
+    (dict(epilogue=1), _lib.STATUS_BAD_EPILOGUE),  # bias missing
+    (dict(epilogue=9), _lib.STATUS_BAD_EPILOGUE),
+])
+def test_gemm_validation(kw, status):
+    d = _desc(**kw)
+    assert _lib.load().vedic_gemm(ctypes.byref(d)) == status
+
+
+def test_null_descriptor_and_helpers():
+    lib = _lib.load()
+    assert lib.vedic_gemm(None) == _lib.STATUS_NULL_POINTER
+    assert lib.vedic_gemm_f32(None, None, None, 0, 4, 4, None) == _lib.STATUS_BAD_DIM
+    assert lib.vedic_gemm_f16_f32out(None, 4, 4, None, 4, None, 1.0, 0.0, None) == _lib.STATUS_NULL_POINTER
+    assert lib.vedic_add_bias(None, None, 0, 3, None) == _lib.STATUS_BAD_DIM
+    assert lib.vedic_gelu(None, 0, None) == _lib.STATUS_BAD_DIM
+    assert lib.vedic_cast_f32_to_f16(None, None, 5, None) == _lib.STATUS_NULL_POINTER
+    r = _lib.VerifyResult()
+    assert lib.vedic_verify(None, None, None, 1, 0, 1, 0.01, ctypes.byref(r), None) == _lib.STATUS_BAD_DIM
+
+
+def test_python_mirror_rejects_cpu_tensors():
+    import torch
+
+    from logos_amd import vedic
+
+    with pytest.raises(ValueError):
+        vedic.vedic_gemm(torch.ones(2, 2), torch.ones(2, 2))

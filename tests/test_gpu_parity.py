@@ -1,0 +1,263 @@
+"""GPU parity of the gfx950 kernels against the CPU oracle, through the C ABI.
+
+Bar (the north star's): infinity-norm relative error against an fp64 oracle
+on the same inputs <= 1e-5 * sqrt(K) for FP32 and <= 2e-3 for fp16-in /
+fp32-accumulate (fp16 inputs rounded by the reference's clamp + RNE cast, the
+oracle fed the same rounded values).  The bitwise restatement of the
+reference's CPU vedic_gemm is compared too, at the sum of both bounds.
+Integer and byte work (the fp16 cast) is compared bit for bit.
+"""
+import zlib
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import oracle as o  # noqa: E402
+from tests._gpu_helpers import (FP16_TOL, check, dev, dev_f16, fp32_tol, host, normal,  # noqa: E402
+                                restated)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from logos_amd import vedic
+
+    assert vedic.backend_name() == "hip-native-gfx950"
+    yield
+
+
+def V():
+    from logos_amd import vedic
+
+    return vedic
+
+
+# ---------------------------------------------------------------- known answers
+
+def test_kat_small_exact():
+    vedic = V()
+    C = host(vedic.vedic_gemm(dev(np.array([[1, 2], [3, 4]], np.float32)),
+                              dev(np.array([[5, 6], [7, 8]], np.float32))))
+    assert C.tolist() == [[19, 22], [43, 50]]
+    I = dev(np.eye(2, dtype=np.float32))
+    assert host(vedic.vedic_gemm_bias(I, I, dev(np.array([3, 5], np.float32)))).tolist() == [[4, 5], [3, 6]]
+    A = np.arange(1, 10, dtype=np.float32).reshape(3, 3)
+    B = np.arange(9, 0, -1, dtype=np.float32).reshape(3, 3)
+    C = host(vedic.vedic_gemm(dev(A), dev(B)))
+    assert C[0, 0] == 30 and C[2, 2] == 90
+    C = host(vedic.vedic_gemm(dev(np.array([[1, 10, 100, 1000], [2, 20, 200, 2000]], np.float32)),
+                              dev(np.array([[1, 0], [0, 1], [1, 0], [0, 1]], np.float32))))
+    assert C[0].tolist() == [101, 1010]
+    # S6: constant A=1, B=2, K=8 -> 16 (tests/test_syntax_build.cu:196-260)
+    assert np.all(host(vedic.vedic_gemm(dev(np.ones((4, 8), np.float32)),
+                                        dev(np.full((8, 4), 2.0, np.float32)))) == 16.0)
+    # M22 second 64-row tile with A @ I = A (exact)
+    Am = np.array([[(i + 1) * 10 + (k + 1) for k in range(3)] for i in range(70)], np.float32)
+    assert np.array_equal(host(vedic.vedic_gemm(dev(Am), dev(np.eye(3, dtype=np.float32)))), Am)
+    # fp16 path on small integers is exact (products exact, sums < 2^24)
+    rng = np.random.default_rng(11)
+    Ai = rng.integers(-8, 9, (40, 72)).astype(np.float32)
+    Bi = rng.integers(-8, 9, (72, 24)).astype(np.float32)
+    a16, _ = dev_f16(Ai)
+    b16, _ = dev_f16(Bi)
+    assert np.array_equal(host(vedic.gemm_fp16_fp32out(a16, b16)), Ai.astype(np.float64) @ Bi)
+
+
+def test_golden_vectors(golden):
+    vedic = V()
+    g = golden
+    for key in [k for k in g if k.startswith("nn_") and k.endswith("_C")]:
+        base = key[:-2]
+        A, B = g[base + "_A"], g[base + "_B"]
+        got = host(vedic.vedic_gemm(dev(A), dev(B)))
+        want = g[key]
+        assert o.inf_rel_err(got, want) <= 2 * fp32_tol(A.shape[1]), base
+    got = host(vedic.vedic_gemm_bias(dev(g["bias_A"]), dev(g["bias_W"]), dev(g["bias_b"])))
+    assert o.inf_rel_err(got, g["bias_C"]) <= 2 * fp32_tol(33)
+    got = host(vedic.gemm_bias_gelu(dev(g["bias_A"]), dev(g["bias_W"]), dev(g["bias_b"])))
+    assert o.inf_rel_err(got, g["gelu_H"]) <= 2 * fp32_tol(33)
+    x = dev(g["gelu_x"])
+    assert o.inf_rel_err(host(vedic.gelu_(x)), g["gelu_y"]) <= 1e-6
+    got = host(vedic.gemm_nt(dev(g["nt_dY"]), dev(g["nt_W"])))
+    assert o.inf_rel_err(got, g["nt_dX"]) <= 2 * fp32_tol(31)
+    got = host(vedic.gemm_tn(dev(g["tn_X"]), dev(g["tn_dY"])))
+    assert o.inf_rel_err(got, g["tn_dW"]) <= 2 * fp32_tol(31)
+    acc = dev(g["tn_pre"])
+    got = host(vedic.gemm_tn(dev(g["tn_X"]), dev(g["tn_dY"]), out=acc, beta=1.0))
+    assert o.inf_rel_err(got, g["tn_dW_acc"]) <= 2 * fp32_tol(31)
+
+
+# ----------------------------------------------------- random shapes, all paths
+
+SHAPES = [(1, 1, 1), (3, 5, 7), (17, 33, 19), (64, 64, 64), (65, 66, 67), (128, 256, 128),
+          (129, 257, 130), (200, 136, 264), (300, 1000, 520), (513, 1001, 257)]
+OPS = {"NN": o.NN, "NT": o.NT, "TN": o.TN}
+
+
+def _operands(rng, layout, M, N, K):
+    A = normal(rng, (K, M) if layout == o.TN else (M, K))
+    B = normal(rng, (N, K) if layout == o.NT else (K, N), std=0.5)
+    return A, B
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("opname", list(OPS))
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_random_shapes(dtype, opname, shape):
+    vedic = V()
+    layout = OPS[opname]
+    M, N, K = shape
+    rng = np.random.default_rng(zlib.crc32(f"{dtype}-{opname}-{shape}".encode()))
+    A, B = _operands(rng, layout, M, N, K)
+    if dtype == "f16":
+        a, A = dev_f16(A)
+        b, B = dev_f16(B)
+        tol = FP16_TOL
+    else:
+        a, b = dev(A), dev(B)
+        tol = fp32_tol(K)
+    got = host(vedic.gemm(layout, a, b))
+    err = check(got, layout, A, B, tol=tol, label=f"{dtype} {opname} {shape}")
+    ref = restated(layout, A, B)
+    err2 = o.inf_rel_err(got, ref)
+    assert err2 <= tol + fp32_tol(K), f"vs restatement {err2:.3e}"
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("opname", list(OPS))
+def test_epilogues_alpha_beta_preact(dtype, opname):
+    vedic = V()
+    layout = OPS[opname]
+    rng = np.random.default_rng(99)
+    for (M, N, K) in [(77, 141, 96), (256, 512, 320)]:
+        A, B = _operands(rng, layout, M, N, K)
+        bias = normal(rng, (N,), std=0.1)
+        C0 = normal(rng, (M, N))
+        if dtype == "f16":
+            a, A = dev_f16(A)
+            b, B = dev_f16(B)
+            tol = FP16_TOL
+        else:
+            a, b = dev(A), dev(B)
+            tol = fp32_tol(K)
+        # bias only
+        got = host(vedic.gemm(layout, a, b, bias=dev(bias), epilogue=vedic.EPI_BIAS))
+        check(got, layout, A, B, tol=tol, bias=bias, label="bias")
+        # bias + gelu with the pre-activation stored
+        pre = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        got = host(vedic.gemm(layout, a, b, bias=dev(bias), epilogue=vedic.EPI_BIAS_GELU, preact=pre))
+        check(got, layout, A, B, tol=tol, bias=bias, gelu=True, label="bias+gelu")
+        check(host(pre), layout, A, B, tol=tol, bias=bias, label="preact")
+        # gelu without bias
+        got = host(vedic.gemm(layout, a, b, epilogue=vedic.EPI_GELU))
+        check(got, layout, A, B, tol=tol, gelu=True, label="gelu")
+        # alpha, beta accumulate
+        c = dev(C0)
+        got = host(vedic.gemm(layout, a, b, c, alpha=0.5, beta=1.0))
+        check(got, layout, A, B, tol=tol, alpha=0.5, beta=1.0, C0=C0, label="alpha/beta")
+
+
+def test_leading_dimensions_and_unaligned_views():
+    vedic = V()
+    rng = np.random.default_rng(5)
+    M, N, K = 96, 80, 72
+    # operands that are column slices of wider buffers (ld > cols)
+    Abig = normal(rng, (M, K + 8))
+    Bbig = normal(rng, (K, N + 16))
+    a = dev(Abig)[:, :K]
+    b = dev(Bbig)[:, 3:3 + N]  # base offset of 3 floats: not 16-byte aligned
+    Cbig = torch.zeros((M, N + 5), dtype=torch.float32, device="cuda")
+    c = Cbig[:, :N]
+    vedic.gemm(vedic.OP_NN, a, b, c)
+    got = host(c)
+    check(got, o.NN, Abig[:, :K], Bbig[:, 3:3 + N], tol=fp32_tol(K), label="ld views")
+    assert np.all(host(Cbig)[:, N:] == 0), "store outside C's columns"
+    # fp16 with odd K (element-wise loader)
+    A = normal(rng, (33, 45))
+    B = normal(rng, (45, 29))
+    a16, Ar = dev_f16(A)
+    b16, Br = dev_f16(B)
+    check(host(vedic.gemm_fp16_fp32out(a16, b16)), o.NN, Ar, Br, tol=FP16_TOL, label="odd fp16")
+
+
+def test_fp16_output():
+    vedic = V()
+    rng = np.random.default_rng(6)
+    M, N, K = 130, 264, 200
+    A, B = normal(rng, (M, K)), normal(rng, (K, N), std=0.1)
+    a, A = dev_f16(A)
+    b, B = dev_f16(B)
+    got = host(vedic.gemm_fp16_fp16out(a, b))
+    # one extra binary16 rounding of the result: relative 2^-11 on top
+    check(got, o.NN, A, B, tol=FP16_TOL + 2.0 ** -11, label="f16 out")
+    C0 = normal(rng, (M, N))
+    c = dev(C0).half()
+    got = host(vedic.gemm_fp16_fp16out(a, b, c, alpha=2.0, beta=0.5))
+    C0r = o.f16_round(C0)
+    check(got, o.NN, A, B, tol=FP16_TOL + 2.0 ** -10, alpha=2.0, beta=0.5, C0=C0r, label="f16 out ab")
+
+
+def test_no_write_outside_c():
+    vedic = V()
+    rng = np.random.default_rng(7)
+    M, N, K = 100, 70, 64
+    A, B = normal(rng, (M, K)), normal(rng, (K, N))
+    buf = torch.full((M + 2, N), 7.0, dtype=torch.float32, device="cuda")
+    vedic.vedic_gemm(dev(A), dev(B), out=buf[1:M + 1])
+    h = host(buf)
+    assert np.all(h[0] == 7.0) and np.all(h[M + 1] == 7.0)
+
+
+def test_shape_errors_raise():
+    vedic = V()
+    with pytest.raises(ValueError):
+        vedic.vedic_gemm(dev(np.ones((2, 3), np.float32)), dev(np.ones((4, 2), np.float32)))
+    with pytest.raises(ValueError):
+        vedic.vedic_gemm_bias(dev(np.ones((2, 3), np.float32)), dev(np.ones((3, 4), np.float32)),
+                              dev(np.ones(3, np.float32)))
+
+
+# ------------------------------------------------------------- helper kernels
+
+def test_cast_bitexact_and_helpers():
+    vedic = V()
+    rng = np.random.default_rng(8)
+    x = np.concatenate([(rng.standard_normal(100003) * 3000).astype(np.float32),
+                        np.array([1e6, -1e6, np.inf, -np.inf, 65519, 65520, 3e-8, 6e-8, -0.0], np.float32)])
+    got = vedic.cast_fp32_to_fp16(dev(x)).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, o.f32_to_f16_bits(x))
+    # unaligned (element-wise path)
+    t = dev(np.concatenate([np.zeros(1, np.float32), x]))[1:]
+    out = torch.empty(x.size + 1, dtype=torch.float16, device="cuda")[1:]
+    vedic.cast_fp32_to_fp16(t, out)
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), o.f32_to_f16_bits(x))
+    h = vedic.cast_fp16_to_fp32(vedic.cast_fp32_to_fp16(dev(x)))
+    assert np.array_equal(host(h), o.f16_round(x))
+    # add_bias (add_bias_kernel semantics, tests/test_cuda_kernels.cu:123-168)
+    C = normal(rng, (4, 8))
+    b = normal(rng, (8,))
+    got = host(vedic.add_bias(dev(C), dev(b)))
+    assert np.array_equal(got, C + b)
+    # gelu_ against the fp32 reference gelu
+    y = normal(rng, (4097,), std=3.0)
+    assert o.inf_rel_err(host(vedic.gelu_(dev(y))), o.gelu(y)) <= 1e-6
+
+
+def test_verify_checksum():
+    vedic = V()
+    rng = np.random.default_rng(9)
+    for (M, K, N) in [(32, 64, 32), (63, 97, 47), (128, 256, 128), (16, 512, 16)]:
+        # positive inputs keep colsum(A) . rowsum(B) far from zero
+        A, B = normal(rng, (M, K), absval=True), normal(rng, (K, N), absval=True)
+        a, b = dev(A), dev(B)
+        c = vedic.vedic_gemm(a, b)
+        r = vedic.verify(a, b, c, tolerance=0.05)
+        s, p = o.checksum(A, B, host(c))
+        assert r.passed
+        assert abs(r.checksum_vedic - p) <= 1e-5 * max(1.0, abs(p))
+        assert abs(r.checksum_C - s) <= 1e-5 * max(1.0, abs(s))

@@ -1,0 +1,217 @@
+"""Pins the CPU oracle (oracle/vedic_oracle.c) before it is trusted as the GPU checker.
+
+Each check is chosen so a plausible mistake in the oracle (dropped term, wrong
+index, transposed operand, wrong rounding) fails it:
+  * the reference's own known-answer tests (tests/test_math_unit.cpp M1, M17,
+    M22; tests/test_syntax_build.cu S6; tests/test_cuda_kernels.cu K1, K6);
+  * bitwise equality with the reference's own CPU GEMM, compiled in place into
+    oracle/_ref (when present) and through the committed golden vectors it wrote;
+  * numpy float64 matmul, brute force on small integer matrices (exact in fp32);
+  * the adjoint identity for NT/TN and the checksum identity;
+  * numpy's binary16 conversion (round to nearest even) for the cast.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+
+
+def test_kat_2x2():
+    # tests/test_math_unit.cpp:292-301
+    C = o.vedic_gemm(np.array([[1, 2], [3, 4]]), np.array([[5, 6], [7, 8]]))
+    assert C.tolist() == [[19, 22], [43, 50]]
+
+
+def test_kat_identity_bias():
+    # tests/test_math_unit.cpp:304-319: I.I + [3, 5]
+    I = np.eye(2, dtype=np.float32)
+    assert o.vedic_gemm_bias(I, I, [3, 5]).tolist() == [[4, 5], [3, 6]]
+
+
+def test_kat_m17():
+    # tests/test_math_unit.cpp:1848-1978
+    A = np.arange(1, 10, dtype=np.float32).reshape(3, 3)
+    B = np.arange(9, 0, -1, dtype=np.float32).reshape(3, 3)
+    C = o.vedic_gemm(A, B)
+    assert C[0, 0] == 30 and C[2, 2] == 90
+    C = o.vedic_gemm([[1, 10, 100, 1000], [2, 20, 200, 2000]], [[1, 0], [0, 1], [1, 0], [0, 1]])
+    assert C[0].tolist() == [101, 1010]
+    C = o.vedic_gemm([[1, 2], [3, 4]], [[5, 6, 7], [8, 9, 10]])
+    assert C[0].tolist() == [21, 24, 27] and C[1, 2] == 3 * 7 + 4 * 10
+    A = np.arange(1, 17, dtype=np.float32).reshape(4, 4)
+    assert np.array_equal(o.vedic_gemm(A, np.eye(4)), A)
+    C = o.vedic_gemm([[1, 2], [3, 4], [5, 6]], [[7, 8, 9], [10, 11, 12]])
+    assert C.tolist() == [[27, 30, 33], [61, 68, 75], [95, 106, 117]]
+    C = o.vedic_gemm([[2, 3], [4, 5]], [[2, 0], [0, 2]])
+    assert C.tolist() == [[4, 6], [8, 10]]
+    R = o.vedic_gemm_bias(np.ones((3, 4)), np.ones((4, 5)), np.full(5, 0.5))
+    assert np.all(R == 4.5)
+    R = o.vedic_gemm_bias(np.zeros((3, 4)), np.eye(4), [1, 2, 3, 4])
+    assert np.all(R == np.array([1, 2, 3, 4], np.float32))
+
+
+def test_kat_m22_rows_cols_second_tile():
+    # tests/test_math_unit.cpp:2475-2608: A[i][k] = (i+1)*10 + (k+1) times I,
+    # row/column selectors, and M = 70 (a second 64-row tile).
+    M, K = 70, 3
+    A = np.array([[(i + 1) * 10 + (k + 1) for k in range(K)] for i in range(M)], np.float32)
+    assert np.array_equal(o.vedic_gemm(A, np.eye(K)), A)
+    sel = np.zeros((K, 1), np.float32)
+    sel[1, 0] = 1
+    assert np.array_equal(o.vedic_gemm(A, sel)[:, 0], A[:, 1])
+    with pytest.raises(ValueError):
+        o.vedic_gemm(np.ones((2, 3)), np.ones((4, 2)))
+
+
+def test_kat_s6_constant_and_irregular():
+    # tests/test_syntax_build.cu:196-260: A=1, B=2, K=8 -> 16; 3x5x7 irregular with bias.
+    assert np.all(o.vedic_gemm(np.ones((4, 8)), np.full((8, 4), 2.0)) == 16.0)
+    M, K, N = 3, 5, 7
+    A = np.array([(i % 5) - 2 for i in range(M * K)], np.float32).reshape(M, K)
+    B = np.array([(i % 7) - 3 for i in range(K * N)], np.float32).reshape(K, N)
+    b = 0.25 * np.arange(N, dtype=np.float32)
+    C = o.vedic_gemm_bias(A, B, b)
+    assert np.array_equal(C, (A.astype(np.float64) @ B + b).astype(np.float32))
+
+
+def test_integer_bruteforce_exact():
+    rng = np.random.default_rng(1)
+    for M, K, N in [(1, 1, 1), (5, 9, 3), (64, 64, 64), (65, 130, 67)]:
+        A = rng.integers(-8, 9, (M, K)).astype(np.float32)
+        B = rng.integers(-8, 9, (K, N)).astype(np.float32)
+        want = np.zeros((M, N), np.int64)
+        for k in range(K):
+            want += np.outer(A[:, k].astype(np.int64), B[k].astype(np.int64))
+        assert np.array_equal(o.vedic_gemm(A, B, nthreads=3), want.astype(np.float32))
+
+
+def test_bitwise_equal_naive_order_and_threads():
+    rng = np.random.default_rng(2)
+    A = rng.standard_normal((130, 150), dtype=np.float32)
+    B = rng.standard_normal((150, 70), dtype=np.float32)
+    c1 = o.vedic_gemm(A, B, nthreads=1)
+    assert np.array_equal(c1, o.vedic_gemm(A, B, nthreads=5))
+    assert np.array_equal(c1, o.reference_gemm(A, B))
+
+
+@pytest.mark.skipif(not o.ref_available(), reason="oracle/_ref not built (needs /root/reference)")
+def test_bitwise_equal_reference_build():
+    rng = np.random.default_rng(3)
+    for M, K, N in [(3, 5, 7), (64, 64, 64), (100, 200, 150), (129, 65, 31)]:
+        A = rng.standard_normal((M, K), dtype=np.float32)
+        B = rng.standard_normal((K, N), dtype=np.float32)
+        b = rng.standard_normal(N, dtype=np.float32)
+        assert np.array_equal(o.vedic_gemm(A, B), o.ref_vedic_gemm(A, B))
+        assert np.array_equal(o.vedic_gemm_bias(A, B, b), o.ref_vedic_gemm_bias(A, B, b))
+        W = rng.standard_normal((N, K), dtype=np.float32)
+        assert np.array_equal(o.gemm_nt(A, W), o.ref_gemm_nt(A, W))
+        X = rng.standard_normal((K, M), dtype=np.float32)
+        dY = rng.standard_normal((K, N), dtype=np.float32)
+        pre = rng.standard_normal((M, N), dtype=np.float32)
+        assert np.array_equal(o.gemm_tn(X, dY, pre), o.ref_gemm_tn(X, dY, pre))
+    x = rng.standard_normal(5000, dtype=np.float32) * 4
+    assert np.array_equal(o.gelu(x), o.ref_gelu(x))
+
+
+def test_golden_vectors(golden):
+    g = golden
+    for key in [k for k in g if k.startswith("nn_") and k.endswith("_C")]:
+        base = key[:-2]
+        assert np.array_equal(o.vedic_gemm(g[base + "_A"], g[base + "_B"]), g[key]), base
+    assert np.array_equal(o.vedic_gemm_bias(g["bias_A"], g["bias_W"], g["bias_b"]), g["bias_C"])
+    assert np.array_equal(o.gelu(g["bias_C"]), g["gelu_H"])
+    assert np.array_equal(o.gelu(g["gelu_x"]), g["gelu_y"])
+    assert np.array_equal(o.gemm_nt(g["nt_dY"], g["nt_W"]), g["nt_dX"])
+    assert np.array_equal(o.gemm_tn(g["tn_X"], g["tn_dY"]), g["tn_dW"])
+    assert np.array_equal(o.gemm_tn(g["tn_X"], g["tn_dY"], g["tn_pre"]), g["tn_dW_acc"])
+
+
+def test_against_numpy_f64_all_layouts():
+    rng = np.random.default_rng(4)
+    M, N, K = 37, 45, 53
+    A = rng.standard_normal((M, K), dtype=np.float32)
+    B = rng.standard_normal((K, N), dtype=np.float32)
+    b = rng.standard_normal(N, dtype=np.float32)
+    ref = A.astype(np.float64) @ B.astype(np.float64)
+    tol = o.fp32_tolerance(K)
+    assert o.inf_rel_err(o.vedic_gemm(A, B), ref) < tol
+    out, absdot = o.gemm_f64(o.NN, A, B)
+    assert np.allclose(out, ref, rtol=1e-12, atol=1e-12)
+    assert np.allclose(absdot, np.abs(A.astype(np.float64)) @ np.abs(B.astype(np.float64)))
+    out, _ = o.gemm_f64(o.NT, A, np.ascontiguousarray(B.T))
+    assert np.allclose(out, ref, rtol=1e-12, atol=1e-12)
+    out, _ = o.gemm_f64(o.TN, np.ascontiguousarray(A.T), B)
+    assert np.allclose(out, ref, rtol=1e-12, atol=1e-12)
+    out, _ = o.gemm_f64(o.NN, A, B, bias=b)
+    assert np.allclose(out, ref + b, rtol=1e-12, atol=1e-12)
+    out, _ = o.gemm_f64(o.NN, A, B, bias=b, gelu=True)
+    h = ref + b
+    want = 0.5 * h * (1 + np.tanh(np.sqrt(2 / np.pi) * (h + 0.044715 * h ** 3)))
+    assert np.allclose(out, want, rtol=1e-9, atol=1e-12)
+
+
+def test_nt_tn_adjoint_identity():
+    # <dY, X W> = <dY W^T, X> = <X^T dY, W>, evaluated with the fp32 restatement.
+    rng = np.random.default_rng(5)
+    S, Din, Dout = 96, 40, 56
+    X = rng.standard_normal((S, Din), dtype=np.float32)
+    W = rng.standard_normal((Din, Dout), dtype=np.float32)
+    dY = rng.standard_normal((S, Dout), dtype=np.float32)
+    Y = o.vedic_gemm(X, W).astype(np.float64)
+    dX = o.gemm_nt(dY, np.ascontiguousarray(W)).astype(np.float64)  # W stored [Din x Dout] = [N x K]
+    dW = o.gemm_tn(X, dY).astype(np.float64)
+    lhs = np.sum(dY * Y)
+    assert abs(lhs - np.sum(dX * X)) <= 1e-4 * np.sum(np.abs(dY) @ np.abs(W.T) * np.abs(X))
+    assert abs(lhs - np.sum(dW * W)) <= 1e-4 * np.sum(np.abs(X.T) @ np.abs(dY) * np.abs(W))
+    # the definitions via an explicit transpose
+    assert np.array_equal(dX, o.vedic_gemm(dY, np.ascontiguousarray(W.T)))
+    assert np.array_equal(dW, o.vedic_gemm(np.ascontiguousarray(X.T), dY))
+    # accumulate: pre + X^T dY element by element
+    pre = rng.standard_normal((Din, Dout), dtype=np.float32)
+    assert np.array_equal(o.gemm_tn(X, dY, pre), pre + o.gemm_tn(X, dY))
+
+
+def test_f16_rounding_matches_numpy_and_k6():
+    rng = np.random.default_rng(6)
+    x = np.concatenate([
+        (rng.standard_normal(200000) * 3000).astype(np.float32),
+        (rng.standard_normal(20000) * 1e-5).astype(np.float32),
+        np.array([65504, 65519, 65520, 7e4, -7e4, 1e6, -1e6, np.inf, -np.inf,
+                  6e-8, 3e-8, 2.98e-8, -0.0, 0.0, 1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11], np.float32),
+    ])
+    clamped = np.clip(x, -65504, 65504)
+    assert np.array_equal(o.f32_to_f16_bits(x), clamped.astype(np.float16).view(np.uint16))
+    # K6 (tests/test_cuda_kernels.cu:380-425): +-1e6 clamps to +-65504; (i-128)*0.5 round-trips.
+    assert o.f16_round([1e6, -1e6]).tolist() == [65504.0, -65504.0]
+    v = (np.arange(256, dtype=np.float32) - 128) * 0.5
+    assert np.array_equal(o.f16_round(v), v)
+    # fminf/fmaxf clamp: NaN maps to +65504, as the reference kernel's clamp does.
+    assert o.f16_round([np.nan]).tolist() == [65504.0]
+
+
+def test_gelu_special_values():
+    x = np.array([0.0, 10.0, -10.0, 1.0, -1.0], np.float32)
+    y = o.gelu(x)
+    assert y[0] == 0.0 and y[1] == 10.0 and abs(y[2]) < 1e-20
+    g = lambda t: 0.5 * t * (1 + np.tanh(0.7978845608 * (t + 0.044715 * t ** 3)))
+    assert np.allclose(y[3:], g(x[3:].astype(np.float64)), rtol=1e-6)
+
+
+def test_checksum_identity():
+    rng = np.random.default_rng(7)
+    A = rng.standard_normal((50, 30), dtype=np.float32)
+    B = rng.standard_normal((30, 40), dtype=np.float32)
+    s, p = o.checksum(A, B, o.vedic_gemm(A, B))
+    assert abs(s - p) <= 1e-5 * np.sum(np.abs(A).sum(0) * np.abs(B).sum(1))
+    # a dropped column of C breaks it
+    C = o.vedic_gemm(A, B)
+    C[:, 3] = 0
+    s2, _ = o.checksum(A, B, C)
+    assert abs(s2 - p) > 1e-3
+
+
+def test_rejects_bad_dims():
+    with pytest.raises(ValueError):
+        o.vedic_gemm(np.ones((2, 3)), np.ones((2, 3)))
+    with pytest.raises(ValueError):
+        o.vedic_gemm_bias(np.ones((2, 3)), np.ones((3, 4)), np.ones(3))
