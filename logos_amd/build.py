@@ -21,7 +21,13 @@ PKG = os.path.join(ROOT, "logos_amd")
 CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "liblogos_vedic.so")
-SOURCES = ["vedic_gemm_mfma.hip", "vedic_capi.hip"]
+SOURCES = [
+    "vedic_gemm_f16_nn.hip",
+    "vedic_gemm_f16_nt.hip",
+    "vedic_gemm_f16_tn.hip",
+    "vedic_gemm_mfma.hip",
+    "vedic_capi.hip",
+]
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [
@@ -54,7 +60,7 @@ def _run(cmd: list[str], cwd: str | None = None) -> None:
         sys.stderr.write(out + "\n")
 
 
-def build_library(jobs: int = 4) -> str:
+def build_library(jobs: int = 6) -> str:
     os.makedirs(OBJ, exist_ok=True)
     cc = hipcc()
     objs = []
@@ -81,7 +87,7 @@ def build_oracle(with_reference: bool = True) -> None:
 
 def main() -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--jobs", type=int, default=4)
+    ap.add_argument("--jobs", type=int, default=6)
     ap.add_argument("--no-oracle", action="store_true")
     args = ap.parse_args()
     print(build_library(args.jobs))

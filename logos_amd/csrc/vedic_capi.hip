@@ -7,10 +7,14 @@
 
 #include "../../include/logos_vedic.h"
 #include "vedic_common.hpp"
+#include "vedic_epilogue.hpp"
 
 namespace vedic {
-hipError_t launch_gemm_f16(int op, bool vec, const GemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_f16_generic(int op, const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f32(int op, bool vec, const GemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_f16_direct_nn(const GemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_f16_direct_nt(const GemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_f16_direct_tn(const GemmArgs& a, hipStream_t s);
 }  // namespace vedic
 
 using namespace vedic;
@@ -24,6 +28,9 @@ static int hip_status(hipError_t e) {
 }
 
 static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Largest leading dimension (elements) the kernels' 32-bit tile offsets allow.
+static constexpr int64_t kMaxLd = int64_t(1) << 22;
 
 // ------------------------------------------------------------------ GEMM
 
@@ -77,9 +84,25 @@ extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
     const bool vec = aligned16(d->A) && aligned16(d->B) && d->lda % ve == 0 && d->ldb % ve == 0 &&
                      a_row % ve == 0 && b_row % ve == 0;
 
+    a.epi_kind = epi_kind_of(a.epi, a.alpha, a.beta);
+
+    // Tiles are addressed with 32-bit buffer offsets from the tile's first
+    // row: a few hundred rows of any operand or output must stay below 2 GiB.
+    if (d->ldc >= kMaxLd || (d->preact && d->ld_preact >= kMaxLd)) return VEDIC_STATUS_TOO_LARGE;
+
     hipStream_t s = static_cast<hipStream_t>(d->stream);
-    hipError_t e = d->in_dtype == VEDIC_DT_F16 ? launch_gemm_f16(d->op, vec, a, s)
-                                               : launch_gemm_f32(d->op, vec, a, s);
+    hipError_t e;
+    if (d->in_dtype == VEDIC_DT_F16) {
+        if (vec && d->lda < kMaxLd && d->ldb < kMaxLd) {
+            e = d->op == VEDIC_OP_NN   ? launch_gemm_f16_direct_nn(a, s)
+                : d->op == VEDIC_OP_NT ? launch_gemm_f16_direct_nt(a, s)
+                                       : launch_gemm_f16_direct_tn(a, s);
+        } else {
+            e = launch_gemm_f16_generic(d->op, a, s);
+        }
+    } else {
+        e = launch_gemm_f32(d->op, vec, a, s);
+    }
     return hip_status(e);
 }
 

@@ -64,6 +64,7 @@ struct GemmArgs {
     int M, N, K;
     float alpha, beta;
     int epi;
+    int epi_kind;  // EpiKind (vedic_epilogue.hpp), derived from epi/alpha/beta
     int tiles_m, tiles_n;
     int group_m;
 };

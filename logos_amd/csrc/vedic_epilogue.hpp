@@ -1,0 +1,137 @@
+// vedic_epilogue.hpp -- the fused GEMM epilogue shared by the MFMA kernels.
+//
+// 32x32 MFMA accumulator layout: lane l holds column l%32 of its 32x32 block
+// and, in element 4*g + r, row 8*g + 4*(l/32) + r.
+//
+// The epilogue kind is a template parameter of the kernel (chosen on the host
+// from the flags), so each kind compiles to a straight-line sequence.  C, the
+// pre-activation and the old C (beta != 0) go through buffer instructions
+// whose resource base is the wave tile's first row: the per-lane offset is
+// fixed, the row offset of each (block, group, row) step is wave-uniform and
+// rides in the SGPR offset, so a store costs no address arithmetic.  On edge
+// tiles out-of-range elements get the offset 0x80000000, past the resource's
+// record bound: their stores are dropped and their loads read zero.
+#pragma once
+
+#include "vedic_common.hpp"
+
+namespace vedic {
+
+enum EpiKind : int {
+    EK_PLAIN = 0,          // C = acc
+    EK_BIAS = 1,           // C = acc + b
+    EK_BIAS_GELU = 2,      // C = gelu(acc + b)
+    EK_BIAS_GELU_PRE = 3,  // P = acc + b; C = gelu(P)
+    EK_ACCUM = 4,          // C = C + acc           (beta = 1, the dW accumulation)
+    EK_GENERIC = 5,        // any flag combination (runtime flags)
+};
+
+__host__ __device__ inline int epi_kind_of(int epi, float alpha, float beta) {
+    if (epi == 0) return EK_PLAIN;
+    if (epi == EPI_BIAS) return EK_BIAS;
+    if (epi == (EPI_BIAS | EPI_GELU)) return EK_BIAS_GELU;
+    if (epi == (EPI_BIAS | EPI_GELU | EPI_PREACT)) return EK_BIAS_GELU_PRE;
+    if (epi == EPI_BETA && beta == 1.0f && alpha == 1.0f) return EK_ACCUM;
+    return EK_GENERIC;
+}
+
+constexpr uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p) {
+    // raw buffer: stride 0, num_records 2^31 - 1, dword3 for the gfx9 data format 32
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, 0x7FFFFFFF, 0x00020000);
+}
+
+__device__ __forceinline__ void st_f32(float v, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rs, (int)voff, (int)soff, 0);
+}
+
+__device__ __forceinline__ float ld_f32(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)voff, (int)soff, 0));
+}
+
+__device__ __forceinline__ void st_f16(float v, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+    _Float16 h = (_Float16)v;
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, h), rs, (int)voff, (int)soff, 0);
+}
+
+__device__ __forceinline__ float ld_f16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+    uint16_t b = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)voff, (int)soff, 0);
+    return (float)__builtin_bit_cast(_Float16, b);
+}
+
+// Writes a (32*MI) x (32*NI) wave tile whose top-left output is (row0, col0).
+// CHECK: the tile may extend past M or N.  Offsets are 32-bit: the caller
+// guarantees (32*MI) * ld * 4 < 2^31 for ldc and ldp.
+template <int KIND, bool CHECK, int MI, int NI>
+__device__ __forceinline__ void epilogue(const GemmArgs& a, const float16_t (&acc)[MI][NI], int row0, int col0,
+                                         int lane) {
+    const int l32 = lane & 31, h = lane >> 5;
+    const bool f16out = (KIND == EK_GENERIC) && (a.epi & EPI_F16OUT);
+    const int es = f16out ? 2 : 4;
+    const char* cbase = static_cast<const char*>(a.C) + ((int64_t)row0 * a.ldc) * es;
+    const __amdgpu_buffer_rsrc_t rc = buffer_rsrc(cbase);
+    __amdgpu_buffer_rsrc_t rp = rc;
+    const bool pre = (KIND == EK_BIAS_GELU_PRE) || (KIND == EK_GENERIC && (a.epi & EPI_PREACT));
+    if (pre) rp = buffer_rsrc(a.preact + (int64_t)row0 * a.ldp);
+    const uint32_t ldc_b = (uint32_t)(a.ldc * es);
+    const uint32_t ldp_b = (uint32_t)(a.ldp * 4);
+    const bool want_bias = (KIND == EK_BIAS || KIND == EK_BIAS_GELU || KIND == EK_BIAS_GELU_PRE) ||
+                           (KIND == EK_GENERIC && (a.epi & EPI_BIAS));
+    const int row_lim = a.M - row0 - 4 * h;  // rows 4h + u of the tile exist iff u < row_lim
+
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+        const int col = col0 + 32 * j + l32;
+        const bool col_ok = !CHECK || col < a.N;
+        float bj = 0.0f;
+        if (want_bias && col_ok) bj = a.bias[col];
+        const uint32_t vc = (uint32_t)(4 * h) * ldc_b + (uint32_t)(col * es);
+        const uint32_t vp = (uint32_t)(4 * h) * ldp_b + (uint32_t)(col * 4);
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int u = 32 * i + 8 * g + r;  // wave-uniform row step
+                    const uint32_t sc = (uint32_t)u * ldc_b;
+                    const uint32_t sp = (uint32_t)u * ldp_b;
+                    uint32_t oc = vc, op = vp;
+                    if (CHECK) {
+                        const bool ok = col_ok && (u < row_lim);
+                        oc = ok ? vc : kOob;
+                        op = ok ? vp : kOob;
+                    }
+                    float v = acc[i][j][4 * g + r];
+                    if constexpr (KIND == EK_PLAIN) {
+                        st_f32(v, rc, oc, sc);
+                    } else if constexpr (KIND == EK_BIAS) {
+                        st_f32(v + bj, rc, oc, sc);
+                    } else if constexpr (KIND == EK_BIAS_GELU) {
+                        st_f32(gelu_tanh(v + bj), rc, oc, sc);
+                    } else if constexpr (KIND == EK_BIAS_GELU_PRE) {
+                        v += bj;
+                        st_f32(v, rp, op, sp);
+                        st_f32(gelu_tanh(v), rc, oc, sc);
+                    } else if constexpr (KIND == EK_ACCUM) {
+                        st_f32(ld_f32(rc, oc, sc) + v, rc, oc, sc);
+                    } else {
+                        const int epi = a.epi;
+                        if (epi & EPI_ALPHA) v *= a.alpha;
+                        if (epi & EPI_BETA) v += a.beta * (f16out ? ld_f16(rc, oc, sc) : ld_f32(rc, oc, sc));
+                        v += bj;
+                        if (epi & EPI_PREACT) st_f32(v, rp, op, sp);
+                        if (epi & EPI_GELU) v = gelu_tanh(v);
+                        if (f16out)
+                            st_f16(v, rc, oc, sc);
+                        else
+                            st_f32(v, rc, oc, sc);
+                    }
+                }
+            }
+        }
+    }
+}
+
+}  // namespace vedic

@@ -31,6 +31,7 @@
 // masked stores).  A VEC=false instantiation loads element by element and
 // accepts any leading dimension and alignment.
 #include "vedic_common.hpp"
+#include "vedic_epilogue.hpp"
 
 namespace vedic {
 
@@ -244,8 +245,8 @@ struct Mfma<float> {
     }
 };
 
-// OP: 0 NN, 1 NT, 2 TN.
-template <typename T, int OP, int BM, int BN, int WM, int WN, bool VEC>
+// OP: 0 NN, 1 NT, 2 TN; KIND: the epilogue (vedic_epilogue.hpp).
+template <typename T, int OP, int BM, int BN, int WM, int WN, bool VEC, int KIND>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
 gemm_mfma_kernel(GemmArgs args) {
     constexpr int WAVES_N = BN / WN;
@@ -303,94 +304,61 @@ gemm_mfma_kernel(GemmArgs args) {
         __syncthreads();
     }
 
-    // Epilogue.  32x32 accumulator layout: lane l holds column l%32 and rows
-    // 8*g + 4*(l/32) + r of its block in element 4*g + r.
-    const int epi = args.epi;
-    const int l32 = lane & 31, h = lane >> 5;
-#pragma unroll
-    for (int j = 0; j < NI; ++j) {
-        const int col = n0 + wn * WN + 32 * j + l32;
-        const bool col_ok = col < args.N;
-        const float bj = ((epi & EPI_BIAS) && col_ok) ? args.bias[col] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < MI; ++i) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int row = m0 + wm * WM + 32 * i + 8 * g + 4 * h + r;
-                    if (!col_ok || row >= args.M) continue;
-                    float v = acc[i][j][4 * g + r];
-                    if (epi & EPI_ALPHA) v *= args.alpha;
-                    const int64_t off = (int64_t)row * args.ldc + col;
-                    if (epi & EPI_BETA) {
-                        float old = (epi & EPI_F16OUT)
-                                        ? (float)static_cast<const _Float16*>(args.C)[off]
-                                        : static_cast<const float*>(args.C)[off];
-                        v += args.beta * old;
-                    }
-                    v += bj;
-                    if (epi & EPI_PREACT) args.preact[(int64_t)row * args.ldp + col] = v;
-                    if (epi & EPI_GELU) v = gelu_tanh(v);
-                    if (epi & EPI_F16OUT)
-                        static_cast<_Float16*>(args.C)[off] = (_Float16)v;
-                    else
-                        static_cast<float*>(args.C)[off] = v;
-                }
-            }
-        }
-    }
+    const int row0 = m0 + wm * WM, col0 = n0 + wn * WN;
+    const bool full = (row0 + WM <= args.M) && (col0 + WN <= args.N);
+    if (KIND != EK_GENERIC && full)
+        epilogue<KIND, false, MI, NI>(args, acc, row0, col0, lane);
+    else
+        epilogue<KIND, true, MI, NI>(args, acc, row0, col0, lane);
 }
 
 // ------------------------------------------------------------------ launch
 
-struct TileCfg {
-    int BM, BN;
-};
-
-template <typename T, int OP, int BM, int BN, int WM, int WN, bool VEC>
+template <typename T, int OP, bool VEC, int KIND>
 static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
+    constexpr int BM = 128, BN = 128, WM = 64, WN = 64;
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
     if (a.group_m <= 0) a.group_m = 8;
     const int nblk = a.tiles_m * a.tiles_n;
     constexpr int NT = (BM / WM) * (BN / WN) * 64;
-    hipLaunchKernelGGL((gemm_mfma_kernel<T, OP, BM, BN, WM, WN, VEC>), dim3(nblk), dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((gemm_mfma_kernel<T, OP, BM, BN, WM, WN, VEC, KIND>), dim3(nblk), dim3(NT), 0, s, a);
     return hipGetLastError();
 }
 
-template <typename T, int OP, bool VEC>
-static hipError_t launch_op(GemmArgs a, hipStream_t s) {
-    if constexpr (sizeof(T) == 2) {
-        // fp16: 256x256 tiles (4 waves of 128x128) when they fill the chip,
-        // else 128x128 tiles (4 waves of 64x64).
-        const int64_t big = (int64_t)((a.M + 255) / 256) * ((a.N + 255) / 256);
-        if (big >= 256) return launch_cfg<T, OP, 256, 256, 128, 128, VEC>(a, s);
-        return launch_cfg<T, OP, 128, 128, 64, 64, VEC>(a, s);
-    } else {
-        return launch_cfg<T, OP, 128, 128, 64, 64, VEC>(a, s);
+// Vector loads: every epilogue kind.  Element-wise loads (odd shapes and
+// alignments): the generic epilogue only.
+template <typename T, int OP>
+static hipError_t launch_op(bool vec, const GemmArgs& a, hipStream_t s) {
+    if (!vec) return launch_cfg<T, OP, false, EK_GENERIC>(a, s);
+    switch (a.epi_kind) {
+        case EK_PLAIN: return launch_cfg<T, OP, true, EK_PLAIN>(a, s);
+        case EK_BIAS: return launch_cfg<T, OP, true, EK_BIAS>(a, s);
+        case EK_BIAS_GELU: return launch_cfg<T, OP, true, EK_BIAS_GELU>(a, s);
+        case EK_BIAS_GELU_PRE: return launch_cfg<T, OP, true, EK_BIAS_GELU_PRE>(a, s);
+        case EK_ACCUM: return launch_cfg<T, OP, true, EK_ACCUM>(a, s);
+        default: return launch_cfg<T, OP, true, EK_GENERIC>(a, s);
     }
 }
 
-template <typename T>
-static hipError_t launch_dtype(int op, bool vec, const GemmArgs& a, hipStream_t s) {
-    switch (op * 2 + (vec ? 1 : 0)) {
-        case 0: return launch_op<T, 0, false>(a, s);
-        case 1: return launch_op<T, 0, true>(a, s);
-        case 2: return launch_op<T, 1, false>(a, s);
-        case 3: return launch_op<T, 1, true>(a, s);
-        case 4: return launch_op<T, 2, false>(a, s);
-        case 5: return launch_op<T, 2, true>(a, s);
+hipError_t launch_gemm_f32(int op, bool vec, const GemmArgs& a, hipStream_t s) {
+    switch (op) {
+        case 0: return launch_op<float, 0>(vec, a, s);
+        case 1: return launch_op<float, 1>(vec, a, s);
+        case 2: return launch_op<float, 2>(vec, a, s);
     }
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemm_f16(int op, bool vec, const GemmArgs& a, hipStream_t s) {
-    return launch_dtype<_Float16>(op, vec, a, s);
-}
-
-hipError_t launch_gemm_f32(int op, bool vec, const GemmArgs& a, hipStream_t s) {
-    return launch_dtype<float>(op, vec, a, s);
+// fp16 operands that the direct-load kernel cannot take (odd extents,
+// unaligned bases or leading dimensions): element-wise loads, generic epilogue.
+hipError_t launch_gemm_f16_generic(int op, const GemmArgs& a, hipStream_t s) {
+    switch (op) {
+        case 0: return launch_cfg<_Float16, 0, false, EK_GENERIC>(a, s);
+        case 1: return launch_cfg<_Float16, 1, false, EK_GENERIC>(a, s);
+        case 2: return launch_cfg<_Float16, 2, false, EK_GENERIC>(a, s);
+    }
+    return hipErrorInvalidValue;
 }
 
 }  // namespace vedic
