@@ -1,0 +1,315 @@
+// VedicGEMM_hip.hpp -- C++ drop-in for the GPU Vedic GEMM surface of LOGOS,
+// over the C ABI of liblogos_vedic.so (logos_vedic.h).  Link with
+// -llogos_vedic -lamdhip64.
+//
+// It keeps the reference's names, argument order and error conventions so a
+// caller of cuda/VedicGEMM.cuh and cuda/MixedPrecision.cuh switches by
+// changing the include:
+//   GPUTensor, gpu_alloc, gpu_free, h2d, d2h      cuda/VedicGEMM.cuh:136-180
+//   cuda_vedic_gemm, cuda_vedic_gemm_bias,
+//   cuda_vedic_gemm_uses_cublas, cuda_gelu       cuda/VedicGEMM.cuh:182-187
+//   cuda_add_bias (the add_bias_kernel launch)   cuda/VedicGEMM.cuh:191
+//   cuda_vedic_verify, VedicVerifyResult          cuda/VedicGEMM.cuh:162-167,193
+//   cuda_gemm_fp16_fp32out / _fp16out             cuda/VedicGEMM.cuh:251-252
+//   HalfTensor, half_alloc,
+//   cuda_cast_fp32_to_fp16 / _fp16_to_fp32        cuda/MixedPrecision.cuh:100-132,177-196
+// and adds the entry points the reference's backward lacks (it runs naive
+// kernels, cuda/train_gpu.cu:210-545): cuda_vedic_gemm_nt / _tn and their
+// fp16 forms, and the fused FFN epilogue cuda_vedic_gemm_bias_gelu /
+// cuda_gemm_fp16_bias_gelu (replacing GEMM + add_bias_kernel + D2D copy +
+// cuda_gelu, cuda/ModelGPU.cu:1023-1028).
+//
+// Errors: shape mismatches throw std::invalid_argument (the reference's CPU
+// convention, include/VedicGEMM.hpp:27-30; its GPU wrappers do not check
+// shapes at all), HIP failures throw std::runtime_error (CUDA_CHECK,
+// cuda/VedicGEMM.cuh:111-133).  Every call runs on `stream` (default: the
+// null stream, as the reference's launches do) and is asynchronous, except
+// cuda_vedic_verify and the copies, which synchronise as the reference's do.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <stdexcept>
+#include <string>
+
+#include "logos_vedic.h"
+
+#define HIP_CHECK(call)                                                                         \
+    do {                                                                                        \
+        hipError_t _e = (call);                                                                 \
+        if (_e != hipSuccess) {                                                                 \
+            char _msg[256];                                                                     \
+            snprintf(_msg, sizeof(_msg), "HIP error at %s:%d: %s", __FILE__, __LINE__,         \
+                     hipGetErrorString(_e));                                                    \
+            throw std::runtime_error(_msg);                                                     \
+        }                                                                                       \
+    } while (0)
+
+namespace vedic_hip {
+
+// Maps a vedic_status_t to the reference's exception types.
+inline void check(int status, const char* what) {
+    if (status == VEDIC_STATUS_OK) return;
+    std::string msg = std::string(what) + ": " + vedic_status_string(status);
+    if (status == VEDIC_STATUS_HIP_ERROR) {
+        msg += " (";
+        msg += hipGetErrorString(static_cast<hipError_t>(vedic_last_hip_error()));
+        msg += ")";
+        throw std::runtime_error(msg);
+    }
+    throw std::invalid_argument(msg);
+}
+
+inline void require(bool ok, const char* what) {
+    if (!ok) throw std::invalid_argument(std::string("VedicGEMM: ") + what);
+}
+
+}  // namespace vedic_hip
+
+// Row-major fp32 matrix in device memory; owns it (move-only).
+struct GPUTensor {
+    float* data = nullptr;
+    int rows = 0, cols = 0, size = 0;
+
+    GPUTensor() = default;
+    GPUTensor(const GPUTensor&) = delete;
+    GPUTensor& operator=(const GPUTensor&) = delete;
+    GPUTensor(GPUTensor&& o) noexcept : data(o.data), rows(o.rows), cols(o.cols), size(o.size) {
+        o.data = nullptr;
+        o.rows = o.cols = o.size = 0;
+    }
+    GPUTensor& operator=(GPUTensor&& o) noexcept {
+        if (this != &o) {
+            if (data) (void)hipFree(data);
+            data = o.data;
+            rows = o.rows;
+            cols = o.cols;
+            size = o.size;
+            o.data = nullptr;
+            o.rows = o.cols = o.size = 0;
+        }
+        return *this;
+    }
+    ~GPUTensor() {
+        if (data) (void)hipFree(data);
+    }
+    bool valid() const { return data != nullptr && size > 0; }
+};
+
+// Row-major binary16 matrix in device memory (the AMP shadow / activation copy).
+struct HalfTensor {
+    __half* data = nullptr;
+    int rows = 0, cols = 0, size = 0;
+
+    HalfTensor() = default;
+    HalfTensor(const HalfTensor&) = delete;
+    HalfTensor& operator=(const HalfTensor&) = delete;
+    HalfTensor(HalfTensor&& o) noexcept : data(o.data), rows(o.rows), cols(o.cols), size(o.size) {
+        o.data = nullptr;
+        o.rows = o.cols = o.size = 0;
+    }
+    HalfTensor& operator=(HalfTensor&& o) noexcept {
+        if (this != &o) {
+            if (data) (void)hipFree(data);
+            data = o.data;
+            rows = o.rows;
+            cols = o.cols;
+            size = o.size;
+            o.data = nullptr;
+            o.rows = o.cols = o.size = 0;
+        }
+        return *this;
+    }
+    ~HalfTensor() {
+        if (data) (void)hipFree(data);
+    }
+    bool valid() const { return data != nullptr && size > 0; }
+};
+
+struct VedicVerifyResult {
+    float checksum_C;
+    float checksum_vedic;
+    float relative_error;
+    bool pass;
+};
+
+// ------------------------------------------------------------ memory
+
+// Zero-filled rows x cols fp32 matrix (cudaMalloc + cudaMemset, cuda/VedicGEMM.cu:594-600).
+inline GPUTensor gpu_alloc(int rows, int cols) {
+    vedic_hip::require(rows >= 0 && cols >= 0, "gpu_alloc: negative size");
+    GPUTensor t;
+    t.rows = rows;
+    t.cols = cols;
+    t.size = rows * cols;
+    if (t.size > 0) {
+        HIP_CHECK(hipMalloc(&t.data, (size_t)t.size * sizeof(float)));
+        HIP_CHECK(hipMemset(t.data, 0, (size_t)t.size * sizeof(float)));
+    }
+    return t;
+}
+
+inline void gpu_free(GPUTensor& t) {
+    if (t.data) {
+        (void)hipFree(t.data);
+        t.data = nullptr;
+        t.size = 0;
+    }
+}
+
+inline void h2d(GPUTensor& dst, const float* src, int size) {
+    HIP_CHECK(hipMemcpy(dst.data, src, (size_t)size * sizeof(float), hipMemcpyHostToDevice));
+}
+
+inline void d2h(float* dst, const GPUTensor& src, int size) {
+    HIP_CHECK(hipMemcpy(dst, src.data, (size_t)size * sizeof(float), hipMemcpyDeviceToHost));
+}
+
+// Zero-filled rows x cols binary16 matrix (cuda/MixedPrecision.cuh:125-132).
+inline HalfTensor half_alloc(int rows, int cols) {
+    vedic_hip::require(rows >= 0 && cols >= 0, "half_alloc: negative size");
+    HalfTensor t;
+    t.rows = rows;
+    t.cols = cols;
+    t.size = rows * cols;
+    if (t.size > 0) {
+        HIP_CHECK(hipMalloc(&t.data, (size_t)t.size * sizeof(__half)));
+        HIP_CHECK(hipMemset(t.data, 0, (size_t)t.size * sizeof(__half)));
+    }
+    return t;
+}
+
+// -------------------------------------------------------- fp32 GEMMs
+
+// C = A . B (cuda/VedicGEMM.cu:645-673); M = A.rows, K = A.cols, N = B.cols.
+inline void cuda_vedic_gemm(const GPUTensor& A, const GPUTensor& B, GPUTensor& C,
+                            hipStream_t stream = nullptr) {
+    vedic_hip::require(B.rows == A.cols, "cuda_vedic_gemm: A.cols != B.rows");
+    vedic_hip::require(C.rows == A.rows && C.cols == B.cols, "cuda_vedic_gemm: C is not A.rows x B.cols");
+    vedic_hip::check(vedic_gemm_f32(A.data, B.data, C.data, A.rows, A.cols, B.cols, stream),
+                     "cuda_vedic_gemm");
+}
+
+// Always false: no vendor BLAS is linked (cuda/VedicGEMM.cu:637-643).
+inline bool cuda_vedic_gemm_uses_cublas() { return vedic_uses_vendor_blas() != 0; }
+
+// C = A . W + bias[j], bias added after the full dot (cuda/VedicGEMM.cu:675-690).
+inline void cuda_vedic_gemm_bias(const GPUTensor& A, const GPUTensor& W, const GPUTensor& bias,
+                                 GPUTensor& C, hipStream_t stream = nullptr) {
+    vedic_hip::require(W.rows == A.cols, "cuda_vedic_gemm_bias: A.cols != W.rows");
+    vedic_hip::require(bias.size == W.cols, "cuda_vedic_gemm_bias: bias size != W.cols");
+    vedic_hip::require(C.rows == A.rows && C.cols == W.cols, "cuda_vedic_gemm_bias: C shape");
+    vedic_hip::check(vedic_gemm_bias_f32(A.data, W.data, bias.data, C.data, A.rows, A.cols, W.cols, stream),
+                     "cuda_vedic_gemm_bias");
+}
+
+// H = gelu_tanh(A . W + bias); `preact` (nullable) receives A . W + bias.
+// New: the reference runs GEMM, add_bias_kernel, a D2D copy and cuda_gelu
+// (cuda/ModelGPU.cu:1023-1028).
+inline void cuda_vedic_gemm_bias_gelu(const GPUTensor& A, const GPUTensor& W, const GPUTensor& bias,
+                                      GPUTensor& H, GPUTensor* preact = nullptr,
+                                      hipStream_t stream = nullptr) {
+    vedic_hip::require(W.rows == A.cols, "cuda_vedic_gemm_bias_gelu: A.cols != W.rows");
+    vedic_hip::require(bias.size == W.cols, "cuda_vedic_gemm_bias_gelu: bias size != W.cols");
+    vedic_hip::require(H.rows == A.rows && H.cols == W.cols, "cuda_vedic_gemm_bias_gelu: H shape");
+    vedic_hip::require(!preact || (preact->rows == A.rows && preact->cols == W.cols),
+                       "cuda_vedic_gemm_bias_gelu: preact shape");
+    vedic_hip::check(vedic_gemm_bias_gelu_f32(A.data, W.data, bias.data, H.data,
+                                              preact ? preact->data : nullptr, A.rows, A.cols, W.cols,
+                                              stream),
+                     "cuda_vedic_gemm_bias_gelu");
+}
+
+// dX = dY . W^T + beta dX with W stored [in x out] = [N x K].
+// Replaces lmhead_grad_dx / ffn_da / ffn_dx / attn_dConcat / attn_dHeadOut
+// (beta = 0) and attn_dX_from_QKV (beta = 1), cuda/train_gpu.cu:221-230,
+// 323-332,358-367,536-545,514-523,492-501.
+inline void cuda_vedic_gemm_nt(const GPUTensor& dY, const GPUTensor& W, GPUTensor& dX, float beta = 0.0f,
+                               hipStream_t stream = nullptr) {
+    vedic_hip::require(W.cols == dY.cols, "cuda_vedic_gemm_nt: dY.cols != W.cols");
+    vedic_hip::require(dX.rows == dY.rows && dX.cols == W.rows, "cuda_vedic_gemm_nt: dX shape");
+    vedic_hip::check(vedic_gemm_nt_f32(dY.data, W.data, dX.data, dY.rows, W.rows, dY.cols, beta, stream),
+                     "cuda_vedic_gemm_nt");
+}
+
+// dW = X^T . dY + beta dW (beta = 1: the reference's atomicAdd accumulation
+// into zeroed grad buffers, cuda/train_gpu.cu:210-219,312-321,347-356,
+// 525-534,503-512,481-490 -- here deterministic).
+inline void cuda_vedic_gemm_tn(const GPUTensor& X, const GPUTensor& dY, GPUTensor& dW, float beta = 1.0f,
+                               hipStream_t stream = nullptr) {
+    vedic_hip::require(X.rows == dY.rows, "cuda_vedic_gemm_tn: X.rows != dY.rows");
+    vedic_hip::require(dW.rows == X.cols && dW.cols == dY.cols, "cuda_vedic_gemm_tn: dW shape");
+    vedic_hip::check(vedic_gemm_tn_f32(X.data, dY.data, dW.data, X.cols, dY.cols, X.rows, beta, stream),
+                     "cuda_vedic_gemm_tn");
+}
+
+// ---------------------------------------------- fp16-in / fp32-acc GEMMs
+
+// C = alpha A . B + beta C; A [M x K], B [K x N] binary16, C fp32
+// (cuda/VedicGEMM.cu:1150-1178).
+inline void cuda_gemm_fp16_fp32out(const __half* A, int M, int K, const __half* B, int N, float* C,
+                                   float alpha = 1.f, float beta = 0.f, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_gemm_f16_f32out(A, M, K, B, N, C, alpha, beta, stream), "cuda_gemm_fp16_fp32out");
+}
+
+// Same with a binary16 C, rounded once from the fp32 accumulator
+// (cuda/VedicGEMM.cu:1182-1197).
+inline void cuda_gemm_fp16_fp16out(const __half* A, int M, int K, const __half* B, int N, __half* C,
+                                   float alpha = 1.f, float beta = 0.f, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_gemm_f16_f16out(A, M, K, B, N, C, alpha, beta, stream), "cuda_gemm_fp16_fp16out");
+}
+
+// Fused FFN-up on the AMP path: H = gelu_tanh(X . W + bias), fp32 H and
+// (nullable) preact.  Replaces amp_gemm_bias + D2D copy + cuda_gelu
+// (cuda/ModelGPU.cu:819-859,1023-1028).
+inline void cuda_gemm_fp16_bias_gelu(const __half* X, int M, int K, const __half* W, int N, const float* bias,
+                                     float* H, float* preact = nullptr, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_gemm_bias_gelu_f16(X, W, bias, H, preact, M, K, N, stream), "cuda_gemm_fp16_bias_gelu");
+}
+
+// dX[M x N] = dY[M x K] . W^T + beta dX, W stored [N x K], binary16 inputs.
+inline void cuda_gemm_fp16_nt(const __half* dY, int M, int K, const __half* W, int N, float* dX,
+                              float beta = 0.f, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_gemm_nt_f16(dY, W, dX, M, N, K, beta, stream), "cuda_gemm_fp16_nt");
+}
+
+// dW[M x N] = X^T . dY + beta dW, X stored [K x M], dY [K x N], binary16 inputs.
+inline void cuda_gemm_fp16_tn(const __half* X, int K, int M, const __half* dY, int N, float* dW,
+                              float beta = 1.f, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_gemm_tn_f16(X, dY, dW, M, N, K, beta, stream), "cuda_gemm_fp16_tn");
+}
+
+// --------------------------------------------------- elementwise helpers
+
+// C[i][j] += bias[j] (the add_bias_kernel launch, cuda/VedicGEMM.cu:96-102).
+inline void cuda_add_bias(float* C, const float* bias, int M, int N, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_add_bias(C, bias, M, N, stream), "cuda_add_bias");
+}
+
+// In-place tanh-GELU (cuda/VedicGEMM.cu:707-711).
+inline void cuda_gelu(GPUTensor& data, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_gelu(data.data, data.size, stream), "cuda_gelu");
+}
+
+// binary16(clamp(src, +-65504)), round to nearest even (cuda/MixedPrecision.cuh:149-161,177-190).
+inline void cuda_cast_fp32_to_fp16(const float* src, __half* dst, int n, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_cast_f32_to_f16(src, dst, n, stream), "cuda_cast_fp32_to_fp16");
+}
+
+inline void cuda_cast_fp16_to_fp32(const __half* src, float* dst, int n, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_cast_f16_to_f32(src, dst, n, stream), "cuda_cast_fp16_to_fp32");
+}
+
+// Gunitasamuchayah check: sum(C) against colsum(A) . rowsum(B); synchronous
+// (cuda/VedicGEMM.cu:765-814).
+inline VedicVerifyResult cuda_vedic_verify(const GPUTensor& A, const GPUTensor& B, const GPUTensor& C,
+                                           float tolerance = 0.01f, hipStream_t stream = nullptr) {
+    vedic_hip::require(B.rows == A.cols && C.rows == A.rows && C.cols == B.cols,
+                       "cuda_vedic_verify: shapes");
+    vedic_verify_result_t r{};
+    vedic_hip::check(vedic_verify(A.data, B.data, C.data, A.rows, A.cols, B.cols, tolerance, &r, stream),
+                     "cuda_vedic_verify");
+    return VedicVerifyResult{r.checksum_C, r.checksum_vedic, r.relative_error, r.pass != 0};
+}

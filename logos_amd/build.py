@@ -78,6 +78,20 @@ def build_library(jobs: int = 6) -> str:
     return LIB
 
 
+CPP_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "vedic_hip_test.cpp")
+CPP_TEST_BIN = os.path.join(ROOT, "tests", "cpp", "vedic_hip_test")
+
+
+def build_cpp_test() -> str:
+    """Host-only C++ program over include/VedicGEMM_hip.hpp, linked against the
+    library with an rpath relative to itself (so it runs wherever the tree is)."""
+    tmp = CPP_TEST_BIN + ".tmp"
+    _run([hipcc(), "-O2", "-std=c++17", "-Wall", f"-I{os.path.join(ROOT, 'include')}", CPP_TEST_SRC,
+          f"-L{PKG}", "-llogos_vedic", "-Wl,-rpath,$ORIGIN/../../logos_amd", "-o", tmp])
+    os.replace(tmp, CPP_TEST_BIN)
+    return CPP_TEST_BIN
+
+
 def build_oracle(with_reference: bool = True) -> None:
     odir = os.path.join(ROOT, "oracle")
     _run(["make", "-s", "-B", "liblogos_oracle.so"], cwd=odir)
@@ -91,6 +105,7 @@ def main() -> None:
     ap.add_argument("--no-oracle", action="store_true")
     args = ap.parse_args()
     print(build_library(args.jobs))
+    print(build_cpp_test())
     if not args.no_oracle:
         build_oracle()
 

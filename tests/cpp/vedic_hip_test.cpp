@@ -1,0 +1,302 @@
+// vedic_hip_test.cpp -- exercises the C++ drop-in header VedicGEMM_hip.hpp on
+// the GPU the way a LOGOS caller would (GPUTensor / HalfTensor, the
+// reference's function names), against a host float64 computation.
+//
+// Known answers restate the reference's own tests:
+//   tests/test_math_unit.cpp:292-319 (2x2 product, I.I + bias),
+//   tests/test_syntax_build.cu:196-260 (S6: constant A=1, B=2, K=8 -> 16),
+//   tests/test_cuda_kernels.cu:123-168 (K1 add_bias), :380-425 (K6 cast clamp),
+//   include/VedicGEMM.hpp:27-30 (dimension mismatch throws).
+// Built by logos_amd/build.py; run by tests/test_cpp_mirror.py on a GPU box.
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <stdexcept>
+#include <vector>
+
+#include "VedicGEMM_hip.hpp"
+
+static int g_fail = 0;
+
+#define EXPECT(cond, ...)                      \
+    do {                                       \
+        if (!(cond)) {                         \
+            std::printf("FAIL %s:%d: ", __FILE__, __LINE__); \
+            std::printf(__VA_ARGS__);          \
+            std::printf("\n");                 \
+            ++g_fail;                          \
+        }                                      \
+    } while (0)
+
+// splitmix64 -> uniform [-1, 1)
+struct Rng {
+    uint64_t s;
+    explicit Rng(uint64_t seed) : s(seed) {}
+    double next() {
+        uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        z ^= z >> 31;
+        return (double)(z >> 11) * (2.0 / 9007199254740992.0) - 1.0;
+    }
+};
+
+static std::vector<float> rand_vec(Rng& r, size_t n, double scale = 1.0) {
+    std::vector<float> v(n);
+    for (auto& x : v) x = (float)(r.next() * scale);
+    return v;
+}
+
+static GPUTensor upload(const std::vector<float>& h, int rows, int cols) {
+    GPUTensor t = gpu_alloc(rows, cols);
+    h2d(t, h.data(), rows * cols);
+    return t;
+}
+
+static std::vector<float> download(const GPUTensor& t) {
+    std::vector<float> h((size_t)t.size);
+    d2h(h.data(), t, t.size);
+    return h;
+}
+
+// op(A)[i][k], op(B)[k][j] with op given by the storage of each operand.
+enum Layout { NN, NT, TN };
+
+static std::vector<double> ref_gemm(Layout L, const std::vector<float>& A, const std::vector<float>& B, int M,
+                                    int N, int K) {
+    std::vector<double> C((size_t)M * N, 0.0);
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            double s = 0.0;
+            for (int k = 0; k < K; ++k) {
+                double a = L == TN ? A[(size_t)k * M + i] : A[(size_t)i * K + k];
+                double b = L == NT ? B[(size_t)j * K + k] : B[(size_t)k * N + j];
+                s += a * b;
+            }
+            C[(size_t)i * N + j] = s;
+        }
+    return C;
+}
+
+static double inf_rel(const std::vector<float>& got, const std::vector<double>& want) {
+    double num = 0.0, den = 0.0;
+    for (size_t i = 0; i < want.size(); ++i) {
+        num = std::fmax(num, std::fabs((double)got[i] - want[i]));
+        den = std::fmax(den, std::fabs(want[i]));
+    }
+    return den > 0 ? num / den : num;
+}
+
+static double gelu64(double x) {
+    return 0.5 * x * (1.0 + std::tanh(0.7978845608028654 * (x + 0.044715 * x * x * x)));
+}
+
+static void test_known_answers() {
+    GPUTensor A = upload({1, 2, 3, 4}, 2, 2), B = upload({5, 6, 7, 8}, 2, 2), C = gpu_alloc(2, 2);
+    cuda_vedic_gemm(A, B, C);
+    auto c = download(C);
+    EXPECT(c[0] == 19 && c[1] == 22 && c[2] == 43 && c[3] == 50, "2x2 product");
+
+    GPUTensor I = upload({1, 0, 0, 1}, 2, 2), b = upload({3, 5}, 1, 2), D = gpu_alloc(2, 2);
+    cuda_vedic_gemm_bias(I, I, b, D);
+    auto d = download(D);
+    EXPECT(d[0] == 4 && d[1] == 5 && d[2] == 3 && d[3] == 6, "I.I + [3,5]");
+
+    GPUTensor ones = upload(std::vector<float>(32, 1.0f), 4, 8), twos = upload(std::vector<float>(32, 2.0f), 8, 4);
+    GPUTensor S = gpu_alloc(4, 4);
+    cuda_vedic_gemm(ones, twos, S);
+    for (float v : download(S)) EXPECT(v == 16.0f, "S6 constant product %g", v);
+
+    // K1: add_bias over 4 x 8
+    std::vector<float> h(32);
+    for (int i = 0; i < 32; ++i) h[i] = (float)i;
+    GPUTensor Cb = upload(h, 4, 8), bb = upload({1, 2, 3, 4, 5, 6, 7, 8}, 1, 8);
+    cuda_add_bias(Cb.data, bb.data, 4, 8);
+    auto cb = download(Cb);
+    for (int i = 0; i < 32; ++i) EXPECT(cb[i] == h[i] + (float)(i % 8 + 1), "add_bias %d", i);
+
+    EXPECT(!cuda_vedic_gemm_uses_cublas(), "no vendor BLAS");
+    EXPECT(std::string(vedic_backend_name()) == "hip-native-gfx950", "backend name");
+}
+
+static void test_fp32_layouts() {
+    Rng r(42);
+    const int M = 97, N = 131, K = 75;
+    const double tol = 1e-5 * std::sqrt((double)K);
+    auto a = rand_vec(r, (size_t)M * K), bm = rand_vec(r, (size_t)K * N), bias = rand_vec(r, N, 0.1);
+    GPUTensor A = upload(a, M, K), B = upload(bm, K, N), bi = upload(bias, 1, N), C = gpu_alloc(M, N);
+
+    cuda_vedic_gemm(A, B, C);
+    auto want = ref_gemm(NN, a, bm, M, N, K);
+    double e = inf_rel(download(C), want);
+    EXPECT(e <= tol, "fp32 NN err %.3e", e);
+
+    GPUTensor H = gpu_alloc(M, N), P = gpu_alloc(M, N);
+    cuda_vedic_gemm_bias_gelu(A, B, bi, H, &P);
+    std::vector<double> wp(want), wh(want);
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            wp[(size_t)i * N + j] = want[(size_t)i * N + j] + bias[j];
+            wh[(size_t)i * N + j] = gelu64(wp[(size_t)i * N + j]);
+        }
+    e = inf_rel(download(P), wp);
+    EXPECT(e <= tol, "fp32 preact err %.3e", e);
+    e = inf_rel(download(H), wh);
+    EXPECT(e <= tol, "fp32 bias+gelu err %.3e", e);
+
+    // NT: dX[M x N] = dY[M x K] . W^T, W [N x K]
+    auto w = rand_vec(r, (size_t)N * K);
+    GPUTensor W = upload(w, N, K), dX = gpu_alloc(M, N);
+    cuda_vedic_gemm_nt(A, W, dX);
+    e = inf_rel(download(dX), ref_gemm(NT, a, w, M, N, K));
+    EXPECT(e <= tol, "fp32 NT err %.3e", e);
+
+    // TN with beta = 1 onto a pre-filled buffer: dW[K' x N] += X^T . dY
+    // with X = A [M x K] (contraction over M rows), dY = C-shaped [M x N].
+    auto dy = rand_vec(r, (size_t)M * N), pre = rand_vec(r, (size_t)K * N);
+    GPUTensor dY = upload(dy, M, N), dW = upload(pre, K, N);
+    cuda_vedic_gemm_tn(A, dY, dW, 1.0f);
+    auto tn = ref_gemm(TN, a, dy, K, N, M);
+    for (size_t i = 0; i < tn.size(); ++i) tn[i] += pre[i];
+    e = inf_rel(download(dW), tn);
+    EXPECT(e <= 1e-5 * std::sqrt((double)M) * 2, "fp32 TN accumulate err %.3e", e);
+}
+
+static void test_fp16_path() {
+    // small integers: exact in binary16, products exact, sums < 2^24
+    const int M = 40, K = 72, N = 24;
+    Rng r(7);
+    std::vector<float> a((size_t)M * K), b((size_t)K * N);
+    for (auto& x : a) x = (float)std::floor(r.next() * 8.0);
+    for (auto& x : b) x = (float)std::floor(r.next() * 8.0);
+    GPUTensor A32 = upload(a, M, K), B32 = upload(b, K, N);
+    HalfTensor A16 = half_alloc(M, K), B16 = half_alloc(K, N);
+    cuda_cast_fp32_to_fp16(A32.data, A16.data, A16.size);
+    cuda_cast_fp32_to_fp16(B32.data, B16.data, B16.size);
+    GPUTensor C = gpu_alloc(M, N);
+    cuda_gemm_fp16_fp32out(A16.data, M, K, B16.data, N, C.data);
+    auto want = ref_gemm(NN, a, b, M, N, K);
+    auto got = download(C);
+    bool exact = true;
+    for (size_t i = 0; i < want.size(); ++i) exact = exact && (double)got[i] == want[i];
+    EXPECT(exact, "fp16 integer product not exact");
+
+    // alpha/beta: C = 0.5 A.B + 1.0 C
+    cuda_gemm_fp16_fp32out(A16.data, M, K, B16.data, N, C.data, 0.5f, 1.0f);
+    got = download(C);
+    exact = true;
+    for (size_t i = 0; i < want.size(); ++i) exact = exact && (double)got[i] == 1.5 * want[i];
+    EXPECT(exact, "fp16 alpha/beta accumulate not exact");
+
+    // K6: the cast clamps to +-65504 and (i - 128) * 0.5 round-trips
+    std::vector<float> c6 = {1e6f, -1e6f};
+    for (int i = 0; i < 256; ++i) c6.push_back((float)(i - 128) * 0.5f);
+    GPUTensor X = upload(c6, 1, (int)c6.size()), Y = gpu_alloc(1, (int)c6.size());
+    HalfTensor Xh = half_alloc(1, (int)c6.size());
+    cuda_cast_fp32_to_fp16(X.data, Xh.data, X.size);
+    cuda_cast_fp16_to_fp32(Xh.data, Y.data, X.size);
+    auto y = download(Y);
+    EXPECT(y[0] == 65504.0f && y[1] == -65504.0f, "cast clamp");
+    for (int i = 0; i < 256; ++i) EXPECT(y[2 + i] == c6[2 + i], "cast round trip %d", i);
+
+    // fused FFN-up on binary16 operands, NT and TN on the same operands
+    Rng q(9);
+    const int m = 130, k = 96, n = 200;
+    auto xa = rand_vec(q, (size_t)m * k), wa = rand_vec(q, (size_t)k * n, 0.1), bias = rand_vec(q, n, 0.01);
+    GPUTensor X32 = upload(xa, m, k), W32 = upload(wa, k, n), Bi = upload(bias, 1, n);
+    HalfTensor X16 = half_alloc(m, k), W16 = half_alloc(k, n);
+    cuda_cast_fp32_to_fp16(X32.data, X16.data, X16.size);
+    cuda_cast_fp32_to_fp16(W32.data, W16.data, W16.size);
+    GPUTensor Xr = gpu_alloc(m, k), Wr = gpu_alloc(k, n);  // the rounded values, widened
+    cuda_cast_fp16_to_fp32(X16.data, Xr.data, Xr.size);
+    cuda_cast_fp16_to_fp32(W16.data, Wr.data, Wr.size);
+    auto xr = download(Xr), wr = download(Wr);
+    GPUTensor H = gpu_alloc(m, n);
+    cuda_gemm_fp16_bias_gelu(X16.data, m, k, W16.data, n, Bi.data, H.data);
+    auto ref = ref_gemm(NN, xr, wr, m, n, k);
+    for (int i = 0; i < m; ++i)
+        for (int j = 0; j < n; ++j) ref[(size_t)i * n + j] = gelu64(ref[(size_t)i * n + j] + bias[j]);
+    double e = inf_rel(download(H), ref);
+    EXPECT(e <= 2e-3, "fp16 bias+gelu err %.3e", e);
+
+    // NT: [m x n] . W^T with W = Wr read as [k x n] = [N x K] -> dX [m x k]
+    GPUTensor Hn = gpu_alloc(m, n), dX = gpu_alloc(m, k);
+    HalfTensor Hh = half_alloc(m, n);
+    cuda_cast_fp32_to_fp16(H.data, Hh.data, Hh.size);
+    cuda_cast_fp16_to_fp32(Hh.data, Hn.data, Hn.size);
+    auto hr = download(Hn);
+    cuda_gemm_fp16_nt(Hh.data, m, n, W16.data, k, dX.data);
+    e = inf_rel(download(dX), ref_gemm(NT, hr, wr, m, k, n));
+    EXPECT(e <= 2e-3, "fp16 NT err %.3e", e);
+
+    // TN: X^T [k x m] . H [m x n] -> dW [k x n], beta = 0
+    GPUTensor dW = gpu_alloc(k, n);
+    cuda_gemm_fp16_tn(X16.data, m, k, Hh.data, n, dW.data, 0.0f);
+    e = inf_rel(download(dW), ref_gemm(TN, xr, hr, k, n, m));
+    EXPECT(e <= 2e-3, "fp16 TN err %.3e", e);
+}
+
+static void test_errors_and_verify() {
+    GPUTensor A = gpu_alloc(2, 3), B = gpu_alloc(4, 2), C = gpu_alloc(2, 2);
+    bool threw = false;
+    try {
+        cuda_vedic_gemm(A, B, C);
+    } catch (const std::invalid_argument&) {
+        threw = true;
+    }
+    EXPECT(threw, "dimension mismatch must throw std::invalid_argument");
+    threw = false;
+    GPUTensor W = gpu_alloc(3, 4), bias = gpu_alloc(1, 3), D = gpu_alloc(2, 4);
+    try {
+        cuda_vedic_gemm_bias(A, W, bias, D);
+    } catch (const std::invalid_argument&) {
+        threw = true;
+    }
+    EXPECT(threw, "bias size mismatch must throw std::invalid_argument");
+    threw = false;
+    try {
+        cuda_gemm_fp16_fp32out(nullptr, 0, 4, nullptr, 4, nullptr);
+    } catch (const std::invalid_argument&) {
+        threw = true;
+    }
+    EXPECT(threw, "M = 0 must throw std::invalid_argument");
+
+    Rng r(3);
+    const int M = 63, K = 97, N = 47;
+    std::vector<float> a((size_t)M * K), b((size_t)K * N);
+    for (auto& x : a) x = (float)std::fabs(r.next());
+    for (auto& x : b) x = (float)std::fabs(r.next());
+    GPUTensor Av = upload(a, M, K), Bv = upload(b, K, N), Cv = gpu_alloc(M, N);
+    cuda_vedic_gemm(Av, Bv, Cv);
+    VedicVerifyResult v = cuda_vedic_verify(Av, Bv, Cv, 0.05f);
+    EXPECT(v.pass && v.relative_error < 1e-4f, "verify: rel %.3e", v.relative_error);
+}
+
+int main() {
+    int dev = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    hipDeviceProp_t p;
+    HIP_CHECK(hipGetDeviceProperties(&p, dev));
+    std::printf("device %s, %d CUs\n", p.gcnArchName, p.multiProcessorCount);
+    try {
+        test_known_answers();
+        std::printf("known answers done\n");
+        test_fp32_layouts();
+        std::printf("fp32 layouts done\n");
+        test_fp16_path();
+        std::printf("fp16 path done\n");
+        test_errors_and_verify();
+        std::printf("errors and verify done\n");
+    } catch (const std::exception& e) {
+        std::printf("FAIL: unexpected exception: %s\n", e.what());
+        return 2;
+    }
+    HIP_CHECK(hipDeviceSynchronize());
+    if (g_fail) {
+        std::printf("%d check(s) FAILED\n", g_fail);
+        return 1;
+    }
+    std::printf("ALL PASSED\n");
+    return 0;
+}
