@@ -5,6 +5,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <atomic>
+
 #include "../../include/logos_vedic.h"
 #include "vedic_common.hpp"
 #include "vedic_epilogue.hpp"
@@ -15,6 +17,23 @@ hipError_t launch_gemm_f32(int op, bool vec, const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_nn(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_nt(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_tn(const GemmArgs& a, hipStream_t s);
+}  // namespace vedic
+
+namespace vedic {
+
+// Compute units of the calling thread's current device, queried once per
+// device (256 on MI355X); the persistent GEMM grids are sized by it.
+int device_cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
 }  // namespace vedic
 
 using namespace vedic;

@@ -130,6 +130,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, const float16_t (&ac
                     }
                 }
             }
+            // One 32 x 32 block at a time: keeps the 16 row offsets of a block
+            // short-lived instead of all 32 * MI of them in SGPRs at once.
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 }

@@ -1,9 +1,25 @@
-// vedic_gemm_f16_nn.hip -- instantiates the fp16 direct-load GEMM for op NN
-// (one translation unit per op so the build compiles them in parallel).
+// vedic_gemm_f16_nn.hip -- instantiates the fp16 GEMM for op NN (one
+// translation unit per op so the build compiles them in parallel).  The kernels
+// are instantiated explicitly so that every launch has its host stub.
 #include "vedic_gemm_f16.hpp"
 
 namespace vedic {
+
+template __global__ void gemm_f16_kernel<0, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_PLAIN>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_BIAS>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_BIAS_GELU>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_BIAS_GELU_PRE>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_ACCUM>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_GENERIC>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_PLAIN>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_BIAS>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_BIAS_GELU>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_BIAS_GELU_PRE>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_ACCUM>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_GENERIC>(GemmArgs);
+
 hipError_t launch_gemm_f16_direct_nn(const GemmArgs& a, hipStream_t s) {
     return launch_gemm_f16_direct_op<0>(a, s);
 }
+
 }  // namespace vedic
