@@ -7,20 +7,27 @@ fp32 accumulate and fp32 output, on one GPU.  One "step" is one launch of the
 fused GEMM over the whole problem, inputs already resident in HBM.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+    python bench.py --all            # every BASELINE configuration, one JSON line each
+    python bench.py --summarize-traffic FETCH_DIR WRITE_DIR COPY_FETCH_DIR COPY_WRITE_DIR
+                                     # rocprofv3 --pmc CSVs -> profiles/traffic_<workload>.txt
 
-Prints one JSON line (rank 0) with the metric named in BASELINE.json plus:
-  roofline      the dominant kernel against MI355X's published dense fp16
-                MFMA peak (2.5 PFLOP/s), its average launch duration taken
-                with HIP events on the launch stream over the timed region;
-  cpu_baseline  the reference CPU path (the reference's own vedic_gemm_bias +
-                gelu built from its sources into oracle/_ref when that was
-                built, else the bitwise restatement in oracle/) on a bounded
-                row sample of the same workload, single-threaded as the
-                reference is.
+The default run prints one JSON line with the metric named in BASELINE.json plus:
+  roofline      the GEMM kernel against MI355X's published dense MFMA peak
+                (fp16 2.5 PFLOP/s, fp32 157.3 TFLOP/s) or, for the skinny
+                decode shapes, against 8 TB/s of HBM; its average launch time is
+                taken with HIP events on the launch stream over the timed region.
+                `traffic` is the HBM bytes per launch from the committed
+                rocprofv3 FETCH_SIZE / WRITE_SIZE summary, scaled by a copy
+                kernel of known size (None when no summary is committed);
+  cpu_baseline  the reference CPU path -- the reference's own vedic_gemm_bias +
+                gelu built from its sources into oracle/_ref when that was built,
+                else the bitwise restatement in oracle/ -- on a bounded sample of
+                the same workload, single-threaded as the reference is.
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import ctypes
 import json
 import os
@@ -33,17 +40,36 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "GEMM TFLOP/s + % of MFMA peak, FFN-up 8192x1024x4096 fp16->fp32, 1 GPU"
-PEAK_TFLOPS = {"fp16": 2500.0, "fp32": 157.3}  # MI355X dense MFMA, published
+PEAK = {"fp16": 2500.0, "fp32": 157.3}  # MI355X dense MFMA, TFLOP/s (published)
+HBM_PEAK_GBS = 8000.0                   # MI355X HBM3E, GB/s (published)
 
-# name: (M, K, N, op, dtype, epilogue)
+# One GEMM: (M, K, N, op, dtype, epilogue, beta).  op as stored:
+#   NN A[MxK] B[KxN]; NT A[MxK] B[NxK]; TN A[KxM] B[KxN].
+def _g(M, K, N, op="NN", dtype="fp16", epi="none", beta=0.0):
+    return dict(M=M, K=K, N=N, op=op, dtype=dtype, epi=epi, beta=beta)
+
+
+# BASELINE.json configs; each workload is a list of GEMMs run back to back per step.
 WORKLOADS = {
-    "ffn_up_fp16_bias_gelu": (8192, 1024, 4096, "NN", "fp16", "bias_gelu"),
-    "ffn_down_dx_nt_fp16": (8192, 1024, 4096, "NT", "fp16", "none"),
-    "ffn_down_dw_tn_fp16": (4096, 8192, 1024, "TN", "fp16", "none"),
-    "lm_head_fp16": (8192, 1024, 8192, "NN", "fp16", "none"),
-    "lm_head_fp32": (8192, 1024, 8192, "NN", "fp32", "none"),
-    "fp32_nn_512": (512, 1024, 1024, "NN", "fp32", "none"),
+    "fp32_nn_512x1024x1024": dict(cfg=1, gemms=[_g(512, 1024, 1024, dtype="fp32")]),
+    "ffn_up_fp16_bias_gelu": dict(cfg=2, gemms=[_g(8192, 1024, 4096, epi="bias_gelu")]),
+    "ffn_down_dx_nt_fp16": dict(cfg=3, gemms=[_g(8192, 1024, 4096, op="NT")]),
+    "ffn_down_dw_tn_fp16": dict(cfg=3, gemms=[_g(4096, 8192, 1024, op="TN", beta=1.0)]),
+    "lm_head_fp16": dict(cfg=4, gemms=[_g(8192, 1024, 8192)]),
+    "lm_head_fp32": dict(cfg=4, gemms=[_g(8192, 1024, 8192, dtype="fp32")]),
+    **{f"decode_fp16_m{m}": dict(cfg=4, hbm=True, gemms=[_g(m, 1024, 8192)]) for m in (1, 2, 4, 8, 16, 32)},
+    **{f"decode_fp32_m{m}": dict(cfg=4, hbm=True, gemms=[_g(m, 1024, 8192, dtype="fp32")]) for m in (1, 32)},
+    # one 219M-model block at d=1024, seq=8192: 4 forward GEMMs + their dX (NT) and dW (TN, beta=1)
+    "block_fwd_bwd_fp16": dict(cfg=5, gemms=[
+        _g(8192, 1024, 3072), _g(8192, 1024, 1024), _g(8192, 1024, 4096, epi="bias_gelu"),
+        _g(8192, 4096, 1024, epi="bias"),
+        _g(8192, 3072, 1024, op="NT"), _g(8192, 1024, 1024, op="NT"), _g(8192, 4096, 1024, op="NT"),
+        _g(8192, 1024, 4096, op="NT"),
+        _g(1024, 8192, 3072, op="TN", beta=1.0), _g(1024, 8192, 1024, op="TN", beta=1.0),
+        _g(1024, 8192, 4096, op="TN", beta=1.0), _g(4096, 8192, 1024, op="TN", beta=1.0),
+    ]),
 }
+COPY_WORKLOAD = "copy_256mib"  # calibration for the FETCH_SIZE / WRITE_SIZE counters
 
 
 def parse():
@@ -51,74 +77,266 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="ffn_up_fp16_bias_gelu", choices=sorted(WORKLOADS))
-    ap.add_argument("--cpu-rows", type=int, default=None,
-                    help="rows of the workload timed on the CPU baseline (default: ~10-30 s of work)")
+    ap.add_argument("--workload", default="ffn_up_fp16_bias_gelu", choices=sorted(WORKLOADS) + [COPY_WORKLOAD])
+    ap.add_argument("--all", action="store_true", help="every workload, one JSON line each")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="target CPU time of the cpu_baseline sample (default run)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--summarize-traffic", nargs=4, metavar="DIR",
+                    help="FETCH, WRITE, copy FETCH, copy WRITE rocprofv3 output directories")
     return ap.parse_args()
 
 
+# ------------------------------------------------------------- traffic summary
+
+def _pmc_kib(dirpath: str, counter: str, kernel_substr: str):
+    """Mean per-dispatch value of `counter` (KiB) over dispatches of kernels
+    whose name contains kernel_substr, from a rocprofv3 --pmc -f csv run."""
+    vals = []
+    for root, _, files in os.walk(dirpath):
+        for fn in files:
+            if not fn.endswith("counter_collection.csv"):
+                continue
+            with open(os.path.join(root, fn)) as f:
+                for r in csv.DictReader(f):
+                    if r["Counter_Name"] == counter and kernel_substr in r["Kernel_Name"]:
+                        vals.append(float(r["Counter_Value"]))
+    if not vals:
+        raise SystemExit(f"no {counter} rows for '{kernel_substr}' under {dirpath}")
+    return sum(vals) / len(vals), len(vals)
+
+
+def summarize_traffic(args):
+    fetch_dir, write_dir, cfetch_dir, cwrite_dir = args.summarize_traffic
+    kern = "gemm_f16_kernel" if WORKLOADS[args.workload]["gemms"][0]["dtype"] == "fp16" else "gemm_mfma_kernel"
+    fetch, nf = _pmc_kib(fetch_dir, "FETCH_SIZE", kern)
+    write, nw = _pmc_kib(write_dir, "WRITE_SIZE", kern)
+    # torch's copy_ of 256 MiB (the runtime's copyBuffer blit) reads and writes exactly 256 MiB
+    cfetch, _ = _pmc_kib(cfetch_dir, "FETCH_SIZE", "copyBuffer")
+    cwrite, _ = _pmc_kib(cwrite_dir, "WRITE_SIZE", "copyBuffer")
+    ref_kib = 256.0 * 1024
+    f_fetch, f_write = ref_kib / cfetch, ref_kib / cwrite
+    hbm = (fetch * f_fetch + write * f_write) * 1024.0
+    out = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.txt")
+    with open(out, "w") as f:
+        f.write(f"# HBM traffic per launch of {kern} for bench.py --workload {args.workload}\n")
+        f.write("# rocprofv3 --pmc FETCH_SIZE, then --pmc WRITE_SIZE (KiB per dispatch), each scaled by\n")
+        f.write("# the same counter read on torch's copy of 256 MiB (bench.py --workload copy_256mib).\n")
+        f.write("# FETCH_SIZE counts L2-to-fabric reads: repeated fetches by different XCDs' L2s\n")
+        f.write("# are all counted, whether the Infinity Cache or HBM serves them.\n")
+        f.write(f"fetch_kib_per_dispatch: {fetch:.1f}  (mean of {nf} dispatches)\n")
+        f.write(f"write_kib_per_dispatch: {write:.1f}  (mean of {nw} dispatches)\n")
+        f.write(f"copy_fetch_kib: {cfetch:.1f}\ncopy_write_kib: {cwrite:.1f}\n")
+        f.write(f"fetch_scale: {f_fetch:.4f}\nwrite_scale: {f_write:.4f}\n")
+        f.write(f"hbm_bytes_per_launch: {int(hbm)}\n")
+    print(open(out).read())
+
+
 def traffic_from_profiles(workload: str):
-    """HBM bytes per launch measured by the rocprofv3 --pmc runs whose summary
-    is committed under profiles/ (FETCH_SIZE + WRITE_SIZE, scaled by the copy
-    kernel calibration); None if that summary is absent."""
-    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+    """HBM bytes per launch from the committed summary, or None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.txt")
     if not os.path.exists(path):
         return None
-    try:
-        with open(path) as f:
-            return int(json.load(f)["hbm_bytes_per_launch"])
-    except (OSError, ValueError, KeyError):
-        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("hbm_bytes_per_launch:"):
+                return int(line.split(":")[1].split()[0])
+    return None
 
 
-def cpu_baseline(M, K, N, op, dtype, epi, rows):
-    """Times the reference CPU path on `rows` rows of the workload (1 thread)."""
+# ------------------------------------------------------------------ CPU leg
+
+def cpu_baseline(w: dict, seconds: float, seed: int = 7):
+    """The reference CPU path (single thread) on a row sample of the workload's
+    GEMMs, repeated until about `seconds` of CPU time.  Rows of every GEMM are
+    independent and cost the same, so TFLOP/s over a row sample is the rate
+    of the whole GEMM."""
     from oracle import oracle as o
 
-    rng = np.random.default_rng(7)
     kind = "reference" if o.ref_available() else "port"
-    A = rng.standard_normal((rows, K), dtype=np.float32)
-    B = (rng.standard_normal((K, N), dtype=np.float32) * np.float32(0.02))
-    bias = (rng.standard_normal(N, dtype=np.float32) * np.float32(0.01))
-    if dtype == "fp16":
-        A, B = o.f16_round(A), o.f16_round(B)
-    if op == "NT":
-        Bt = np.ascontiguousarray(B.T)
-    t0 = time.perf_counter()
-    if kind == "reference":
-        if op == "NN":
-            C = o.ref_vedic_gemm_bias(A, B, bias) if epi != "none" else o.ref_vedic_gemm(A, B)
-        elif op == "NT":
-            C = o.ref_gemm_nt(A, Bt)
-        else:  # TN: output rows are columns of X[K x M]
-            C = o.ref_gemm_tn(np.ascontiguousarray(A.T), B)
-        if epi == "bias_gelu":
-            C = o.ref_gelu(C)
-    else:
-        if op == "NN":
-            C = o.vedic_gemm_bias(A, B, bias, nthreads=1) if epi != "none" else o.vedic_gemm(A, B, nthreads=1)
-        elif op == "NT":
-            C = o.gemm_nt(A, Bt, nthreads=1)
-        else:
-            C = o.gemm_tn(np.ascontiguousarray(A.T), B, nthreads=1)
-        if epi == "bias_gelu":
-            C = o.gelu(C)
-    dt = time.perf_counter() - t0
-    flops = 2.0 * rows * K * N
+    rng = np.random.default_rng(seed)
+    per_gemm = max(seconds / len(w["gemms"]), 0.5)
+    total_flops = 0.0
+    total_t = 0.0
+    parts = []
+    for g in w["gemms"]:
+        M, K, N, op = g["M"], g["K"], g["N"], g["op"]
+        # ~20 GFLOP/s single thread: rows for about per_gemm seconds, 1..M
+        rows = int(max(1, min(M, 2.0e10 * per_gemm / (2.0 * K * N))))
+        A = rng.standard_normal((rows, K), dtype=np.float32)
+        B = (rng.standard_normal((K, N), dtype=np.float32) * np.float32(0.02))
+        bias = (rng.standard_normal(N, dtype=np.float32) * np.float32(0.01))
+        if g["dtype"] == "fp16":
+            A, B = o.f16_round(A), o.f16_round(B)
+        if op == "NT":
+            B = np.ascontiguousarray(B.T)
+        if op == "TN":
+            A = np.ascontiguousarray(A.T)
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            if kind == "reference":
+                if op == "NN":
+                    C = o.ref_vedic_gemm_bias(A, B, bias) if g["epi"] != "none" else o.ref_vedic_gemm(A, B)
+                elif op == "NT":
+                    C = o.ref_gemm_nt(A, B)
+                else:
+                    C = o.ref_gemm_tn(A, B)
+                if g["epi"] == "bias_gelu":
+                    C = o.ref_gelu(C)
+            else:
+                if op == "NN":
+                    C = (o.vedic_gemm_bias(A, B, bias, nthreads=1) if g["epi"] != "none"
+                         else o.vedic_gemm(A, B, nthreads=1))
+                elif op == "NT":
+                    C = o.gemm_nt(A, B, nthreads=1)
+                else:
+                    C = o.gemm_tn(A, B, nthreads=1)
+                if g["epi"] == "bias_gelu":
+                    C = o.gelu(C)
+            reps += 1
+            if time.perf_counter() - t0 >= per_gemm:
+                break
+        dt = time.perf_counter() - t0
+        total_flops += reps * 2.0 * rows * K * N
+        total_t += dt
+        parts.append(f"{op} {rows}/{M} rows x{reps}")
     return {
-        "value": flops / dt / 1e12,
+        "value": total_flops / total_t / 1e12,
         "unit": "TFLOP/s",
         "cores": 1,
         "kind": kind,
-        "sample": f"{rows} of {M} rows ({rows * K * N * 2 / 1e9:.1f} GFLOP), {dt:.1f} s, "
-                  f"single thread, reference flags -O3 -march=x86-64",
+        "sample": f"{'; '.join(parts)} ({total_flops / 1e9:.1f} GFLOP in {total_t:.1f} s), single thread, "
+                  f"reference flags -O3 -march=x86-64",
         "threads_available": os.cpu_count(),
     }
 
 
+# ------------------------------------------------------------------ GPU leg
+
+def make_step(w: dict, dev, torch):
+    """Allocates seeded inputs for every GEMM of the workload and returns
+    (step function, list of (desc, flops, algorithmic HBM bytes))."""
+    from logos_amd import _lib
+
+    lib = _lib.load()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x4C4F474F ^ (w["cfg"] << 8))
+    stream = torch.cuda.current_stream()
+    keep = []
+    items = []
+    for g in w["gemms"]:
+        M, K, N, op = g["M"], g["K"], g["N"], g["op"]
+        a_shape = (K, M) if op == "TN" else (M, K)
+        b_shape = (N, K) if op == "NT" else (K, N)
+        A = torch.randn(a_shape, generator=gen, device=dev)
+        B = torch.randn(b_shape, generator=gen, device=dev) * 0.02
+        bias = torch.randn((N,), generator=gen, device=dev) * 0.01
+        if g["dtype"] == "fp16":
+            A, B = A.half(), B.half()
+        C = torch.randn((M, N), generator=gen, device=dev) * 1e-3 if g["beta"] else torch.empty((M, N), device=dev)
+        keep += [A, B, bias, C]
+        epi = {"none": _lib.EPI_NONE, "bias": _lib.EPI_BIAS, "bias_gelu": _lib.EPI_BIAS_GELU}[g["epi"]]
+        d = _lib.GemmDesc(
+            op={"NN": _lib.OP_NN, "NT": _lib.OP_NT, "TN": _lib.OP_TN}[op],
+            in_dtype=_lib.DT_F16 if g["dtype"] == "fp16" else _lib.DT_F32, out_dtype=_lib.DT_F32,
+            M=M, N=N, K=K, A=A.data_ptr(), lda=A.shape[1], B=B.data_ptr(), ldb=B.shape[1],
+            C=C.data_ptr(), ldc=N, alpha=1.0, beta=g["beta"],
+            bias=bias.data_ptr() if g["epi"] != "none" else None, epilogue=epi,
+            preact=None, ld_preact=0, stream=stream.cuda_stream)
+        es = 2 if g["dtype"] == "fp16" else 4
+        hbm = (M * K + K * N) * es + M * N * 4 * (2 if g["beta"] else 1) + (N * 4 if g["epi"] != "none" else 0)
+        items.append((d, 2.0 * M * N * K, hbm))
+    ptrs = [ctypes.byref(d) for d, _, _ in items]
+    gemm = lib.vedic_gemm
+
+    def step():
+        for p in ptrs:
+            rc = gemm(p)
+            if rc:
+                raise RuntimeError(f"vedic_gemm failed: {_lib.status_string(rc)}")
+
+    step.keep = keep  # inputs stay alive with the closure
+    return step, items
+
+
+def time_steps(step, steps, warmup, torch):
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return ev0.elapsed_time(ev1) / steps, wall
+
+
+def run_workload(name, args, torch, dev, with_cpu):
+    w = WORKLOADS[name]
+    step, items = make_step(w, dev, torch)
+    ms, wall = time_steps(step, args.steps, args.warmup, torch)
+    flops = sum(f for _, f, _ in items)
+    hbm = sum(b for _, _, b in items)
+    dtype = w["gemms"][0]["dtype"]
+    tflops = flops / (ms * 1e-3) / 1e12
+    if w.get("hbm"):
+        gbs = hbm / (ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(name),
+                "algorithmic_bytes_per_launch": hbm}
+    else:
+        roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK[dtype], "unit": "TFLOP/s",
+                "frac": round(tflops / PEAK[dtype], 4), "traffic": traffic_from_profiles(name),
+                "algorithmic_flops_per_launch": flops, "algorithmic_bytes_per_launch": hbm}
+    roof["kernel_avg_us"] = round(ms * 1e3 / len(items), 3)
+    cpu = cpu_baseline(w, args.cpu_seconds) if with_cpu else None
+    g0 = w["gemms"][0]
+    config = {"workload": name, "baseline_config": w["cfg"], "gemms": len(items),
+              "accumulate": "fp32", "output": "fp32"}
+    if len(items) == 1:
+        config.update({k: g0[k] for k in ("M", "K", "N", "op", "epi", "beta")})
+    return {
+        "metric": METRIC if name == "ffn_up_fp16_bias_gelu" else f"GEMM TFLOP/s, {name}, 1 GPU",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic (seeded torch.randn: activations N(0,1), weights N(0,0.02), bias N(0,0.01); "
+                "fp16 operands rounded by torch's half() cast)",
+        "config": config,
+        "pct_of_peak": round(100.0 * tflops / PEAK[dtype], 2),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "wall_s": round(wall, 4),
+    }
+
+
+def run_copy(args, torch, dev):
+    n = 256 * 1024 * 1024 // 4
+    src = torch.randn(n, device=dev)
+    dst = torch.empty_like(src)
+    ms, _ = time_steps(lambda: dst.copy_(src), args.steps, args.warmup, torch)
+    gbs = 2 * n * 4 / (ms * 1e-3) / 1e9
+    return {"workload": COPY_WORKLOAD, "ms_per_copy": round(ms, 5), "GB/s": round(gbs, 1)}
+
+
 def main():
     args = parse()
+    if args.summarize_traffic:
+        summarize_traffic(args)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
                           "n_gpus": args.gpus}))
@@ -126,103 +344,20 @@ def main():
 
     import torch
 
-    from logos_amd import _lib, vedic
-
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
-    M, K, N, op, dtype, epi = WORKLOADS[args.workload]
-    lib = _lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    g = torch.Generator(device=dev)
-    g.manual_seed(0x4C4F474F)
-    op_code = {"NN": vedic.OP_NN, "NT": vedic.OP_NT, "TN": vedic.OP_TN}[op]
-    a_shape = (K, M) if op == "TN" else (M, K)
-    b_shape = (N, K) if op == "NT" else (K, N)
-    A32 = torch.randn(a_shape, generator=g, device=dev)
-    B32 = torch.randn(b_shape, generator=g, device=dev) * 0.02
-    bias = torch.randn((N,), generator=g, device=dev) * 0.01
-    if dtype == "fp16":
-        A = vedic.cast_fp32_to_fp16(A32)
-        B = vedic.cast_fp32_to_fp16(B32)
-        del A32, B32
-    else:
-        A, B = A32, B32
-    C = torch.empty((M, N), dtype=torch.float32, device=dev)
-    stream = torch.cuda.current_stream()
-    desc = _lib.GemmDesc(
-        op=op_code, in_dtype=_lib.DT_F16 if dtype == "fp16" else _lib.DT_F32, out_dtype=_lib.DT_F32,
-        M=M, N=N, K=K, A=A.data_ptr(), lda=A.shape[1], B=B.data_ptr(), ldb=B.shape[1],
-        C=C.data_ptr(), ldc=N, alpha=1.0, beta=0.0,
-        bias=bias.data_ptr() if epi != "none" else None,
-        epilogue=_lib.EPI_BIAS_GELU if epi == "bias_gelu" else _lib.EPI_NONE,
-        preact=None, ld_preact=0, stream=stream.cuda_stream)
-    pdesc = ctypes.byref(desc)
-    gemm = lib.vedic_gemm
-
-    def step():
-        rc = gemm(pdesc)
-        if rc:
-            raise RuntimeError(f"vedic_gemm failed: {_lib.status_string(rc)}")
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    ev0.record(stream)
-    for _ in range(args.steps):
-        step()
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    gpu_ms = ev0.elapsed_time(ev1)
-    ms_per_step = gpu_ms / args.steps
-    flops = 2.0 * M * N * K
-    tflops = flops / (ms_per_step * 1e-3) / 1e12
-    peak = PEAK_TFLOPS[dtype]
-
-    cpu = None
-    if not args.no_cpu:
-        rows = args.cpu_rows
-        if rows is None:
-            # ~10-30 s of single-thread work at ~8-10 GFLOP/s
-            rows = max(64, min(M, int(1.6e11 / (2.0 * K * N))))
-            rows -= rows % 64
-        cpu = cpu_baseline(M, K, N, op, dtype, epi, rows)
-
-    out = {
-        "metric": METRIC,
-        "value": round(tflops, 2),
-        "unit": "TFLOP/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": dtype,
-        "data": "synthetic (seeded torch.randn: X~N(0,1), W~N(0,0.02), bias~N(0,0.01); "
-                "fp16 by the library's clamp+RNE cast)",
-        "config": {"workload": args.workload, "M": M, "K": K, "N": N, "op": op,
-                   "accumulate": "fp32", "output": "fp32", "epilogue": epi},
-        "pct_of_peak": round(100.0 * tflops / peak, 2),
-        "roofline": {
-            "bound": "mfma",
-            "achieved": round(tflops, 2),
-            "peak": peak,
-            "unit": "TFLOP/s",
-            "frac": round(tflops / peak, 4),
-            "traffic": traffic_from_profiles(args.workload),
-            "kernel_avg_us": round(ms_per_step * 1e3, 3),
-            "algorithmic_flops_per_launch": flops,
-        },
-        "cpu_baseline": cpu,
-        "wall_s": round(wall, 4),
-    }
-    print(json.dumps(out), flush=True)
+    if args.workload == COPY_WORKLOAD:
+        print(json.dumps(run_copy(args, torch, dev)), flush=True)
+        return
+    if args.all:
+        for name in WORKLOADS:
+            out = run_workload(name, args, torch, dev, with_cpu=not args.no_cpu)
+            print(json.dumps(out), flush=True)
+            torch.cuda.empty_cache()
+        return
+    print(json.dumps(run_workload(args.workload, args, torch, dev, with_cpu=not args.no_cpu)), flush=True)
 
 
 if __name__ == "__main__":
