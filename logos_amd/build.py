@@ -26,6 +26,7 @@ SOURCES = [
     "vedic_gemm_f16_nt.hip",
     "vedic_gemm_f16_tn.hip",
     "vedic_gemm_mfma.hip",
+    "vedic_gemm_skinny.hip",
     "vedic_capi.hip",
 ]
 

@@ -17,6 +17,7 @@ hipError_t launch_gemm_f32(int op, bool vec, const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_nn(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_nt(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_tn(const GemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_f16_skinny(const GemmArgs& a, hipStream_t s);
 }  // namespace vedic
 
 namespace vedic {
@@ -112,7 +113,10 @@ extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
     hipStream_t s = static_cast<hipStream_t>(d->stream);
     hipError_t e;
     if (d->in_dtype == VEDIC_DT_F16) {
-        if (vec && d->lda < kMaxLd && d->ldb < kMaxLd) {
+        if (vec && d->lda < kMaxLd && d->ldb < kMaxLd && d->op == VEDIC_OP_NN && d->M <= 32) {
+            // decode-time shapes: bound by streaming B once from HBM
+            e = launch_gemm_f16_skinny(a, s);
+        } else if (vec && d->lda < kMaxLd && d->ldb < kMaxLd) {
             e = d->op == VEDIC_OP_NN   ? launch_gemm_f16_direct_nn(a, s)
                 : d->op == VEDIC_OP_NT ? launch_gemm_f16_direct_nt(a, s)
                                        : launch_gemm_f16_direct_tn(a, s);

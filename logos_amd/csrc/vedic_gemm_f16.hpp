@@ -55,8 +55,14 @@ __device__ __forceinline__ int swz_kc(int r) {
     if constexpr (CPR == 8) return (r & 7) ^ ((r >> 3) & 3);
     else return ((r >> 1) ^ (r >> 3)) & 3;
 }
-// MC slot swizzle (rows of at least 16 slots, i.e. BM / BN >= 128).
-__device__ __forceinline__ int swz_mc(int k) { return 4 * (k & 3); }
+// MC slot swizzle.  Rows of 16 or more slots (BM / BN >= 128): slots XOR
+// 4 (k mod 4).  Rows of 4 slots (32 columns, 64 bytes) need none: the four
+// k rows a 16-lane transpose read touches already fill a 256-byte bank window.
+template <int R>
+__device__ __forceinline__ int swz_mc(int k) {
+    static_assert(R == 32 || R >= 128, "MC layouts of 32 or >= 128 columns");
+    return R >= 128 ? 4 * (k & 3) : 0;
+}
 
 // vmcnt(N), expcnt and lgkmcnt left at their maxima (gfx9 encoding).
 template <int N>
@@ -87,7 +93,7 @@ struct Side {
         const int q = (wave * NLD + i) * 64 + lane;
         row = q / CPR;
         const int p = q % CPR;
-        c = KC ? (p ^ swz_kc<CPR>(row)) : (p ^ swz_mc(row));
+        c = KC ? (p ^ swz_kc<CPR>(row)) : (p ^ swz_mc<R>(row));
     }
     __device__ __forceinline__ void init(int wave, int lane, int64_t ld, int mn0, int MN) {
 #pragma unroll
@@ -138,7 +144,7 @@ __device__ __forceinline__ half8_t read_frag(const char* lds, int rc0, int kk, i
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int k = 16 * kk + 8 * (g >> 1) + 4 * t + (s >> 2);
-            const int off = k * (2 * R) + (((n >> 3) ^ swz_mc(k)) << 4) + 8 * (s & 1);
+            const int off = k * (2 * R) + (((n >> 3) ^ swz_mc<R>(k)) << 4) + 8 * (s & 1);
             u.q[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(lds + off));
         }
         return u.h;
@@ -219,8 +225,6 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
     constexpr int L = SA::NLD + SB::NLD;  // load instructions per wave per stage
     static_assert(ST >= 2 && ST <= 4, "2 to 4 LDS stages");
     static_assert((ST - 2) * L < 64, "vmcnt range");
-    static_assert(A_KC || BM >= 128, "MC swizzle needs 16 slots per row");
-    static_assert(B_KC || BN >= 128, "MC swizzle needs 16 slots per row");
 
     // One LDS object per operand and stage: reads of one stage provably do
     // not alias the direct loads into another.

@@ -261,3 +261,43 @@ def test_verify_checksum():
         assert r.passed
         assert abs(r.checksum_vedic - p) <= 1e-5 * max(1.0, abs(p))
         assert abs(r.checksum_C - s) <= 1e-5 * max(1.0, abs(s))
+
+
+# ------------------------------------------------ skinny M (decode) kernel
+
+@pytest.mark.parametrize("M", [1, 2, 5, 16, 31, 32])
+@pytest.mark.parametrize("K,N", [(64, 8), (200, 40), (1000, 264), (1024, 8192), (3000, 520)])
+def test_skinny_m_fp16(M, K, N):
+    """M <= 32 NN products take the split-K decode kernel: every K length
+    (partial 64-deep stages, quarters past K), every column edge, every row count."""
+    vedic = V()
+    rng = np.random.default_rng(zlib.crc32(f"skinny-{M}-{K}-{N}".encode()))
+    A, B = normal(rng, (M, K)), normal(rng, (K, N), std=0.05)
+    a, A = dev_f16(A)
+    b, B = dev_f16(B)
+    got = host(vedic.gemm(vedic.OP_NN, a, b))
+    check(got, o.NN, A, B, tol=FP16_TOL, label=f"skinny {M}x{K}x{N}")
+    ref = restated(o.NN, A, B)
+    assert o.inf_rel_err(got, ref) <= FP16_TOL + fp32_tol(K)
+
+
+def test_skinny_m_epilogues():
+    vedic = V()
+    rng = np.random.default_rng(17)
+    M, K, N = 7, 520, 264
+    A, B = normal(rng, (M, K)), normal(rng, (K, N), std=0.05)
+    bias, C0 = normal(rng, (N,), std=0.1), normal(rng, (M, N))
+    a, A = dev_f16(A)
+    b, B = dev_f16(B)
+    pre = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    got = host(vedic.gemm(vedic.OP_NN, a, b, bias=dev(bias), epilogue=vedic.EPI_BIAS_GELU, preact=pre))
+    check(got, o.NN, A, B, tol=FP16_TOL, bias=bias, gelu=True, label="skinny bias+gelu")
+    check(host(pre), o.NN, A, B, tol=FP16_TOL, bias=bias, label="skinny preact")
+    got = host(vedic.gemm(vedic.OP_NN, a, b, dev(C0), alpha=0.5, beta=1.0))
+    check(got, o.NN, A, B, tol=FP16_TOL, alpha=0.5, beta=1.0, C0=C0, label="skinny alpha/beta")
+    got = host(vedic.gemm_fp16_fp16out(a, b))
+    check(got, o.NN, A, B, tol=FP16_TOL + 2.0 ** -11, label="skinny f16 out")
+    # no write outside C: a view with a wider leading dimension
+    buf = torch.full((M, N + 8), 3.0, dtype=torch.float32, device="cuda")
+    vedic.gemm(vedic.OP_NN, a, b, buf[:, :N])
+    assert np.all(host(buf)[:, N:] == 3.0)
