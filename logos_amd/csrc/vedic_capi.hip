@@ -52,6 +52,82 @@ static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; 
 // Largest leading dimension (elements) the kernels' 32-bit tile offsets allow.
 static constexpr int64_t kMaxLd = int64_t(1) << 22;
 
+// ------------------------------------------------------------ split-K
+
+// C = epi(alpha * sum_s ws[s] + beta * C_old + bias), the slices added in
+// ascending s so the result does not depend on timing.  ws is [S][M][N].
+__global__ void splitk_reduce_kernel(const float* __restrict__ ws, int S, GemmArgs a) {
+    const int64_t total = (int64_t)a.M * a.N;
+    const int epi = a.epi;
+    const bool f16out = epi & EPI_F16OUT;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int i = (int)(idx / a.N), j = (int)(idx - (int64_t)i * a.N);
+        float v = ws[idx];
+        for (int t = 1; t < S; ++t) v += ws[(int64_t)t * total + idx];
+        const int64_t c = (int64_t)i * a.ldc + j;
+        if (epi & EPI_ALPHA) v *= a.alpha;
+        if (epi & EPI_BETA)
+            v += a.beta * (f16out ? (float)static_cast<const _Float16*>(a.C)[c] : static_cast<const float*>(a.C)[c]);
+        if (epi & EPI_BIAS) v += a.bias[j];
+        if (epi & EPI_PREACT) a.preact[(int64_t)i * a.ldp + j] = v;
+        if (epi & EPI_GELU) v = gelu_tanh(v);
+        if (f16out)
+            static_cast<_Float16*>(a.C)[c] = (_Float16)v;
+        else
+            static_cast<float*>(a.C)[c] = v;
+    }
+}
+
+// Number of contraction slices for an fp16 product whose output is too
+// small to give every CU a tile: output tiles of 128 x 128 below half the CU
+// count and K of at least 2048.  1 = no split.
+static int choose_ksplit(int M, int N, int K, int cus) {
+    const int64_t big = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+    if (big >= cus) return 1;  // the 256 x 256 kernel fills the GPU
+    const int64_t tiles = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+    if (tiles * 2 > cus || K < 2048) return 1;
+    int s = (int)(cus / tiles);
+    s = s < 8 ? s : 8;
+    s = s < K / 1024 ? s : K / 1024;
+    return s >= 2 ? s : 1;
+}
+
+// Runs the product as `ks` slices into a stream-ordered workspace, then the
+// reduction with the caller's epilogue.
+static hipError_t launch_f16_split(int op, const GemmArgs& a, int ks, hipStream_t s) {
+    const int kslice = (((a.K + ks - 1) / ks) + 63) / 64 * 64;
+    ks = (a.K + kslice - 1) / kslice;
+    const int64_t total = (int64_t)a.M * a.N;
+    float* ws = nullptr;
+    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), sizeof(float) * (size_t)total * ks, s);
+    if (e != hipSuccess) return e;
+    GemmArgs p = a;
+    p.C = ws;
+    p.ldc = a.N;
+    p.bias = nullptr;
+    p.preact = nullptr;
+    p.ldp = 0;
+    p.alpha = 1.0f;
+    p.beta = 0.0f;
+    p.epi = 0;
+    p.epi_kind = EK_PLAIN;
+    p.ksplit = ks;
+    p.kslice = kslice;
+    p.c_split_stride = total;
+    e = op == VEDIC_OP_NN   ? launch_gemm_f16_direct_nn(p, s)
+        : op == VEDIC_OP_NT ? launch_gemm_f16_direct_nt(p, s)
+                            : launch_gemm_f16_direct_tn(p, s);
+    if (e == hipSuccess) {
+        int64_t blocks = (total + 255) / 256;
+        if (blocks > 8192) blocks = 8192;
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s, ws, ks, a);
+        e = hipGetLastError();
+    }
+    const hipError_t f = hipFreeAsync(ws, s);
+    return e != hipSuccess ? e : f;
+}
+
 // ------------------------------------------------------------------ GEMM
 
 extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
@@ -117,9 +193,13 @@ extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
             // decode-time shapes: bound by streaming B once from HBM
             e = launch_gemm_f16_skinny(a, s);
         } else if (vec && d->lda < kMaxLd && d->ldb < kMaxLd) {
-            e = d->op == VEDIC_OP_NN   ? launch_gemm_f16_direct_nn(a, s)
-                : d->op == VEDIC_OP_NT ? launch_gemm_f16_direct_nt(a, s)
-                                       : launch_gemm_f16_direct_tn(a, s);
+            const int ks = choose_ksplit(d->M, d->N, d->K, device_cu_count());
+            if (ks > 1)
+                e = launch_f16_split(d->op, a, ks, s);
+            else
+                e = d->op == VEDIC_OP_NN   ? launch_gemm_f16_direct_nn(a, s)
+                    : d->op == VEDIC_OP_NT ? launch_gemm_f16_direct_nt(a, s)
+                                           : launch_gemm_f16_direct_tn(a, s);
         } else {
             e = launch_gemm_f16_generic(d->op, a, s);
         }

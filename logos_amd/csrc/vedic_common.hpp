@@ -67,6 +67,11 @@ struct GemmArgs {
     int epi_kind;  // EpiKind (vedic_epilogue.hpp), derived from epi/alpha/beta
     int tiles_m, tiles_n;
     int group_m;
+    // split-K: work item w covers tile w % ntiles over contraction indices
+    // [s * kslice, (s + 1) * kslice), s = w / ntiles; its raw fp32 partial goes
+    // to C + s * c_split_stride.  ksplit = 1: one item per tile over all of K.
+    int ksplit, kslice;
+    int64_t c_split_stride;
 };
 
 }  // namespace vedic

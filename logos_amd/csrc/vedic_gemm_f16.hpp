@@ -206,14 +206,34 @@ __device__ __forceinline__ void tile_of(const GemmArgs& a, int t, int& tm, int& 
     tn = in_g / rows;
 }
 
+// One work item: a tile and its slice of the contraction.
+struct WorkItem {
+    int m0, n0, kb, ke, nk, s;
+};
+
+template <int BM, int BN, int BK>
+__device__ __forceinline__ WorkItem work_of(const GemmArgs& a, int w, int ntiles) {
+    WorkItem it;
+    it.s = w / ntiles;
+    int tm, tn;
+    tile_of(a, w - it.s * ntiles, tm, tn);
+    it.m0 = tm * BM;
+    it.n0 = tn * BN;
+    it.kb = it.s * a.kslice;
+    it.ke = min(a.K, it.kb + a.kslice);
+    it.nk = (it.ke - it.kb + BK - 1) / BK;
+    return it;
+}
+
 #define VEDIC_A_TILE(k) \
     (A_KC ? A + (int64_t)m0 * args.lda + ((k) < K ? (k) : 0) : A + (int64_t)((k) < K ? (k) : 0) * args.lda + m0)
 #define VEDIC_B_TILE(k) \
     (B_KC ? B + (int64_t)n0 * args.ldb + ((k) < K ? (k) : 0) : B + (int64_t)((k) < K ? (k) : 0) * args.ldb + n0)
 #define VEDIC_ISSUE(kt, la, lb)                                                          \
     do {                                                                                 \
-        sa.load(VEDIC_A_TILE((kt) * BK), (la), wave, lane, K - (kt) * BK);               \
-        sb.load(VEDIC_B_TILE((kt) * BK), (lb), wave, lane, K - (kt) * BK);               \
+        const int k_ = it.kb + (kt) * BK;                                                \
+        sa.load(VEDIC_A_TILE(k_), (la), wave, lane, it.ke - k_);                         \
+        sb.load(VEDIC_B_TILE(k_), (lb), wave, lane, it.ke - k_);                         \
     } while (0)
 
 template <int OP, int BM, int BN, int BK, int ST, int WGM, int WGN, int KIND>
@@ -245,24 +265,23 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
     const _Float16* __restrict__ A = static_cast<const _Float16*>(args.A);
     const _Float16* __restrict__ B = static_cast<const _Float16*>(args.B);
     const int K = args.K;
-    const int nk = (K + BK - 1) / BK;
     const int G = gridDim.x;
     const int b = blockIdx.x;
     const int base = (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
     const int ntiles = args.tiles_m * args.tiles_n;
+    const int nwork = ntiles * args.ksplit;
 
-    int t = base;
-    if (t >= ntiles) return;
-    int tm, tn;
-    tile_of(args, t, tm, tn);
-    int m0 = tm * BM, n0 = tn * BN;
+    int w = base;
+    if (w >= nwork) return;
+    WorkItem it = work_of<BM, BN, BK>(args, w, ntiles);
+    int m0 = it.m0, n0 = it.n0;
     SA sa;
     SB sb;
     sa.init(wave, lane, args.lda, m0, args.M);
     sb.init(wave, lane, args.ldb, n0, args.N);
 #pragma unroll
     for (int s = 0; s < ST - 1; ++s)
-        if (s < nk) VEDIC_ISSUE(s, As[s], Bs[s]);
+        if (s < it.nk) VEDIC_ISSUE(s, As[s], Bs[s]);
 
     while (true) {
         float16_t acc[MI][NI];
@@ -271,6 +290,7 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
 #pragma unroll
             for (int j = 0; j < NI; ++j) acc[i][j] = float16_t{};
 
+        const int nk = it.nk;
         for (int k0 = 0; k0 < nk; k0 += ST) {
 #pragma unroll
             for (int s = 0; s < ST; ++s) {
@@ -290,24 +310,26 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
         }
 
         const int row0 = m0 + wm * WM, col0 = n0 + wn * WN;
-        t += G;
-        const bool more = t < ntiles;
+        GemmArgs ea = args;
+        if (args.ksplit > 1) ea.C = static_cast<float*>(args.C) + it.s * args.c_split_stride;
+        w += G;
+        const bool more = w < nwork;
         if (more) {
             __syncthreads();  // every wave is done reading the stage buffers
-            tile_of(args, t, tm, tn);
-            m0 = tm * BM;
-            n0 = tn * BN;
+            it = work_of<BM, BN, BK>(args, w, ntiles);
+            m0 = it.m0;
+            n0 = it.n0;
             sa.init(wave, lane, args.lda, m0, args.M);
             sb.init(wave, lane, args.ldb, n0, args.N);
 #pragma unroll
             for (int s = 0; s < ST - 1; ++s)
-                if (s < nk) VEDIC_ISSUE(s, As[s], Bs[s]);
+                if (s < it.nk) VEDIC_ISSUE(s, As[s], Bs[s]);
         }
         const bool full = (row0 + WM <= args.M) && (col0 + WN <= args.N);
         if (KIND != EK_GENERIC && full)
-            epilogue<KIND, false, MI, NI>(args, acc, row0, col0, lane);
+            epilogue<KIND, false, MI, NI>(ea, acc, row0, col0, lane);
         else
-            epilogue<KIND, true, MI, NI>(args, acc, row0, col0, lane);
+            epilogue<KIND, true, MI, NI>(ea, acc, row0, col0, lane);
         if (!more) break;
     }
 }
@@ -331,9 +353,13 @@ static hipError_t launch_f16(GemmArgs a, hipStream_t s) {
     a.tiles_m = (a.M + Cfg::BM - 1) / Cfg::BM;
     a.tiles_n = (a.N + Cfg::BN - 1) / Cfg::BN;
     if (a.group_m <= 0) a.group_m = 8;
-    const int ntiles = a.tiles_m * a.tiles_n;
+    if (a.ksplit < 1) {
+        a.ksplit = 1;
+        a.kslice = a.K;
+    }
+    const int nwork = a.tiles_m * a.tiles_n * a.ksplit;
     const int cus = device_cu_count();
-    const int grid = ntiles < cus ? ntiles : cus;
+    const int grid = nwork < cus ? nwork : cus;
     hipLaunchKernelGGL((gemm_f16_kernel<OP, Cfg::BM, Cfg::BN, Cfg::BK, Cfg::ST, Cfg::WGM, Cfg::WGN, KIND>),
                        dim3(grid), dim3(Cfg::WGM * Cfg::WGN * 64), 0, s, a);
     return hipGetLastError();

@@ -301,3 +301,47 @@ def test_skinny_m_epilogues():
     buf = torch.full((M, N + 8), 3.0, dtype=torch.float32, device="cuda")
     vedic.gemm(vedic.OP_NN, a, b, buf[:, :N])
     assert np.all(host(buf)[:, N:] == 3.0)
+
+
+# ----------------------------------------------------------- split-K path
+
+@pytest.mark.parametrize("opname", list(OPS))
+@pytest.mark.parametrize("shape", [(256, 256, 4096), (100, 200, 3000), (1024, 1024, 8192), (136, 264, 2112)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_split_k(opname, shape):
+    """Small outputs with a long contraction are split over K into a workspace
+    and reduced in a fixed order; results must match a single pass."""
+    vedic = V()
+    layout = OPS[opname]
+    M, N, K = shape
+    rng = np.random.default_rng(zlib.crc32(f"splitk-{opname}-{shape}".encode()))
+    A, B = _operands(rng, layout, M, N, K)
+    a, A = dev_f16(A)
+    b, B = dev_f16(B)
+    got = host(vedic.gemm(layout, a, b))
+    check(got, layout, A, B, tol=FP16_TOL, label=f"split-K {opname} {shape}")
+    # deterministic: a second run is bit-identical
+    assert np.array_equal(host(vedic.gemm(layout, a, b)), got)
+
+
+def test_split_k_epilogues():
+    vedic = V()
+    rng = np.random.default_rng(23)
+    M, N, K = 192, 256, 4096
+    A, B = normal(rng, (K, M)), normal(rng, (K, N), std=0.05)
+    bias, C0 = normal(rng, (N,), std=0.1), normal(rng, (M, N))
+    a, A = dev_f16(A)
+    b, B = dev_f16(B)
+    pre = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    got = host(vedic.gemm(vedic.OP_TN, a, b, bias=dev(bias), epilogue=vedic.EPI_BIAS_GELU, preact=pre))
+    check(got, o.TN, A, B, tol=FP16_TOL, bias=bias, gelu=True, label="split-K bias+gelu")
+    check(host(pre), o.TN, A, B, tol=FP16_TOL, bias=bias, label="split-K preact")
+    got = host(vedic.gemm_tn(a, b, out=dev(C0), beta=1.0))
+    check(got, o.TN, A, B, tol=FP16_TOL, beta=1.0, C0=C0, label="split-K accumulate")
+    c16 = dev(C0).half()
+    got = host(vedic.gemm(vedic.OP_TN, a, b, c16, alpha=2.0, beta=0.5, out_dtype=torch.float16))
+    check(got, o.TN, A, B, tol=FP16_TOL + 2.0 ** -10, alpha=2.0, beta=0.5, C0=o.f16_round(C0),
+          label="split-K f16 out")
+    buf = torch.full((M, N + 8), 5.0, dtype=torch.float32, device="cuda")
+    vedic.gemm(vedic.OP_TN, a, b, buf[:, :N])
+    assert np.all(host(buf)[:, N:] == 5.0)
