@@ -18,6 +18,7 @@ hipError_t launch_gemm_f16_direct_nn(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_nt(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_tn(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_skinny(const GemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_f32_skinny(const GemmArgs& a, hipStream_t s);
 }  // namespace vedic
 
 namespace vedic {
@@ -79,24 +80,32 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ ws, int S, GemmAr
     }
 }
 
-// Number of contraction slices for an fp16 product whose output is too
-// small to give every CU a tile: output tiles of 128 x 128 below half the CU
-// count and K of at least 2048.  1 = no split.
-static int choose_ksplit(int M, int N, int K, int cus) {
-    const int64_t big = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-    if (big >= cus) return 1;  // the 256 x 256 kernel fills the GPU
+// Number of contraction slices for a product whose output is too small to
+// give every CU a tile: 128 x 128 output tiles below half the CU count, and
+// slices of at least `min_slice` contraction steps (fp16: 1024, fp32: 128 --
+// an fp32 MFMA does an eighth of the work per cycle of an fp16 one, so a
+// slice carries the fixed prologue / epilogue cost in fewer steps).
+// 1 = no split.
+static int choose_ksplit(int M, int N, int K, int cus, bool f16) {
+    if (f16) {
+        const int64_t big = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+        if (big >= cus) return 1;  // the 256 x 256 kernel fills the GPU
+    }
+    const int min_slice = f16 ? 1024 : 128;
     const int64_t tiles = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
-    if (tiles * 2 > cus || K < 2048) return 1;
+    if (tiles * 2 > cus || K < 2 * min_slice) return 1;
     int s = (int)(cus / tiles);
     s = s < 8 ? s : 8;
-    s = s < K / 1024 ? s : K / 1024;
+    s = s < K / min_slice ? s : K / min_slice;
     return s >= 2 ? s : 1;
 }
 
 // Runs the product as `ks` slices into a stream-ordered workspace, then the
-// reduction with the caller's epilogue.
-static hipError_t launch_f16_split(int op, const GemmArgs& a, int ks, hipStream_t s) {
-    const int kslice = (((a.K + ks - 1) / ks) + 63) / 64 * 64;
+// reduction with the caller's epilogue.  Slices are whole contraction steps
+// of the kernel (64 fp16 or 32 fp32 values).
+static hipError_t launch_split(bool f16, int op, bool vec, const GemmArgs& a, int ks, hipStream_t s) {
+    const int step = f16 ? 64 : 32;
+    const int kslice = (((a.K + ks - 1) / ks) + step - 1) / step * step;
     ks = (a.K + kslice - 1) / kslice;
     const int64_t total = (int64_t)a.M * a.N;
     float* ws = nullptr;
@@ -115,9 +124,12 @@ static hipError_t launch_f16_split(int op, const GemmArgs& a, int ks, hipStream_
     p.ksplit = ks;
     p.kslice = kslice;
     p.c_split_stride = total;
-    e = op == VEDIC_OP_NN   ? launch_gemm_f16_direct_nn(p, s)
-        : op == VEDIC_OP_NT ? launch_gemm_f16_direct_nt(p, s)
-                            : launch_gemm_f16_direct_tn(p, s);
+    if (f16)
+        e = op == VEDIC_OP_NN   ? launch_gemm_f16_direct_nn(p, s)
+            : op == VEDIC_OP_NT ? launch_gemm_f16_direct_nt(p, s)
+                                : launch_gemm_f16_direct_tn(p, s);
+    else
+        e = launch_gemm_f32(op, vec, p, s);
     if (e == hipSuccess) {
         int64_t blocks = (total + 255) / 256;
         if (blocks > 8192) blocks = 8192;
@@ -193,9 +205,9 @@ extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
             // decode-time shapes: bound by streaming B once from HBM
             e = launch_gemm_f16_skinny(a, s);
         } else if (vec && d->lda < kMaxLd && d->ldb < kMaxLd) {
-            const int ks = choose_ksplit(d->M, d->N, d->K, device_cu_count());
+            const int ks = choose_ksplit(d->M, d->N, d->K, device_cu_count(), true);
             if (ks > 1)
-                e = launch_f16_split(d->op, a, ks, s);
+                e = launch_split(true, d->op, true, a, ks, s);
             else
                 e = d->op == VEDIC_OP_NN   ? launch_gemm_f16_direct_nn(a, s)
                     : d->op == VEDIC_OP_NT ? launch_gemm_f16_direct_nt(a, s)
@@ -203,8 +215,11 @@ extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
         } else {
             e = launch_gemm_f16_generic(d->op, a, s);
         }
+    } else if (vec && d->lda < kMaxLd && d->ldb < kMaxLd && d->op == VEDIC_OP_NN && d->M <= 32) {
+        e = launch_gemm_f32_skinny(a, s);
     } else {
-        e = launch_gemm_f32(d->op, vec, a, s);
+        const int ks = choose_ksplit(d->M, d->N, d->K, device_cu_count(), false);
+        e = ks > 1 ? launch_split(false, d->op, vec, a, ks, s) : launch_gemm_f32(d->op, vec, a, s);
     }
     return hip_status(e);
 }

@@ -161,13 +161,18 @@ struct Stager {
     }
 };
 
-// Maps the launch's linear workgroup id to an output tile (tm, tn).
-__device__ __forceinline__ void tile_coords(const GemmArgs& a, int& tm, int& tn) {
-    int nblk = a.tiles_m * a.tiles_n;
+// Maps the launch's linear workgroup id to an output tile (tm, tn) and a
+// contraction slice ks (split-K; 0 without a split).  Logical id L covers
+// tile L mod ntiles, slice L / ntiles.
+__device__ __forceinline__ void tile_coords(const GemmArgs& a, int& tm, int& tn, int& ks) {
+    const int ntiles = a.tiles_m * a.tiles_n;
+    const int nblk = gridDim.x;
     int bid = blockIdx.x;
     // Hardware deals workgroup ids to the 8 XCDs round-robin.  Re-number so
     // that XCD x owns logical ids [x * nblk/8, (x+1) * nblk/8).
     if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+    ks = bid / ntiles;
+    bid -= ks * ntiles;
     int gm = a.group_m;
     int per_group = gm * a.tiles_n;
     int g = bid / per_group;
@@ -264,9 +269,12 @@ gemm_mfma_kernel(GemmArgs args) {
     const int wave = tid >> 6;
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
-    int tm, tn;
-    tile_coords(args, tm, tn);
+    int tm, tn, ks;
+    tile_coords(args, tm, tn, ks);
     const int m0 = tm * BM, n0 = tn * BN;
+    // contraction range [kb, ke) of this workgroup's slice
+    const int kb = ks * args.kslice;
+    const int ke = min(args.K, kb + args.kslice);
 
     const T* __restrict__ A = static_cast<const T*>(args.A);
     const T* __restrict__ B = static_cast<const T*>(args.B);
@@ -280,10 +288,10 @@ gemm_mfma_kernel(GemmArgs args) {
 #pragma unroll
         for (int j = 0; j < NI; ++j) acc[i][j] = float16_t{};
 
-    const int nk = (args.K + BK - 1) / BK;
+    const int nk = (ke - kb + BK - 1) / BK;
 
-    sa.load(A, args.lda, m0, 0, args.M, args.K, tid);
-    sb.load(B, args.ldb, n0, 0, args.N, args.K, tid);
+    sa.load(A, args.lda, m0, kb, args.M, ke, tid);
+    sb.load(B, args.ldb, n0, kb, args.N, ke, tid);
     sa.store(smem, tid);
     sb.store(smem + BM * kRowBytes, tid);
     __syncthreads();
@@ -293,8 +301,8 @@ gemm_mfma_kernel(GemmArgs args) {
         char* nxt = smem + ((kt + 1) & 1) * STAGE;
         const bool more = kt + 1 < nk;
         if (more) {
-            sa.load(A, args.lda, m0, (kt + 1) * BK, args.M, args.K, tid);
-            sb.load(B, args.ldb, n0, (kt + 1) * BK, args.N, args.K, tid);
+            sa.load(A, args.lda, m0, kb + (kt + 1) * BK, args.M, ke, tid);
+            sb.load(B, args.ldb, n0, kb + (kt + 1) * BK, args.N, ke, tid);
         }
         Mfma<T>::template step<MI, NI>(cur, cur + BM * kRowBytes, wm * WM, wn * WN, lane, acc);
         if (more) {
@@ -305,11 +313,13 @@ gemm_mfma_kernel(GemmArgs args) {
     }
 
     const int row0 = m0 + wm * WM, col0 = n0 + wn * WN;
+    GemmArgs ea = args;
+    if (args.ksplit > 1) ea.C = static_cast<float*>(args.C) + ks * args.c_split_stride;
     const bool full = (row0 + WM <= args.M) && (col0 + WN <= args.N);
     if (KIND != EK_GENERIC && full)
-        epilogue<KIND, false, MI, NI>(args, acc, row0, col0, lane);
+        epilogue<KIND, false, MI, NI>(ea, acc, row0, col0, lane);
     else
-        epilogue<KIND, true, MI, NI>(args, acc, row0, col0, lane);
+        epilogue<KIND, true, MI, NI>(ea, acc, row0, col0, lane);
 }
 
 // ------------------------------------------------------------------ launch
@@ -320,7 +330,11 @@ static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
     if (a.group_m <= 0) a.group_m = 8;
-    const int nblk = a.tiles_m * a.tiles_n;
+    if (a.ksplit < 1) {
+        a.ksplit = 1;
+        a.kslice = a.K;
+    }
+    const int nblk = a.tiles_m * a.tiles_n * a.ksplit;
     constexpr int NT = (BM / WM) * (BN / WN) * 64;
     hipLaunchKernelGGL((gemm_mfma_kernel<T, OP, BM, BN, WM, WN, VEC, KIND>), dim3(nblk), dim3(NT), 0, s, a);
     return hipGetLastError();

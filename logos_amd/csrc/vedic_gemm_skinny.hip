@@ -2,112 +2,247 @@
 // the decode-time LM head (one to 32 new rows against a [K x N] weight).
 //
 // Such a product reads the weight once and does little arithmetic per byte,
-// so it is bound by HBM bandwidth, not by the matrix cores; the kernel is
+// so it is bound by HBM bandwidth, not by the matrix cores; the kernels are
 // built to keep as many weight bytes in flight as possible:
 //  * one workgroup per 32 output columns (256 workgroups for N = 8192), all
 //    M <= 32 rows in one 32 x 32 MFMA block (rows past M load as zeros);
-//  * the four waves split K into contiguous quarters; each wave issues every
-//    load of a round (four 64-deep stages of A and B, 32 KiB) at once into its
-//    own LDS region, then consumes the stages as they land.  A wave reads only
-//    what it loaded itself, so no barrier is needed until the end;
+//  * the four waves split K into contiguous quarters.  Each wave keeps four
+//    stages of A and B in flight in its own LDS region and refills a stage
+//    as soon as its MFMAs have read it.  A wave reads only what it loaded
+//    itself, so no barrier is needed until the end;
+//  * one LDS object per stage, indexed at compile time, so the compiler can
+//    tell which in-flight direct loads an LDS read depends on (with a single
+//    object, every read waits for every load);
 //  * the four partial 32 x 32 sums are added through LDS in a fixed order
 //    (wave 0 + 1 + 2 + 3), so the result does not depend on timing;
 //  * wave 0 applies the epilogue (alpha, beta, bias, GELU, pre-activation,
 //    fp16 output) shared with the tiled kernels.
-// Operands are fp16 (v_mfma_f32_32x32x16_f16) with the tiled kernels' LDS
-// layouts (A: K-contiguous swizzled rows; B: [k][32 columns] rows of 64 bytes
-// read with ds_read_b64_tr_b16, conflict free without a swizzle).
+//
+// fp16 (v_mfma_f32_32x32x16_f16): 64-deep stages with the tiled kernels' LDS
+// layouts (A: K-contiguous swizzled rows, one ds_read_b128 per operand; B:
+// [k][32 columns] rows of 64 bytes read with ds_read_b64_tr_b16, conflict free
+// without a swizzle).
+//
+// fp32 (v_mfma_f32_32x32x2_f32): 32-deep stages.
+//  * A: 32 rows x 32 k (128-byte rows, chunks swizzled as in the tiled
+//    kernels); lane (r, h) reads chunk 2c + h of row r with one ds_read_b128:
+//    four consecutive k, one for each of four MFMAs.
+//  * B: 32 k rows x 32 columns (128 bytes).  Rows are interleaved in groups
+//    of eight -- k row 8g + j sits at position 8g + 2j (j < 4) or
+//    8g + 2(j - 4) + 1 (j >= 4) -- so the two wave halves, which read k rows
+//    4 apart, read rows of opposite parity: consecutive 128-byte rows fall in
+//    opposite halves of the 64 banks, and a 64-lane ds_read_b32 is conflict
+//    free.
 #include "vedic_gemm_f16.hpp"
 
 namespace vedic {
 
-constexpr int kSkStages = 4;  // 64-deep stages per wave per round
-constexpr int kSkBK = 64;
+constexpr int kSkStages = 4;     // stages in flight per wave
+constexpr int kSkStage = 8192;   // bytes per stage per wave: 4 KiB of A + 4 KiB of B
 
-template <int KIND>
-__global__ void __launch_bounds__(256) gemm_f16_skinny_kernel(GemmArgs a) {
-    using SA = Side<true, 32, kSkBK, 1>;   // A: 32 rows x 64 k, 4 KiB, 4 loads
-    using SB = Side<false, 32, kSkBK, 1>;  // B: 64 k x 32 columns, 4 KiB, 4 loads
-    constexpr int L = SA::NLD + SB::NLD;
-    constexpr int STAGE = SA::BYTES + SB::BYTES;
-    __shared__ __attribute__((aligned(1024))) char lds[4 * kSkStages * STAGE];  // 128 KiB
+// fp16 operands, 64-deep stages.  Direct loads without branches: each lane
+// keeps its byte offset and the first contraction index of its chunk, and an
+// out-of-range chunk takes the out-of-range offset.
+struct SkinnyF16 {
+    static constexpr int BK = 64;
+    static constexpr int L = 8;  // direct-load instructions per stage per wave
+    static constexpr bool kUniformRounds = false;
+    using T = _Float16;
+    uint32_t aoff[4], boff[4];
+    int ak[4], bk[4];
+    __device__ __forceinline__ void init(const GemmArgs& a, int n0, int lane) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // A: 32 rows x 8 chunks of 8 k (KC layout, rows of 128 bytes)
+            const int q = i * 64 + lane;
+            const int row = q >> 3;
+            const int c = (q & 7) ^ swz_kc<8>(row);
+            aoff[i] = row < a.M ? (uint32_t)(row * a.lda * 2 + c * 16) : kOob;
+            ak[i] = 8 * c;
+            // B: 64 k rows x 4 chunks of 8 columns (MC layout, rows of 64 bytes)
+            const int k = q >> 2, cb = q & 3;
+            const int col = n0 + 8 * cb;
+            boff[i] = col + 8 <= a.N ? (uint32_t)((int64_t)k * a.ldb * 2 + col * 2) : kOob;
+            bk[i] = k;
+        }
+    }
+    // k0 < K; krem = contraction values left in the wave's range (<= 0: none)
+    __device__ __forceinline__ void issue(const GemmArgs& a, int k0, int krem, char* dst) const {
+        const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(static_cast<const T*>(a.A) + k0);
+        const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(static_cast<const T*>(a.B) + (int64_t)k0 * a.ldb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(dst + i * 1024), 16,
+                                                     ak[i] + 8 <= krem ? aoff[i] : kOob, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(dst + 4096 + i * 1024), 16,
+                                                     bk[i] < krem ? boff[i] : kOob, 0, 0, 0);
+    }
+    __device__ __forceinline__ static void consume(const char* la, int lane, float16_t& acc) {
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; ++kk) {
+            const half8_t af = read_frag<true, 32, BK>(la, 0, kk, lane);
+            const half8_t bf = read_frag<false, 32, BK>(la + 4096, 0, kk, lane);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc, 0, 0, 0);
+        }
+    }
+};
+
+// fp32 operands, 32-deep stages.
+struct SkinnyF32 {
+    static constexpr int BK = 32;
+    static constexpr int L = 8;
+    static constexpr bool kUniformRounds = true;
+    using T = float;
+    // Instruction i of a side fills bytes [1024 i, 1024 (i + 1)) of the
+    // side's 4 KiB; lane q lands at +16 q.
+    uint32_t aoff[4], boff[4];
+    int ak[4], bk[4];
+    __device__ __forceinline__ void init(const GemmArgs& a, int n0, int lane) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 8 * i + (lane >> 3);
+            const int c = (lane & 7) ^ swz_kc<8>(row);
+            aoff[i] = row < a.M ? (uint32_t)(row * a.lda * 4 + c * 16) : kOob;
+            ak[i] = 4 * c;
+            const int j = lane >> 3;  // LDS row 8 i + j holds k row 8 i + (j odd ? 4 + j/2 : j/2)
+            const int k = 8 * i + ((j & 1) ? 4 + (j >> 1) : (j >> 1));
+            const int col = n0 + 4 * (lane & 7);
+            boff[i] = col + 4 <= a.N ? (uint32_t)((int64_t)k * a.ldb * 4 + col * 4) : kOob;
+            bk[i] = k;
+        }
+    }
+    __device__ __forceinline__ void issue(const GemmArgs& a, int k0, int krem, char* dst) const {
+        const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(static_cast<const T*>(a.A) + k0);
+        const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(static_cast<const T*>(a.B) + (int64_t)k0 * a.ldb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(dst + i * 1024), 16,
+                                                     ak[i] + 4 <= krem ? aoff[i] : kOob, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(dst + 4096 + i * 1024), 16,
+                                                     bk[i] < krem ? boff[i] : kOob, 0, 0, 0);
+    }
+    __device__ __forceinline__ static void consume(const char* la, int lane, float16_t& acc) {
+        const int l32 = lane & 31, h = lane >> 5;
+        const char* lb = la + 4096;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            const float4_t av =
+                *reinterpret_cast<const float4_t*>(la + l32 * 128 + (((2 * cc + h) ^ swz_kc<8>(l32)) << 4));
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                // k = 8 cc + 4 h + s sits at LDS row 8 cc + 2 s + h
+                const float bv = *reinterpret_cast<const float*>(lb + (8 * cc + 2 * s + h) * 128 + l32 * 4);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s], bv, acc, 0, 0, 0);
+            }
+        }
+    }
+};
+
+template <class Sk, int KIND>
+__global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs a) {
+    constexpr int BK = Sk::BK, ST = kSkStages, STAGE = kSkStage, L = Sk::L;
+    __shared__ __attribute__((aligned(1024))) char s0[4 * STAGE];
+    __shared__ __attribute__((aligned(1024))) char s1[4 * STAGE];
+    __shared__ __attribute__((aligned(1024))) char s2[4 * STAGE];
+    __shared__ __attribute__((aligned(1024))) char s3[4 * STAGE];
+    char* const Ss[ST] = {s0, s1, s2, s3};
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int n0 = blockIdx.x * 32;
     const int K = a.K;
-    // contiguous K quarter of this wave, a multiple of 64
-    const int kq = ((K + 4 * kSkBK - 1) / (4 * kSkBK)) * kSkBK;
+    // contiguous K quarter of this wave, whole stages
+    const int kq = ((K + 4 * BK - 1) / (4 * BK)) * BK;
     const int kb = min(K, wave * kq), ke = min(K, kb + kq);
-    char* const mine = lds + wave * kSkStages * STAGE;
+    // rounds of ST stages (at least one, so every wave has the same shape;
+    // stages past the range load zeros without touching memory)
+    const int nround = max(1, (ke - kb + ST * BK - 1) / (ST * BK));
 
-    const _Float16* __restrict__ A = static_cast<const _Float16*>(a.A);
-    const _Float16* __restrict__ B = static_cast<const _Float16*>(a.B);
-    SA sa;
-    SB sb;
-    sa.init(0, lane, a.lda, 0, a.M);
-    sb.init(0, lane, a.ldb, n0, a.N);
+    Sk sk;
+    sk.init(a, n0, lane);
+    auto issue = [&](int st, char* buf) {
+        const int k0 = kb + st * BK;
+        sk.issue(a, k0 < K ? k0 : 0, ke - k0, buf + wave * STAGE);
+    };
 
-    float16_t acc[1][1];
-    acc[0][0] = float16_t{};
-    for (int kr = kb; kr < ke; kr += kSkStages * kSkBK) {
+    float16_t acc = float16_t{};
 #pragma unroll
-        for (int s = 0; s < kSkStages; ++s) {
-            // stages past this wave's range load nothing (krem <= 0: every chunk out of range)
-            const int k = kr + s * kSkBK;
-            const int kc = k < K ? k : 0;
-            sa.load(A + kc, mine + s * STAGE, 0, lane, ke - k);
-            sb.load(B + (int64_t)kc * a.ldb + n0, mine + s * STAGE + SA::BYTES, 0, lane, ke - k);
+    for (int st = 0; st < ST; ++st) issue(st, Ss[st]);
+    // Every round but the last refills each stage after reading it.  The
+    // last round either drains (waits 3L, 2L, L, 0) or, for operand types
+    // with kUniformRounds, refills too, with out-of-range zero loads that
+    // touch no memory.  Both forms give every LDS read a wait for its own
+    // stage only, as long as the compiler can follow which stage each load
+    // and read belongs to; with the fp32 B reads (pairs merged into
+    // ds_read2st64_b32) it follows the uniform form, with the fp16 transpose
+    // reads the drain, which saves the zero loads.
+    const int nfill = Sk::kUniformRounds ? nround : nround - 1;
+    for (int r = 0; r < nfill; ++r) {
+#pragma unroll
+        for (int sb = 0; sb < ST; ++sb) {
+            wait_vmcnt<(ST - 1) * L>();  // this stage has landed; ST - 1 later stages in flight
+            Sk::consume(Ss[sb] + wave * STAGE, lane, acc);
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the stage's reads are done
+            issue((r + 1) * ST + sb, Ss[sb]);
         }
+    }
+    if constexpr (Sk::kUniformRounds) {
+        wait_vmcnt<0>();  // the trailing zero loads still write LDS
+    } else {
 #pragma unroll
-        for (int s = 0; s < kSkStages; ++s) {
-            if (s == 0) wait_vmcnt<3 * L>();
-            else if (s == 1) wait_vmcnt<2 * L>();
-            else if (s == 2) wait_vmcnt<L>();
+        for (int sb = 0; sb < ST; ++sb) {
+            if (sb == 0) wait_vmcnt<3 * L>();
+            else if (sb == 1) wait_vmcnt<2 * L>();
+            else if (sb == 2) wait_vmcnt<L>();
             else wait_vmcnt<0>();
-            const char* la = mine + s * STAGE;
-            const char* lb = la + SA::BYTES;
-#pragma unroll
-            for (int kk = 0; kk < kSkBK / 16; ++kk) {
-                const half8_t af = read_frag<true, 32, kSkBK>(la, 0, kk, lane);
-                const half8_t bf = read_frag<false, 32, kSkBK>(lb, 0, kk, lane);
-                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc[0][0], 0, 0, 0);
-            }
+            Sk::consume(Ss[sb] + wave * STAGE, lane, acc);
         }
-        // the next round overwrites these stages: all reads must have returned
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     }
 
     // fixed-order reduction of the four partial sums through LDS
     __syncthreads();
-    float* red = reinterpret_cast<float*>(lds);
+    float* red = reinterpret_cast<float*>(s0);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) red[(wave * 16 + e) * 64 + lane] = acc[0][0][e];
+    for (int e = 0; e < 16; ++e) red[(wave * 16 + e) * 64 + lane] = acc[e];
     __syncthreads();
     if (wave != 0) return;
+    float16_t sum[1][1];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
         float v = red[e * 64 + lane];
         v += red[(16 + e) * 64 + lane];
         v += red[(32 + e) * 64 + lane];
         v += red[(48 + e) * 64 + lane];
-        acc[0][0][e] = v;
+        sum[0][0][e] = v;
     }
-    epilogue<KIND, true, 1, 1>(a, acc, 0, n0, lane);
+    epilogue<KIND, true, 1, 1>(a, sum, 0, n0, lane);
 }
 
-template __global__ void gemm_f16_skinny_kernel<EK_PLAIN>(GemmArgs);
-template __global__ void gemm_f16_skinny_kernel<EK_GENERIC>(GemmArgs);
+template __global__ void gemm_skinny_kernel<SkinnyF16, EK_PLAIN>(GemmArgs);
+template __global__ void gemm_skinny_kernel<SkinnyF16, EK_GENERIC>(GemmArgs);
+template __global__ void gemm_skinny_kernel<SkinnyF32, EK_PLAIN>(GemmArgs);
+template __global__ void gemm_skinny_kernel<SkinnyF32, EK_GENERIC>(GemmArgs);
 
-// fp16: A, B 16-byte aligned, lda / ldb multiples of 8, N a multiple of 8
-// (checked by the caller); M <= 32, op NN.
-hipError_t launch_gemm_f16_skinny(const GemmArgs& a, hipStream_t s) {
+template <class Sk>
+static hipError_t launch_skinny(const GemmArgs& a, hipStream_t s) {
     const dim3 grid((a.N + 31) / 32);
     if (a.epi_kind == EK_PLAIN)
-        hipLaunchKernelGGL(gemm_f16_skinny_kernel<EK_PLAIN>, grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((gemm_skinny_kernel<Sk, EK_PLAIN>), grid, dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL(gemm_f16_skinny_kernel<EK_GENERIC>, grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((gemm_skinny_kernel<Sk, EK_GENERIC>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
+
+// fp16: A, B 16-byte aligned, lda / ldb multiples of 8 and < 2^22, N a
+// multiple of 8 (checked by the caller); M <= 32, op NN.
+hipError_t launch_gemm_f16_skinny(const GemmArgs& a, hipStream_t s) { return launch_skinny<SkinnyF16>(a, s); }
+
+// fp32: A, B 16-byte aligned, lda / ldb multiples of 4 and < 2^22, N a
+// multiple of 4 (checked by the caller); M <= 32, op NN.
+hipError_t launch_gemm_f32_skinny(const GemmArgs& a, hipStream_t s) { return launch_skinny<SkinnyF32>(a, s); }
 
 }  // namespace vedic

@@ -345,3 +345,77 @@ def test_split_k_epilogues():
     buf = torch.full((M, N + 8), 5.0, dtype=torch.float32, device="cuda")
     vedic.gemm(vedic.OP_TN, a, b, buf[:, :N])
     assert np.all(host(buf)[:, N:] == 5.0)
+
+
+# ------------------------------------------------------- fp32 skinny and split-K
+
+@pytest.mark.parametrize("M", [1, 3, 16, 32])
+@pytest.mark.parametrize("K,N", [(32, 4), (100, 36), (1000, 264), (1024, 8192), (2052, 132)])
+def test_skinny_m_fp32(M, K, N):
+    """M <= 32 strict-fp32 NN products take the fp32 decode kernel: partial
+    32-deep stages, quarters past K, several rounds, column edges."""
+    vedic = V()
+    rng = np.random.default_rng(zlib.crc32(f"skinny32-{M}-{K}-{N}".encode()))
+    A, B = normal(rng, (M, K)), normal(rng, (K, N), std=0.05)
+    got = host(vedic.gemm(vedic.OP_NN, dev(A), dev(B)))
+    check(got, o.NN, A, B, tol=fp32_tol(K), label=f"skinny fp32 {M}x{K}x{N}")
+    ref = restated(o.NN, A, B)
+    assert o.inf_rel_err(got, ref) <= 2 * fp32_tol(K)
+
+
+def test_skinny_m_fp32_epilogues():
+    vedic = V()
+    rng = np.random.default_rng(29)
+    M, K, N = 5, 776, 140
+    A, B = normal(rng, (M, K)), normal(rng, (K, N), std=0.05)
+    bias, C0 = normal(rng, (N,), std=0.1), normal(rng, (M, N))
+    tol = fp32_tol(K)
+    pre = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    got = host(vedic.gemm(vedic.OP_NN, dev(A), dev(B), bias=dev(bias), epilogue=vedic.EPI_BIAS_GELU, preact=pre))
+    check(got, o.NN, A, B, tol=tol, bias=bias, gelu=True, label="skinny fp32 bias+gelu")
+    check(host(pre), o.NN, A, B, tol=tol, bias=bias, label="skinny fp32 preact")
+    got = host(vedic.gemm(vedic.OP_NN, dev(A), dev(B), dev(C0), alpha=-1.5, beta=0.25))
+    check(got, o.NN, A, B, tol=tol, alpha=-1.5, beta=0.25, C0=C0, label="skinny fp32 alpha/beta")
+    buf = torch.full((M, N + 4), 7.0, dtype=torch.float32, device="cuda")
+    vedic.gemm(vedic.OP_NN, dev(A), dev(B), buf[:, :N])
+    assert np.all(host(buf)[:, N:] == 7.0)
+    assert np.array_equal(host(buf)[:, :N], host(vedic.gemm(vedic.OP_NN, dev(A), dev(B))))
+
+
+@pytest.mark.parametrize("opname", list(OPS))
+@pytest.mark.parametrize("shape", [(512, 1024, 1024), (100, 200, 3000), (136, 264, 2112)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_split_k_fp32(opname, shape):
+    """Strict-fp32 products with few output tiles are split over K (slices of
+    at least 128) and reduced in a fixed order: within the fp32 bound of the
+    oracle and bit-identical run to run."""
+    vedic = V()
+    layout = OPS[opname]
+    M, N, K = shape
+    rng = np.random.default_rng(zlib.crc32(f"splitk32-{opname}-{shape}".encode()))
+    A, B = _operands(rng, layout, M, N, K)
+    a, b = dev(A), dev(B)
+    got = host(vedic.gemm(layout, a, b))
+    check(got, layout, A, B, tol=fp32_tol(K), label=f"split-K fp32 {opname} {shape}")
+    assert o.inf_rel_err(got, restated(layout, A, B)) <= 2 * fp32_tol(K)
+    assert np.array_equal(host(vedic.gemm(layout, a, b)), got)
+
+
+def test_split_k_fp32_epilogues():
+    vedic = V()
+    rng = np.random.default_rng(31)
+    M, N, K = 200, 136, 1500
+    A, B = normal(rng, (M, K)), normal(rng, (K, N), std=0.05)
+    bias, C0 = normal(rng, (N,), std=0.1), normal(rng, (M, N))
+    tol = fp32_tol(K)
+    pre = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    got = host(vedic.gemm(vedic.OP_NN, dev(A), dev(B), bias=dev(bias), epilogue=vedic.EPI_BIAS_GELU, preact=pre))
+    check(got, o.NN, A, B, tol=tol, bias=bias, gelu=True, label="split-K fp32 bias+gelu")
+    check(host(pre), o.NN, A, B, tol=tol, bias=bias, label="split-K fp32 preact")
+    got = host(vedic.gemm(vedic.OP_NN, dev(A), dev(B), dev(C0), alpha=0.75, beta=-2.0))
+    check(got, o.NN, A, B, tol=tol, alpha=0.75, beta=-2.0, C0=C0, label="split-K fp32 alpha/beta")
+    # unaligned leading dimension: the element-wise load path, also split
+    Apad = np.zeros((M, K + 1), np.float32)
+    Apad[:, :K] = A
+    got = host(vedic.gemm(vedic.OP_NN, dev(Apad)[:, :K], dev(B)))
+    check(got, o.NN, A, B, tol=tol, label="split-K fp32 unaligned")
