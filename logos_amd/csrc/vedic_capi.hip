@@ -19,6 +19,9 @@ hipError_t launch_gemm_f16_direct_nt(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_tn(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_skinny(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f32_skinny(const GemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_f32_direct_nn(const GemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_f32_direct_nt(const GemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_f32_direct_tn(const GemmArgs& a, hipStream_t s);
 }  // namespace vedic
 
 namespace vedic {
@@ -80,6 +83,16 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ ws, int S, GemmAr
     }
 }
 
+// fp32 tiles: the direct-load pipelined kernel where the operands allow
+// 16-byte loads and 32-bit tile offsets, else the element-wise kernel.
+static hipError_t launch_f32_tiled(int op, bool vec, const GemmArgs& a, hipStream_t s) {
+    if (vec && a.lda < kMaxLd && a.ldb < kMaxLd)
+        return op == VEDIC_OP_NN   ? launch_gemm_f32_direct_nn(a, s)
+               : op == VEDIC_OP_NT ? launch_gemm_f32_direct_nt(a, s)
+                                   : launch_gemm_f32_direct_tn(a, s);
+    return launch_gemm_f32(op, vec, a, s);
+}
+
 // Number of contraction slices for a product whose output is too small to
 // give every CU a tile: 128 x 128 output tiles below half the CU count, and
 // slices of at least `min_slice` contraction steps (fp16: 1024, fp32: 128 --
@@ -129,7 +142,7 @@ static hipError_t launch_split(bool f16, int op, bool vec, const GemmArgs& a, in
             : op == VEDIC_OP_NT ? launch_gemm_f16_direct_nt(p, s)
                                 : launch_gemm_f16_direct_tn(p, s);
     else
-        e = launch_gemm_f32(op, vec, p, s);
+        e = launch_f32_tiled(op, vec, p, s);
     if (e == hipSuccess) {
         int64_t blocks = (total + 255) / 256;
         if (blocks > 8192) blocks = 8192;
@@ -219,7 +232,7 @@ extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
         e = launch_gemm_f32_skinny(a, s);
     } else {
         const int ks = choose_ksplit(d->M, d->N, d->K, device_cu_count(), false);
-        e = ks > 1 ? launch_split(false, d->op, vec, a, ks, s) : launch_gemm_f32(d->op, vec, a, s);
+        e = ks > 1 ? launch_split(false, d->op, vec, a, ks, s) : launch_f32_tiled(d->op, vec, a, s);
     }
     return hip_status(e);
 }

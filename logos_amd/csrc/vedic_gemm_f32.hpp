@@ -1,0 +1,306 @@
+// vedic_gemm_f32.hpp -- the strict-fp32 GEMM for gfx950 (v_mfma_f32_32x32x2_f32).
+//
+//   C[M x N] = epi(op(A) . op(B)), A, B and C binary32, op NN / NT / TN as in
+//   the fp16 kernel (vedic_gemm_f16.hpp), whose organisation this follows:
+//   persistent XCD-aware tiles, split-K work items, direct global -> LDS
+//   loads with out-of-range zero fill, explicit per-stage vmcnt waits and
+//   fence-free barriers, the next tile's first stages in flight during the
+//   epilogue.
+//
+// An fp32 MFMA does an eighth of the work of an fp16 one per cycle (4096
+// flops in 64 cycles), so per byte loaded there is 16x more matrix-core time:
+// the tile is 128 x 128 with four waves of 64 x 64, and the pipeline is about
+// latency, not bandwidth -- the next 32-deep stage (32 KiB) is in flight while
+// one is consumed, and a second resident workgroup covers the rest.
+//
+// LDS layouts (32 k per stage):
+//  * KC (contraction contiguous in memory: A in NN/NT, B in NT): one 128-byte
+//    row of 32 k per output row/column, 16-byte chunks XOR-swizzled with the
+//    fp16 kernel's swz_kc<8>.  Lane (r, h) reads chunk 2c + h of row r with one
+//    ds_read_b128: four consecutive k, one for each of four MFMAs.
+//  * MC (M or N contiguous: B in NN, A and B in TN): the natural [k][mn] rows
+//    (512 bytes for 128 columns).  The MFMA operand is one fp32 per lane per
+//    k, read with ds_read_b32: the 32 lanes of a half wave read 128
+//    consecutive bytes of row k, the other half row k + 4.  Rows are 512 bytes
+//    (a multiple of the 256-byte bank window), so the 16-byte slots of rows
+//    with bit 2 of k set are XOR 8 (moved by 128 bytes): the two halves then
+//    read opposite halves of the 64 banks, conflict free.
+// Each 32-k stage is consumed as four chunks cc of 8 k: for every MFMA s
+// (0..3) of chunk cc, lane half h contributes k = 8 cc + 4 h + s, on both
+// operands, so every k of the chunk is summed exactly once.
+#pragma once
+
+#include "vedic_gemm_f16.hpp"
+
+namespace vedic {
+
+__device__ __forceinline__ int swz_mc32(int k) { return ((k >> 2) & 1) << 3; }
+
+// One operand side of the fp32 tile: R rows (BM or BN) of the output, 32 deep.
+template <bool KC, int R, int NW>
+struct SideF32 {
+    static constexpr int BK = 32;
+    static constexpr int BYTES = R * BK * 4;
+    static constexpr int NINS = BYTES / 1024;  // 1 KiB direct-load instructions per stage
+    static constexpr int NLD = NINS / NW;      // per wave
+    static_assert(NINS % NW == 0, "stage loads do not divide among the waves");
+    static constexpr int CPR = KC ? 8 : R / 4;  // 16-byte chunks per LDS row
+    static_assert(KC || CPR >= 16, "MC rows of at least 64 columns");
+    uint32_t off[NLD];  // per-lane byte offset from the tile base; kOob outside the matrix
+    int kend[NLD];      // the chunk is inside the contraction range iff kend <= K - k0
+
+    __device__ __forceinline__ static void geom(int wave, int lane, int i, int& row, int& c) {
+        const int q = (wave * NLD + i) * 64 + lane;
+        row = q / CPR;
+        const int p = q % CPR;
+        c = KC ? (p ^ swz_kc<8>(row)) : (p ^ swz_mc32(row));
+    }
+    __device__ __forceinline__ void init(int wave, int lane, int64_t ld, int mn0, int MN) {
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            int row, c;
+            geom(wave, lane, i, row, c);
+            const bool ok = KC ? (mn0 + row < MN) : (mn0 + 4 * c + 4 <= MN);
+            off[i] = ok ? (uint32_t)((int64_t)row * ld * 4 + c * 16) : kOob;
+            kend[i] = KC ? 4 * c + 4 : row + 1;
+        }
+    }
+    // `tile` points at element (mn0, k0) (KC) or (k0, mn0) (MC); krem = K - k0
+    // (<= 0 past the range: zeros, no memory touched).  Branch free, so every
+    // stage's loads have the same shape.
+    __device__ __forceinline__ void load(const float* tile, char* lds, int wave, int lane, int krem) const {
+        const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(tile);
+#pragma unroll
+        for (int i = 0; i < NLD; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds + (wave * NLD + i) * 1024), 16,
+                                                     kend[i] <= krem ? off[i] : kOob, 0, 0, 0);
+    }
+};
+
+// Operand values of chunk cc for row/column rc0 + lane % 32: element s is
+// contraction index 8 cc + 4 (lane / 32) + s.
+template <bool KC, int R>
+__device__ __forceinline__ float4_t read_frag32(const char* lds, int rc0, int cc, int lane) {
+    const int l32 = lane & 31, h = lane >> 5;
+    if constexpr (KC) {
+        const int row = rc0 + l32;
+        return *reinterpret_cast<const float4_t*>(lds + row * 128 + (((2 * cc + h) ^ swz_kc<8>(row)) << 4));
+    } else {
+        const int mn = rc0 + l32;
+        float4_t v;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int k = 8 * cc + 4 * h + s;
+            int off = k * (R * 4) + (((mn >> 2) ^ swz_mc32(k)) << 4) + (mn & 3) * 4;
+            // Keep the four reads separate: pairs merged into ds_read2st64_b32
+            // lose the information that they read only this stage, and every
+            // such read would wait for all direct loads in flight.
+            asm volatile("" : "+v"(off));
+            v[s] = *reinterpret_cast<const float*>(lds + off);
+        }
+        return v;
+    }
+}
+
+// The MFMAs of one 32-k stage, fragments double buffered across the four
+// chunks (reads of chunk cc + 1 interleaved with the MFMAs of chunk cc).
+template <bool A_KC, bool B_KC, int BM, int BN, int MI, int NI>
+__device__ __forceinline__ void mfma_stage32(const char* la, const char* lb, int ar0, int bc0, int lane,
+                                             float16_t (&acc)[MI][NI]) {
+    constexpr int NR = (A_KC ? MI : 4 * MI) + (B_KC ? NI : 4 * NI);  // LDS reads per chunk
+    constexpr int NM = 4 * MI * NI;                                  // MFMAs per chunk
+    float4_t af[2][MI], bf[2][NI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i) af[0][i] = read_frag32<A_KC, BM>(la, ar0 + 32 * i, 0, lane);
+#pragma unroll
+    for (int j = 0; j < NI; ++j) bf[0][j] = read_frag32<B_KC, BN>(lb, bc0 + 32 * j, 0, lane);
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+        const int c = cc & 1, n = c ^ 1;
+        if (cc + 1 < 4) {
+#pragma unroll
+            for (int i = 0; i < MI; ++i) af[n][i] = read_frag32<A_KC, BM>(la, ar0 + 32 * i, cc + 1, lane);
+#pragma unroll
+            for (int j = 0; j < NI; ++j) bf[n][j] = read_frag32<B_KC, BN>(lb, bc0 + 32 * j, cc + 1, lane);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NI; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[c][i][s], bf[c][j][s], acc[i][j], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+#pragma unroll
+    for (int cc = 0; cc + 1 < 4; ++cc) {
+#pragma unroll
+        for (int x = 0; x < (NR < NM ? NR : NM); ++x) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if (NR > NM) __builtin_amdgcn_sched_group_barrier(0x100, NR > NM ? NR - NM : 1, 0);
+        if (NM > NR) __builtin_amdgcn_sched_group_barrier(0x008, NM > NR ? NM - NR : 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+}
+
+#define VEDIC_A_TILE32(k) \
+    (A_KC ? A + (int64_t)m0 * args.lda + ((k) < K ? (k) : 0) : A + (int64_t)((k) < K ? (k) : 0) * args.lda + m0)
+#define VEDIC_B_TILE32(k) \
+    (B_KC ? B + (int64_t)n0 * args.ldb + ((k) < K ? (k) : 0) : B + (int64_t)((k) < K ? (k) : 0) * args.ldb + n0)
+#define VEDIC_ISSUE32(kt, la, lb)                                                        \
+    do {                                                                                 \
+        const int k_ = it.kb + (kt) * BK;                                                \
+        sa.load(VEDIC_A_TILE32(k_), (la), wave, lane, it.ke - k_);                       \
+        sb.load(VEDIC_B_TILE32(k_), (lb), wave, lane, it.ke - k_);                       \
+    } while (0)
+
+template <int OP, int BM, int BN, int ST, int WGM, int WGN, int KIND>
+__global__ void __launch_bounds__(WGM* WGN * 64) gemm_f32_kernel(GemmArgs args) {
+    constexpr int BK = 32;
+    constexpr int NW = WGM * WGN, WM = BM / WGM, WN = BN / WGN, MI = WM / 32, NI = WN / 32;
+    constexpr bool A_KC = OP != 2, B_KC = OP == 1;
+    using SA = SideF32<A_KC, BM, NW>;
+    using SB = SideF32<B_KC, BN, NW>;
+    constexpr int L = SA::NLD + SB::NLD;  // load instructions per wave per stage
+    static_assert(ST >= 2 && ST <= 4, "2 to 4 LDS stages");
+    static_assert((ST - 2) * L < 64, "vmcnt range");
+
+    // One LDS object per stage (A then B): reads of one stage provably do not
+    // alias the direct loads into another.  The compiler follows only a few
+    // distinct direct-load targets; one object per operand and stage (eight
+    // at ST = 4) is past that, and every read would then wait for every load.
+    constexpr int SBYTES = SA::BYTES + SB::BYTES;
+    __shared__ __attribute__((aligned(1024))) char t0[SBYTES];
+    __shared__ __attribute__((aligned(1024))) char t1[SBYTES];
+    __shared__ __attribute__((aligned(1024))) char t2[ST > 2 ? SBYTES : 16];
+    __shared__ __attribute__((aligned(1024))) char t3[ST > 3 ? SBYTES : 16];
+    char* const As[4] = {t0, t1, t2, t3};
+    char* const Bs[4] = {t0 + SA::BYTES, t1 + SA::BYTES, t2 + SA::BYTES, t3 + SA::BYTES};
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const float* __restrict__ A = static_cast<const float*>(args.A);
+    const float* __restrict__ B = static_cast<const float*>(args.B);
+    const int K = args.K;
+    const int G = gridDim.x;
+    const int b = blockIdx.x;
+    const int base = (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
+    const int ntiles = args.tiles_m * args.tiles_n;
+    const int nwork = ntiles * args.ksplit;
+
+    int w = base;
+    if (w >= nwork) return;
+    WorkItem it = work_of<BM, BN, BK>(args, w, ntiles);
+    int m0 = it.m0, n0 = it.n0;
+    SA sa;
+    SB sb;
+    sa.init(wave, lane, args.lda, m0, args.M);
+    sb.init(wave, lane, args.ldb, n0, args.N);
+#pragma unroll
+    for (int s = 0; s < ST - 1; ++s) VEDIC_ISSUE32(s, As[s], Bs[s]);
+
+    while (true) {
+        float16_t acc[MI][NI];
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NI; ++j) acc[i][j] = float16_t{};
+
+        // Uniform pipeline: every stage step waits for the same number of
+        // loads and issues stage kt + ST - 1, which past the work item's
+        // range loads zeros without touching memory; only the MFMAs are
+        // skipped for such stages.  Every step then has the same shape, so
+        // the compiler can tell that a read of stage kt depends only on
+        // stage kt's loads (with steps of different shapes it falls back to
+        // waiting for every load in flight).
+        const int nk = it.nk;
+        for (int k0 = 0; k0 < nk; k0 += ST) {
+#pragma unroll
+            for (int s = 0; s < ST; ++s) {
+                const int kt = k0 + s;
+                wait_vmcnt<(ST - 2) * L>();  // stage kt has landed; ST - 2 later stages in flight
+                stage_barrier();
+                const int sl = (s + ST - 1) % ST;
+                VEDIC_ISSUE32(kt + ST - 1, As[sl], Bs[sl]);
+                if (kt < nk) mfma_stage32<A_KC, B_KC, BM, BN, MI, NI>(As[s], Bs[s], wm * WM, wn * WN, lane, acc);
+            }
+        }
+
+        const int row0 = m0 + wm * WM, col0 = n0 + wn * WN;
+        GemmArgs ea = args;
+        if (args.ksplit > 1) ea.C = static_cast<float*>(args.C) + it.s * args.c_split_stride;
+        w += G;
+        const bool more = w < nwork;
+        if (more) {
+            __syncthreads();  // every wave is done reading the stage buffers
+            it = work_of<BM, BN, BK>(args, w, ntiles);
+            m0 = it.m0;
+            n0 = it.n0;
+            sa.init(wave, lane, args.lda, m0, args.M);
+            sb.init(wave, lane, args.ldb, n0, args.N);
+#pragma unroll
+            for (int s = 0; s < ST - 1; ++s) VEDIC_ISSUE32(s, As[s], Bs[s]);
+        }
+        const bool full = (row0 + WM <= args.M) && (col0 + WN <= args.N);
+        if (KIND != EK_GENERIC && full)
+            epilogue<KIND, false, MI, NI>(ea, acc, row0, col0, lane);
+        else
+            epilogue<KIND, true, MI, NI>(ea, acc, row0, col0, lane);
+        if (!more) break;
+    }
+    wait_vmcnt<0>();  // the trailing zero loads still write LDS
+}
+
+#undef VEDIC_ISSUE32
+#undef VEDIC_A_TILE32
+#undef VEDIC_B_TILE32
+
+// 128 x 128 tiles, four waves of 64 x 64, ST stages of 32 KiB.  Two stages
+// leave room for two workgroups per CU (2 x 64 KiB of LDS), and two
+// workgroups -- two waves per SIMD -- keep the matrix pipe busier than deeper
+// pipelines with one (measured on the 8192 x 8192 x 1024 LM head: 86 % of the
+// fp32 MFMA peak at ST = 2, 74 % at ST = 4).
+#ifndef VEDIC_F32_STAGES
+#define VEDIC_F32_STAGES 2
+#endif
+struct CfgF32 {
+    static constexpr int BM = 128, BN = 128, ST = VEDIC_F32_STAGES, WGM = 2, WGN = 2;
+    static constexpr int PER_CU = ST <= 2 ? 2 : 1;  // resident workgroups per CU (LDS: ST x 32 KiB)
+};
+
+template <int OP, int KIND>
+static hipError_t launch_f32(GemmArgs a, hipStream_t s) {
+    using Cfg = CfgF32;
+    a.tiles_m = (a.M + Cfg::BM - 1) / Cfg::BM;
+    a.tiles_n = (a.N + Cfg::BN - 1) / Cfg::BN;
+    if (a.group_m <= 0) a.group_m = 8;
+    if (a.ksplit < 1) {
+        a.ksplit = 1;
+        a.kslice = a.K;
+    }
+    const int64_t nwork = (int64_t)a.tiles_m * a.tiles_n * a.ksplit;
+    const int64_t slots = (int64_t)device_cu_count() * Cfg::PER_CU;
+    const int grid = (int)(nwork < slots ? nwork : slots);
+    hipLaunchKernelGGL((gemm_f32_kernel<OP, Cfg::BM, Cfg::BN, Cfg::ST, Cfg::WGM, Cfg::WGN, KIND>), dim3(grid),
+                       dim3(Cfg::WGM * Cfg::WGN * 64), 0, s, a);
+    return hipGetLastError();
+}
+
+// Requires: A, B 16-byte aligned; lda, ldb multiples of 4 and < 2^22; the
+// contiguous extent of each operand a multiple of 4 (checked by the caller).
+template <int OP>
+hipError_t launch_gemm_f32_direct_op(const GemmArgs& a, hipStream_t s) {
+    switch (a.epi_kind) {
+        case EK_PLAIN: return launch_f32<OP, EK_PLAIN>(a, s);
+        case EK_BIAS: return launch_f32<OP, EK_BIAS>(a, s);
+        case EK_BIAS_GELU: return launch_f32<OP, EK_BIAS_GELU>(a, s);
+        case EK_BIAS_GELU_PRE: return launch_f32<OP, EK_BIAS_GELU_PRE>(a, s);
+        case EK_ACCUM: return launch_f32<OP, EK_ACCUM>(a, s);
+        default: return launch_f32<OP, EK_GENERIC>(a, s);
+    }
+}
+
+}  // namespace vedic

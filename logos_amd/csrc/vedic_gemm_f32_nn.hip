@@ -1,0 +1,20 @@
+// vedic_gemm_f32_nn.hip -- instantiates the strict-fp32 GEMM for op NN (one
+// translation unit per op so the build compiles them in parallel).  The kernels
+// are instantiated explicitly so that every launch has its host stub.
+#include "vedic_gemm_f32.hpp"
+
+namespace vedic {
+
+#define VEDIC_F32_INST(KIND) \
+    template __global__ void gemm_f32_kernel<0, CfgF32::BM, CfgF32::BN, CfgF32::ST, CfgF32::WGM, CfgF32::WGN, KIND>(GemmArgs);
+VEDIC_F32_INST(EK_PLAIN)
+VEDIC_F32_INST(EK_BIAS)
+VEDIC_F32_INST(EK_BIAS_GELU)
+VEDIC_F32_INST(EK_BIAS_GELU_PRE)
+VEDIC_F32_INST(EK_ACCUM)
+VEDIC_F32_INST(EK_GENERIC)
+#undef VEDIC_F32_INST
+
+hipError_t launch_gemm_f32_direct_nn(const GemmArgs& a, hipStream_t s) { return launch_gemm_f32_direct_op<0>(a, s); }
+
+}  // namespace vedic
