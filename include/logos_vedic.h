@@ -23,6 +23,14 @@
  * after the full dot product, as vedic_gemm_bias does
  * (include/VedicGEMM.hpp:56-65).
  *
+ * Memory: the caller allocates every output.  A product whose output has too
+ * few tiles to fill the GPU and whose contraction is long (fp16: fewer than
+ * 128 tiles of 128 x 128 and K >= 2048; fp32: K >= 256) runs split over K and
+ * takes a stream-ordered fp32 workspace of S * M * N * 4 bytes (S <= 8) with
+ * hipMallocAsync / hipFreeAsync on `stream`; every other call allocates
+ * nothing.  Results never depend on the split or on timing: slices are added
+ * in a fixed order.
+ *
  * Errors follow the reference's conventions: shape errors are
  * VEDIC_STATUS_BAD_DIM (the reference throws std::invalid_argument,
  * include/VedicGEMM.hpp:27-30), device errors VEDIC_STATUS_HIP_ERROR (the
