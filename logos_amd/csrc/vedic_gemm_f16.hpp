@@ -88,6 +88,7 @@ struct Side {
     static_assert(NINS % NW == 0, "stage loads do not divide among the waves");
     static constexpr int CPR = KC ? BK / 8 : R / 8;  // 16-byte chunks per LDS row
     uint32_t off[NLD];  // per-lane byte offset from the tile base; kOob outside the matrix
+    int kend[NLD];      // the chunk is inside the contraction range iff kend <= K - k0
 
     __device__ __forceinline__ static void geom(int wave, int lane, int i, int& row, int& c) {
         const int q = (wave * NLD + i) * 64 + lane;
@@ -102,27 +103,18 @@ struct Side {
             geom(wave, lane, i, row, c);
             const bool ok = KC ? (mn0 + row < MN) : (mn0 + 8 * c + 8 <= MN);
             off[i] = ok ? (uint32_t)((int64_t)row * ld * 2 + c * 16) : kOob;
+            kend[i] = KC ? 8 * c + 8 : row + 1;
         }
     }
     // Direct loads of one stage.  `tile` points at element (mn0, k0) (KC) or
-    // (k0, mn0) (MC); krem = K - k0 (< BK only on the last stage).
+    // (k0, mn0) (MC); krem = K - k0 (<= 0 past the range: zeros, no memory
+    // touched).  Branch free, so every stage's loads have the same shape.
     __device__ __forceinline__ void load(const _Float16* tile, char* lds, int wave, int lane, int krem) const {
         const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(tile);
-        if (krem >= BK) {
 #pragma unroll
-            for (int i = 0; i < NLD; ++i)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds + (wave * NLD + i) * 1024), 16,
-                                                         off[i], 0, 0, 0);
-        } else {
-#pragma unroll
-            for (int i = 0; i < NLD; ++i) {
-                int row, c;
-                geom(wave, lane, i, row, c);
-                const bool in = KC ? (8 * c + 8 <= krem) : (row < krem);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds + (wave * NLD + i) * 1024), 16,
-                                                         in ? off[i] : kOob, 0, 0, 0);
-            }
-        }
+        for (int i = 0; i < NLD; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds + (wave * NLD + i) * 1024), 16,
+                                                     kend[i] <= krem ? off[i] : kOob, 0, 0, 0);
     }
 };
 
@@ -246,18 +238,17 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
     static_assert(ST >= 2 && ST <= 4, "2 to 4 LDS stages");
     static_assert((ST - 2) * L < 64, "vmcnt range");
 
-    // One LDS object per operand and stage: reads of one stage provably do
-    // not alias the direct loads into another.
-    __shared__ __attribute__((aligned(1024))) char a0[SA::BYTES];
-    __shared__ __attribute__((aligned(1024))) char b0[SB::BYTES];
-    __shared__ __attribute__((aligned(1024))) char a1[SA::BYTES];
-    __shared__ __attribute__((aligned(1024))) char b1[SB::BYTES];
-    __shared__ __attribute__((aligned(1024))) char a2[ST > 2 ? SA::BYTES : 16];
-    __shared__ __attribute__((aligned(1024))) char b2[ST > 2 ? SB::BYTES : 16];
-    __shared__ __attribute__((aligned(1024))) char a3[ST > 3 ? SA::BYTES : 16];
-    __shared__ __attribute__((aligned(1024))) char b3[ST > 3 ? SB::BYTES : 16];
-    char* const As[4] = {a0, a1, a2, a3};
-    char* const Bs[4] = {b0, b1, b2, b3};
+    // One LDS object per stage (A then B): reads of one stage provably do not
+    // alias the direct loads into another.  The compiler follows only a few
+    // distinct direct-load targets; one object per operand and stage (eight
+    // at ST = 4) is past that, and every read would then wait for every load.
+    constexpr int SBYTES = SA::BYTES + SB::BYTES;
+    __shared__ __attribute__((aligned(1024))) char t0[SBYTES];
+    __shared__ __attribute__((aligned(1024))) char t1[SBYTES];
+    __shared__ __attribute__((aligned(1024))) char t2[ST > 2 ? SBYTES : 16];
+    __shared__ __attribute__((aligned(1024))) char t3[ST > 3 ? SBYTES : 16];
+    char* const As[4] = {t0, t1, t2, t3};
+    char* const Bs[4] = {t0 + SA::BYTES, t1 + SA::BYTES, t2 + SA::BYTES, t3 + SA::BYTES};
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform per wave
     const int lane = threadIdx.x & 63;
@@ -280,8 +271,7 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
     sa.init(wave, lane, args.lda, m0, args.M);
     sb.init(wave, lane, args.ldb, n0, args.N);
 #pragma unroll
-    for (int s = 0; s < ST - 1; ++s)
-        if (s < it.nk) VEDIC_ISSUE(s, As[s], Bs[s]);
+    for (int s = 0; s < ST - 1; ++s) VEDIC_ISSUE(s, As[s], Bs[s]);
 
     while (true) {
         float16_t acc[MI][NI];
@@ -290,22 +280,23 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
 #pragma unroll
             for (int j = 0; j < NI; ++j) acc[i][j] = float16_t{};
 
+        // Uniform pipeline: every stage step waits for the same number of
+        // loads and issues stage kt + ST - 1, which past the work item's
+        // range loads zeros without touching memory; only the MFMAs are
+        // skipped for such stages.  Every step then has the same shape, so
+        // the compiler can tell that a read of stage kt depends only on
+        // stage kt's loads (with steps of different shapes it falls back to
+        // waiting for every load in flight).
         const int nk = it.nk;
         for (int k0 = 0; k0 < nk; k0 += ST) {
 #pragma unroll
             for (int s = 0; s < ST; ++s) {
                 const int kt = k0 + s;
-                if (kt < nk) {
-                    // stage kt's loads, then at most `ahead` later stages' loads, are outstanding
-                    const int ahead = min(ST - 2, nk - 1 - kt);
-                    if (ahead >= 2) wait_vmcnt<2 * L>();
-                    else if (ahead == 1) wait_vmcnt<L>();
-                    else wait_vmcnt<0>();
-                    stage_barrier();
-                    const int sl = (s + ST - 1) % ST;
-                    if (kt + ST - 1 < nk) VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
-                    mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI>(As[s], Bs[s], wm * WM, wn * WN, lane, acc);
-                }
+                wait_vmcnt<(ST - 2) * L>();  // stage kt has landed; ST - 2 later stages in flight
+                stage_barrier();
+                const int sl = (s + ST - 1) % ST;
+                VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
+                if (kt < nk) mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI>(As[s], Bs[s], wm * WM, wn * WN, lane, acc);
             }
         }
 
@@ -322,8 +313,7 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
             sa.init(wave, lane, args.lda, m0, args.M);
             sb.init(wave, lane, args.ldb, n0, args.N);
 #pragma unroll
-            for (int s = 0; s < ST - 1; ++s)
-                if (s < it.nk) VEDIC_ISSUE(s, As[s], Bs[s]);
+            for (int s = 0; s < ST - 1; ++s) VEDIC_ISSUE(s, As[s], Bs[s]);
         }
         const bool full = (row0 + WM <= args.M) && (col0 + WN <= args.N);
         if (KIND != EK_GENERIC && full)
@@ -332,6 +322,7 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
             epilogue<KIND, true, MI, NI>(ea, acc, row0, col0, lane);
         if (!more) break;
     }
+    wait_vmcnt<0>();  // the trailing zero loads still write LDS
 }
 
 #undef VEDIC_ISSUE
@@ -339,8 +330,14 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
 #undef VEDIC_B_TILE
 
 // Tile configurations: (BM, BN, BK, ST, WGM, WGN).
+#ifndef VEDIC_F16_LARGE_BK
+#define VEDIC_F16_LARGE_BK 64
+#endif
+#ifndef VEDIC_F16_LARGE_ST
+#define VEDIC_F16_LARGE_ST 2
+#endif
 struct CfgLarge {  // 256 x 256, eight waves of 128 x 64
-    static constexpr int BM = 256, BN = 256, BK = 64, ST = 2, WGM = 2, WGN = 4;
+    static constexpr int BM = 256, BN = 256, BK = VEDIC_F16_LARGE_BK, ST = VEDIC_F16_LARGE_ST, WGM = 2, WGN = 4;
 };
 struct CfgSmall {  // 128 x 128, four waves of 64 x 64
     static constexpr int BM = 128, BN = 128, BK = 64, ST = 2, WGM = 2, WGN = 2;
