@@ -55,6 +55,9 @@ WORKLOADS = {
     "ffn_up_fp16_bias_gelu": dict(cfg=2, gemms=[_g(8192, 1024, 4096, epi="bias_gelu")]),
     "ffn_down_dx_nt_fp16": dict(cfg=3, gemms=[_g(8192, 1024, 4096, op="NT")]),
     "ffn_down_dw_tn_fp16": dict(cfg=3, gemms=[_g(4096, 8192, 1024, op="TN", beta=1.0)]),
+    # FFN backward through the activation, fused (SURVEY next-row 1): dH = (dY . W2^T) * gelu'(H)
+    # with db1 += colsum(dH), at config 3's NT shape and config 2's activation
+    "ffn_bwd_dh_gelu_nt_fp16": dict(cfg=3, gemms=[_g(8192, 1024, 4096, op="NT", epi="gelu_bwd")]),
     "lm_head_fp16": dict(cfg=4, gemms=[_g(8192, 1024, 8192)]),
     "lm_head_fp32": dict(cfg=4, gemms=[_g(8192, 1024, 8192, dtype="fp32")]),
     **{f"decode_fp16_m{m}": dict(cfg=4, hbm=True, gemms=[_g(m, 1024, 8192)]) for m in (1, 2, 4, 8, 16, 32)},
@@ -168,6 +171,7 @@ def cpu_baseline(w: dict, seconds: float, seed: int = 7):
         bias = (rng.standard_normal(N, dtype=np.float32) * np.float32(0.01))
         if g["dtype"] == "fp16":
             A, B = o.f16_round(A), o.f16_round(B)
+        Hs = (rng.standard_normal((rows, N), dtype=np.float32) * np.float32(2.0)) if g["epi"] == "gelu_bwd" else None
         if op == "NT":
             B = np.ascontiguousarray(B.T)
         if op == "TN":
@@ -177,16 +181,19 @@ def cpu_baseline(w: dict, seconds: float, seed: int = 7):
         while True:
             if kind == "reference":
                 if op == "NN":
-                    C = o.ref_vedic_gemm_bias(A, B, bias) if g["epi"] != "none" else o.ref_vedic_gemm(A, B)
+                    C = o.ref_vedic_gemm_bias(A, B, bias) if g["epi"] in ("bias", "bias_gelu") else o.ref_vedic_gemm(A, B)
                 elif op == "NT":
                     C = o.ref_gemm_nt(A, B)
                 else:
                     C = o.ref_gemm_tn(A, B)
                 if g["epi"] == "bias_gelu":
                     C = o.ref_gelu(C)
+                if g["epi"] == "gelu_bwd":  # ffn_backward's gelu_backward + bias_backward
+                    C = o.ref_gelu_backward(Hs, C)
+                    o.ref_bias_backward(C)
             else:
                 if op == "NN":
-                    C = (o.vedic_gemm_bias(A, B, bias, nthreads=1) if g["epi"] != "none"
+                    C = (o.vedic_gemm_bias(A, B, bias, nthreads=1) if g["epi"] in ("bias", "bias_gelu")
                          else o.vedic_gemm(A, B, nthreads=1))
                 elif op == "NT":
                     C = o.gemm_nt(A, B, nthreads=1)
@@ -194,6 +201,9 @@ def cpu_baseline(w: dict, seconds: float, seed: int = 7):
                     C = o.gemm_tn(A, B, nthreads=1)
                 if g["epi"] == "bias_gelu":
                     C = o.gelu(C)
+                if g["epi"] == "gelu_bwd":
+                    C = o.gelu_bwd_reference_f32(C, Hs)
+                    C.sum(axis=0)
             reps += 1
             if time.perf_counter() - t0 >= per_gemm:
                 break
@@ -236,16 +246,24 @@ def make_step(w: dict, dev, torch):
             A, B = A.half(), B.half()
         C = torch.randn((M, N), generator=gen, device=dev) * 1e-3 if g["beta"] else torch.empty((M, N), device=dev)
         keep += [A, B, bias, C]
-        epi = {"none": _lib.EPI_NONE, "bias": _lib.EPI_BIAS, "bias_gelu": _lib.EPI_BIAS_GELU}[g["epi"]]
+        epi = {"none": _lib.EPI_NONE, "bias": _lib.EPI_BIAS, "bias_gelu": _lib.EPI_BIAS_GELU,
+               "gelu_bwd": _lib.EPI_GELU_BWD}[g["epi"]]
+        gbwd = g["epi"] == "gelu_bwd"
+        H = torch.randn((M, N), generator=gen, device=dev) * 2.0 if gbwd else None
+        db = torch.zeros((N,), device=dev) if gbwd else None
+        keep += [H, db]
         d = _lib.GemmDesc(
             op={"NN": _lib.OP_NN, "NT": _lib.OP_NT, "TN": _lib.OP_TN}[op],
             in_dtype=_lib.DT_F16 if g["dtype"] == "fp16" else _lib.DT_F32, out_dtype=_lib.DT_F32,
             M=M, N=N, K=K, A=A.data_ptr(), lda=A.shape[1], B=B.data_ptr(), ldb=B.shape[1],
             C=C.data_ptr(), ldc=N, alpha=1.0, beta=g["beta"],
-            bias=bias.data_ptr() if g["epi"] != "none" else None, epilogue=epi,
-            preact=None, ld_preact=0, stream=stream.cuda_stream)
+            bias=bias.data_ptr() if g["epi"] in ("bias", "bias_gelu") else None, epilogue=epi,
+            preact=H.data_ptr() if gbwd else None, ld_preact=N if gbwd else 0, stream=stream.cuda_stream,
+            colsum=db.data_ptr() if gbwd else None, colsum_beta=1.0)
         es = 2 if g["dtype"] == "fp16" else 4
         hbm = (M * K + K * N) * es + M * N * 4 * (2 if g["beta"] else 1) + (N * 4 if g["epi"] != "none" else 0)
+        if gbwd:
+            hbm += M * N * 4 + N * 4  # H read, db read and written
         items.append((d, 2.0 * M * N * K, hbm))
     ptrs = [ctypes.byref(d) for d, _, _ in items]
     gemm = lib.vedic_gemm

@@ -281,6 +281,30 @@ inline void cuda_gemm_fp16_tn(const __half* X, int K, int M, const __half* dY, i
     vedic_hip::check(vedic_gemm_tn_f16(X, dY, dW, M, N, K, beta, stream), "cuda_gemm_fp16_tn");
 }
 
+// FFN backward through the activation, fused (ffn_da + gelu_bwd + bias_grad,
+// cuda/train_gpu.cu:323-345 and 263-273): dH = (dY . W^T) * gelu'(H), W stored
+// [N x K], H the cached pre-activation [M x N]; db (nullable) += colsum(dH).
+inline void cuda_vedic_gemm_nt_gelu_bwd(const GPUTensor& dY, const GPUTensor& W, const GPUTensor& H, GPUTensor& dH,
+                                        float* db = nullptr, hipStream_t stream = nullptr) {
+    vedic_hip::require(W.cols == dY.cols, "cuda_vedic_gemm_nt_gelu_bwd: dY.cols != W.cols");
+    vedic_hip::require(dH.rows == dY.rows && dH.cols == W.rows, "cuda_vedic_gemm_nt_gelu_bwd: dH shape");
+    vedic_hip::require(H.rows == dH.rows && H.cols == dH.cols, "cuda_vedic_gemm_nt_gelu_bwd: H shape");
+    vedic_hip::check(vedic_gemm_nt_gelu_bwd_f32(dY.data, W.data, H.data, dH.data, db, dY.rows, W.rows, dY.cols,
+                                                stream),
+                     "cuda_vedic_gemm_nt_gelu_bwd");
+}
+inline void cuda_gemm_fp16_nt_gelu_bwd(const __half* dY, int M, int K, const __half* W, int N, const float* H,
+                                       float* dH, float* db = nullptr, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_gemm_nt_gelu_bwd_f16(dY, W, H, dH, db, M, N, K, stream), "cuda_gemm_fp16_nt_gelu_bwd");
+}
+
+// db[j] = beta db[j] + sum_s dY[s][j] (bias_grad_kernel, cuda/train_gpu.cu:263-273;
+// the reference accumulates: beta = 1), summed in a fixed order.
+inline void cuda_bias_grad(const float* dY, float* db, int seq, int cols, float beta = 1.0f,
+                           hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_bias_grad(dY, db, seq, cols, beta, stream), "cuda_bias_grad");
+}
+
 // --------------------------------------------------- elementwise helpers
 
 // C[i][j] += bias[j] (the add_bias_kernel launch, cuda/VedicGEMM.cu:96-102).

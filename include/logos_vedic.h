@@ -18,6 +18,8 @@
  *     t     = t + bias[j]                        (if the epilogue has a bias)
  *     pre   = t                                  (stored if preact != NULL)
  *     C     = gelu_tanh(t) or t                  (per the epilogue)
+ *     C     = t * gelu_tanh'(P)                  (VEDIC_EPI_GELU_BWD, P read from preact)
+ *     colsum[j] = colsum_beta * colsum[j] + sum_i C[i][j]   (if colsum != NULL)
  * where gelu_tanh(x) = 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3)))
  * (include/FeedForward.hpp:11-13).  For alpha = 1, beta = 0 the bias is added
  * after the full dot product, as vedic_gemm_bias does
@@ -68,7 +70,9 @@ typedef enum {
     VEDIC_EPI_NONE = 0,
     VEDIC_EPI_BIAS = 1,      /* + bias[j]                 */
     VEDIC_EPI_BIAS_GELU = 2, /* gelu_tanh(t + bias[j])    */
-    VEDIC_EPI_GELU = 3       /* gelu_tanh(t)              */
+    VEDIC_EPI_GELU = 3,      /* gelu_tanh(t)              */
+    VEDIC_EPI_GELU_BWD = 4   /* t * gelu_tanh'(P[i][j]), P = the cached
+                                pre-activation, read through `preact` */
 } vedic_epilogue_t;
 
 typedef enum {
@@ -77,7 +81,8 @@ typedef enum {
 } vedic_dtype_t;
 
 /* Full descriptor of one GEMM.  A and B share in_dtype; C is out_dtype
- * (F16 output only with F16 inputs); bias and preact are always fp32. */
+ * (F16 output only with F16 inputs); bias and preact are always fp32.
+ * Zero-initialise it (`= {0}`) so that fields a caller does not use are off. */
 typedef struct {
     int op;        /* vedic_op_t */
     int in_dtype;  /* vedic_dtype_t of A and B */
@@ -93,9 +98,16 @@ typedef struct {
     float beta;
     const float* bias; /* [N], required for *_BIAS* epilogues */
     int epilogue;      /* vedic_epilogue_t */
-    float* preact;     /* optional [M x ld_preact] pre-activation output */
+    float* preact;     /* optional [M x ld_preact] pre-activation output;
+                          the pre-activation input of VEDIC_EPI_GELU_BWD */
     int64_t ld_preact;
     void* stream;      /* hipStream_t */
+    /* Optional column sums of the final C (fp32 C only):
+     *     colsum[j] = colsum_beta * colsum[j] + sum_i C[i][j]
+     * -- the bias gradient of a layer whose output gradient C is.  Added in a
+     * fixed order (no atomics), so the result does not depend on timing. */
+    float* colsum;
+    float colsum_beta;
 } vedic_gemm_desc_t;
 
 /* The general entry point.  New: the reference has no single descriptor
@@ -154,6 +166,23 @@ int vedic_gemm_tn_f32(const float* X, const float* dY, float* dW, int M, int N, 
                       void* stream);
 int vedic_gemm_tn_f16(const void* X, const void* dY, float* dW, int M, int N, int K, float beta,
                       void* stream);
+
+/* FFN backward through the activation, fused:
+ *     dH[MxN] = (dY[MxK] . W^T) * gelu_tanh'(H),   W stored [NxK],
+ *     db[j]  += sum_i dH[i][j]                     (db nullable),
+ * with H the cached pre-activation [MxN] (the `preact` output of
+ * vedic_gemm_bias_gelu_*).  Replaces ffn_da + gelu_bwd + bias_grad
+ * (cuda/train_gpu.cu:323-332, 334-345, 263-273, launched at :590-600 and
+ * :619-621): one pass over dH instead of three, and no atomics. */
+int vedic_gemm_nt_gelu_bwd_f16(const void* dY, const void* W, const float* H, float* dH, float* db, int M,
+                               int N, int K, void* stream);
+int vedic_gemm_nt_gelu_bwd_f32(const float* dY, const float* W, const float* H, float* dH, float* db, int M,
+                               int N, int K, void* stream);
+
+/* db[j] = beta * db[j] + sum_i dY[i][j] over an MxN fp32 matrix, summed in a
+ * fixed order.  Replaces bias_grad_kernel (cuda/train_gpu.cu:263-273), which
+ * atomicAdds into db (beta = 1). */
+int vedic_bias_grad(const float* dY, float* db, int M, int N, float beta, void* stream);
 
 /* ---- elementwise helpers on the path ---------------------------------- */
 

@@ -28,7 +28,7 @@ STATUS_HIP_ERROR = 7
 STATUS_TOO_LARGE = 8
 
 OP_NN, OP_NT, OP_TN = 0, 1, 2
-EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU = 0, 1, 2, 3
+EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU, EPI_GELU_BWD = 0, 1, 2, 3, 4
 DT_F32, DT_F16 = 0, 1
 
 
@@ -55,6 +55,8 @@ class GemmDesc(ctypes.Structure):
         ("preact", c_vp),
         ("ld_preact", c_i64),
         ("stream", c_vp),
+        ("colsum", c_vp),
+        ("colsum_beta", c_float),
     ]
 
 
@@ -82,6 +84,9 @@ SIGNATURES = {
     "vedic_gemm_nt_f16": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_float, c_vp]),
     "vedic_gemm_tn_f32": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_float, c_vp]),
     "vedic_gemm_tn_f16": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_float, c_vp]),
+    "vedic_gemm_nt_gelu_bwd_f16": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
+    "vedic_gemm_nt_gelu_bwd_f32": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
+    "vedic_bias_grad": (c_int, [c_vp, c_vp, c_int, c_int, c_float, c_vp]),
     "vedic_add_bias": (c_int, [c_vp, c_vp, c_int, c_int, c_vp]),
     "vedic_gelu": (c_int, [c_vp, c_i64, c_vp]),
     "vedic_cast_f32_to_f16": (c_int, [c_vp, c_vp, c_i64, c_vp]),

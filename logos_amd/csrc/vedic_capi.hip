@@ -76,11 +76,81 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ ws, int S, GemmAr
         if (epi & EPI_BIAS) v += a.bias[j];
         if (epi & EPI_PREACT) a.preact[(int64_t)i * a.ldp + j] = v;
         if (epi & EPI_GELU) v = gelu_tanh(v);
+        if (epi & EPI_GELU_BWD) v *= gelu_tanh_grad(a.preact[(int64_t)i * a.ldp + j]);
         if (f16out)
             static_cast<_Float16*>(a.C)[c] = (_Float16)v;
         else
             static_cast<float*>(a.C)[c] = v;
     }
+}
+
+// ------------------------------------------------------------ column sums
+
+// part[b][j] = sum of X[i][j] over the rows i of block b (rows b * rows_per_block
+// .. min(M, (b + 1) * rows_per_block) - 1), added in ascending i.  One thread
+// per column of a 256-column strip, grid (strips, blocks): every row read is
+// one coalesced 1 KiB segment.
+__global__ void colsum_partial_kernel(const float* __restrict__ X, int64_t ldx, int M, int N, int rows_per_block,
+                                      float* __restrict__ part) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= N) return;
+    const int i0 = blockIdx.y * rows_per_block;
+    const int i1 = min(M, i0 + rows_per_block);
+    float acc = 0.0f;
+#pragma unroll 4
+    for (int i = i0; i < i1; ++i) acc += X[(int64_t)i * ldx + j];
+    part[(int64_t)blockIdx.y * N + j] = acc;
+}
+
+// out[j] = beta * out[j] + sum_b part[b][j] in a fixed order, so the column
+// sums do not depend on timing (the reference atomicAdds,
+// cuda/train_gpu.cu:263-273).  A workgroup covers 32 columns with 8 groups of
+// 32 threads: group g adds blocks [g q, (g + 1) q) in ascending order
+// (q = ceil(nblocks / 8); each step reads 128 contiguous bytes), and the 8
+// group sums are added in ascending g.
+__global__ void __launch_bounds__(256) colsum_reduce_kernel(const float* __restrict__ part, int nblocks, int N,
+                                                            float* __restrict__ out, float beta) {
+    __shared__ float sh[8][32];
+    const int c = threadIdx.x & 31, g = threadIdx.x >> 5;
+    const int j = blockIdx.x * 32 + c;
+    const int q = (nblocks + 7) / 8;
+    const int b0 = min(nblocks, g * q), b1 = min(nblocks, b0 + q);
+    float acc = 0.0f;
+    if (j < N) {
+#pragma unroll 4
+        for (int b = b0; b < b1; ++b) acc += part[(int64_t)b * N + j];
+    }
+    sh[g][c] = acc;
+    __syncthreads();
+    if (g == 0 && j < N) {
+        float t = sh[0][c];
+#pragma unroll
+        for (int k = 1; k < 8; ++k) t += sh[k][c];
+        out[j] = beta == 0.0f ? t : beta * out[j] + t;
+    }
+}
+
+static hipError_t launch_colsum_reduce(const float* part, int nblocks, int N, float* out, float beta,
+                                       hipStream_t s) {
+    hipLaunchKernelGGL(colsum_reduce_kernel, dim3((unsigned)((N + 31) / 32)), dim3(256), 0, s, part, nblocks, N,
+                       out, beta);
+    return hipGetLastError();
+}
+
+// Column sums of an M x N fp32 matrix through a stream-ordered workspace of
+// ceil(M / 64) x N partial sums.
+static hipError_t colsum_matrix(const float* X, int64_t ldx, int M, int N, float* out, float beta, hipStream_t s) {
+    constexpr int RB = 64;
+    const int nb = (M + RB - 1) / RB;
+    float* part = nullptr;
+    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&part), sizeof(float) * (size_t)nb * N, s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(colsum_partial_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)nb), dim3(256), 0, s, X,
+                       ldx, M, N, RB, part);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = launch_colsum_reduce(part, nb, N, out, beta, s);
+    const hipError_t f = hipFreeAsync(part, s);
+    return e != hipSuccess ? e : f;
 }
 
 // fp32 tiles: the direct-load pipelined kernel where the operands allow
@@ -134,6 +204,7 @@ static hipError_t launch_split(bool f16, int op, bool vec, const GemmArgs& a, in
     p.beta = 0.0f;
     p.epi = 0;
     p.epi_kind = EK_PLAIN;
+    p.cs_part = nullptr;
     p.ksplit = ks;
     p.kslice = kslice;
     p.c_split_stride = total;
@@ -164,9 +235,13 @@ extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
         !(d->out_dtype == VEDIC_DT_F16 && d->in_dtype == VEDIC_DT_F16))
         return VEDIC_STATUS_BAD_DTYPE;
     if (!d->A || !d->B || !d->C) return VEDIC_STATUS_NULL_POINTER;
-    if (d->epilogue < VEDIC_EPI_NONE || d->epilogue > VEDIC_EPI_GELU) return VEDIC_STATUS_BAD_EPILOGUE;
+    if (d->epilogue < VEDIC_EPI_NONE || d->epilogue > VEDIC_EPI_GELU_BWD) return VEDIC_STATUS_BAD_EPILOGUE;
     const bool want_bias = d->epilogue == VEDIC_EPI_BIAS || d->epilogue == VEDIC_EPI_BIAS_GELU;
     if (want_bias && !d->bias) return VEDIC_STATUS_BAD_EPILOGUE;
+    // GELU backward reads the cached pre-activation through `preact`
+    const bool gelu_bwd = d->epilogue == VEDIC_EPI_GELU_BWD;
+    if (gelu_bwd && !d->preact) return VEDIC_STATUS_BAD_EPILOGUE;
+    if (d->colsum && d->out_dtype != VEDIC_DT_F32) return VEDIC_STATUS_BAD_DTYPE;
 
     const bool a_kc = d->op != VEDIC_OP_TN;
     const bool b_kc = d->op == VEDIC_OP_NT;
@@ -193,10 +268,12 @@ extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
     a.epi = 0;
     if (want_bias) a.epi |= EPI_BIAS;
     if (d->epilogue == VEDIC_EPI_BIAS_GELU || d->epilogue == VEDIC_EPI_GELU) a.epi |= EPI_GELU;
-    if (d->preact) a.epi |= EPI_PREACT;
+    if (gelu_bwd) a.epi |= EPI_GELU_BWD;
+    else if (d->preact) a.epi |= EPI_PREACT;
     if (d->beta != 0.0f) a.epi |= EPI_BETA;
     if (d->alpha != 1.0f) a.epi |= EPI_ALPHA;
     if (d->out_dtype == VEDIC_DT_F16) a.epi |= EPI_F16OUT;
+    if (d->colsum) a.epi |= EPI_COLSUM;
     a.group_m = 8;
 
     // 16-byte vector loads need aligned bases, leading dimensions that keep
@@ -211,28 +288,48 @@ extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
     // row: a few hundred rows of any operand or output must stay below 2 GiB.
     if (d->ldc >= kMaxLd || (d->preact && d->ld_preact >= kMaxLd)) return VEDIC_STATUS_TOO_LARGE;
 
+    const bool f16 = d->in_dtype == VEDIC_DT_F16;
+    const bool direct = vec && d->lda < kMaxLd && d->ldb < kMaxLd;
+    const bool skinny = direct && d->op == VEDIC_OP_NN && d->M <= 32;
+    const int ks = skinny || (f16 && !direct) ? 1 : choose_ksplit(d->M, d->N, d->K, device_cu_count(), f16);
+
     hipStream_t s = static_cast<hipStream_t>(d->stream);
-    hipError_t e;
-    if (d->in_dtype == VEDIC_DT_F16) {
-        if (vec && d->lda < kMaxLd && d->ldb < kMaxLd && d->op == VEDIC_OP_NN && d->M <= 32) {
-            // decode-time shapes: bound by streaming B once from HBM
-            e = launch_gemm_f16_skinny(a, s);
-        } else if (vec && d->lda < kMaxLd && d->ldb < kMaxLd) {
-            const int ks = choose_ksplit(d->M, d->N, d->K, device_cu_count(), true);
-            if (ks > 1)
-                e = launch_split(true, d->op, true, a, ks, s);
-            else
-                e = d->op == VEDIC_OP_NN   ? launch_gemm_f16_direct_nn(a, s)
-                    : d->op == VEDIC_OP_NT ? launch_gemm_f16_direct_nt(a, s)
-                                           : launch_gemm_f16_direct_tn(a, s);
-        } else {
-            e = launch_gemm_f16_generic(d->op, a, s);
-        }
-    } else if (vec && d->lda < kMaxLd && d->ldb < kMaxLd && d->op == VEDIC_OP_NN && d->M <= 32) {
-        e = launch_gemm_f32_skinny(a, s);
+    hipError_t e = hipSuccess;
+    // Column sums: the fused epilogue writes one partial per 32-row block and
+    // column, added afterwards in a fixed order.  A split product sums the
+    // finished C instead.
+    float* cs_part = nullptr;
+    const int cs_blocks = (d->M + 31) / 32;
+    if (d->colsum && ks == 1) {
+        e = hipMallocAsync(reinterpret_cast<void**>(&cs_part), sizeof(float) * (size_t)cs_blocks * d->N, s);
+        if (e != hipSuccess) return hip_status(e);
+        a.cs_part = cs_part;
+    }
+
+    if (skinny) {
+        // decode-time shapes: bound by streaming B once from HBM
+        e = f16 ? launch_gemm_f16_skinny(a, s) : launch_gemm_f32_skinny(a, s);
+    } else if (ks > 1) {
+        e = launch_split(f16, d->op, vec, a, ks, s);
+    } else if (f16 && direct) {
+        e = d->op == VEDIC_OP_NN   ? launch_gemm_f16_direct_nn(a, s)
+            : d->op == VEDIC_OP_NT ? launch_gemm_f16_direct_nt(a, s)
+                                   : launch_gemm_f16_direct_tn(a, s);
+    } else if (f16) {
+        e = launch_gemm_f16_generic(d->op, a, s);
     } else {
-        const int ks = choose_ksplit(d->M, d->N, d->K, device_cu_count(), false);
-        e = ks > 1 ? launch_split(false, d->op, vec, a, ks, s) : launch_f32_tiled(d->op, vec, a, s);
+        e = launch_f32_tiled(d->op, vec, a, s);
+    }
+
+    if (d->colsum && e == hipSuccess) {
+        if (cs_part)
+            e = launch_colsum_reduce(cs_part, cs_blocks, d->N, d->colsum, d->colsum_beta, s);
+        else
+            e = colsum_matrix(static_cast<const float*>(d->C), d->ldc, d->M, d->N, d->colsum, d->colsum_beta, s);
+    }
+    if (cs_part) {
+        const hipError_t f = hipFreeAsync(cs_part, s);
+        if (e == hipSuccess) e = f;
     }
     return hip_status(e);
 }
@@ -330,6 +427,34 @@ extern "C" int vedic_gemm_tn_f16(const void* X, const void* dY, float* dW, int M
                                  float beta, void* stream) {
     vedic_gemm_desc_t d = make_desc(VEDIC_OP_TN, VEDIC_DT_F16, M, N, K, X, M, dY, N, dW, 1.f, beta, stream);
     return vedic_gemm(&d);
+}
+
+extern "C" int vedic_gemm_nt_gelu_bwd_f16(const void* dY, const void* W, const float* H, float* dH, float* db,
+                                          int M, int N, int K, void* stream) {
+    vedic_gemm_desc_t d = make_desc(VEDIC_OP_NT, VEDIC_DT_F16, M, N, K, dY, K, W, K, dH, 1.f, 0.f, stream);
+    d.epilogue = VEDIC_EPI_GELU_BWD;
+    d.preact = const_cast<float*>(H);
+    d.ld_preact = N;
+    d.colsum = db;
+    d.colsum_beta = 1.0f;
+    return vedic_gemm(&d);
+}
+
+extern "C" int vedic_gemm_nt_gelu_bwd_f32(const float* dY, const float* W, const float* H, float* dH, float* db,
+                                          int M, int N, int K, void* stream) {
+    vedic_gemm_desc_t d = make_desc(VEDIC_OP_NT, VEDIC_DT_F32, M, N, K, dY, K, W, K, dH, 1.f, 0.f, stream);
+    d.epilogue = VEDIC_EPI_GELU_BWD;
+    d.preact = const_cast<float*>(H);
+    d.ld_preact = N;
+    d.colsum = db;
+    d.colsum_beta = 1.0f;
+    return vedic_gemm(&d);
+}
+
+extern "C" int vedic_bias_grad(const float* dY, float* db, int M, int N, float beta, void* stream) {
+    if (!dY || !db) return VEDIC_STATUS_NULL_POINTER;
+    if (M <= 0 || N <= 0) return VEDIC_STATUS_BAD_DIM;
+    return hip_status(colsum_matrix(dY, N, M, N, db, beta, static_cast<hipStream_t>(stream)));
 }
 
 // ----------------------------------------------------------- elementwise

@@ -44,6 +44,22 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
+// Derivative of the same tanh-GELU, d/dx [x s(x)] with s = 1 / (1 + exp(-2u)),
+// u = c (x + 0.044715 x^3):  s + x s' = s + 2 x s (1 - s) c (1 + 3 * 0.044715 x^2),
+// using 0.5 (1 + tanh u) = s and sech^2 u = 4 s (1 - s).  Limits: x -> +inf
+// gives 1, x -> -inf gives 0 (s underflows before x grows), NaN propagates.
+__device__ __forceinline__ float gelu_tanh_grad(float x) {
+    constexpr float c = 0.7978845608f;
+    constexpr float k0 = -2.0f * c * 1.4426950408889634f;
+    constexpr float k1 = -2.0f * c * 0.044715f * 1.4426950408889634f;
+    constexpr float k3 = 3.0f * 0.044715f;
+    const float x2 = x * x;
+    const float e = __builtin_amdgcn_exp2f(x * __builtin_fmaf(k1, x2, k0));
+    const float sg = __builtin_amdgcn_rcpf(1.0f + e);
+    const float t = x * sg * (1.0f - sg);  // 0 when sg is 0 or 1
+    return __builtin_fmaf(2.0f * c * t, __builtin_fmaf(k3, x2, 1.0f), sg);
+}
+
 // Epilogue flag bits (internal).
 enum : int {
     EPI_BIAS = 1,
@@ -52,6 +68,8 @@ enum : int {
     EPI_BETA = 8,
     EPI_ALPHA = 16,
     EPI_F16OUT = 32,
+    EPI_GELU_BWD = 64,  // C = t * gelu_tanh_grad(P), P read through `preact`
+    EPI_COLSUM = 128,   // column sums of C into cs_part (per 32-row block)
 };
 
 struct GemmArgs {
@@ -72,6 +90,10 @@ struct GemmArgs {
     // to C + s * c_split_stride.  ksplit = 1: one item per tile over all of K.
     int ksplit, kslice;
     int64_t c_split_stride;
+    // Column sums of the final C (EPI_COLSUM): the epilogue writes, for every
+    // 32-row block b of C and column j, the sum of the block's rows (rows < M)
+    // to cs_part[b * N + j]; a fixed-order pass then adds the blocks.
+    float* cs_part;
 };
 
 }  // namespace vedic

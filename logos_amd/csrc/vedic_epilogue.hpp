@@ -24,9 +24,12 @@ enum EpiKind : int {
     EK_BIAS_GELU_PRE = 3,  // P = acc + b; C = gelu(P)
     EK_ACCUM = 4,          // C = C + acc           (beta = 1, the dW accumulation)
     EK_GENERIC = 5,        // any flag combination (runtime flags)
+    EK_GELU_BWD = 6,       // C = acc * gelu'(P)    (+ column sums if cs_part)
 };
 
 __host__ __device__ inline int epi_kind_of(int epi, float alpha, float beta) {
+    if ((epi & ~EPI_COLSUM) == EPI_GELU_BWD) return EK_GELU_BWD;
+    if (epi & EPI_COLSUM) return EK_GENERIC;
     if (epi == 0) return EK_PLAIN;
     if (epi == EPI_BIAS) return EK_BIAS;
     if (epi == (EPI_BIAS | EPI_GELU)) return EK_BIAS_GELU;
@@ -73,67 +76,124 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, const float16_t (&ac
     const __amdgpu_buffer_rsrc_t rc = buffer_rsrc(cbase);
     __amdgpu_buffer_rsrc_t rp = rc;
     const bool pre = (KIND == EK_BIAS_GELU_PRE) || (KIND == EK_GENERIC && (a.epi & EPI_PREACT));
-    if (pre) rp = buffer_rsrc(a.preact + (int64_t)row0 * a.ldp);
+    const bool gbwd = (KIND == EK_GELU_BWD) || (KIND == EK_GENERIC && (a.epi & EPI_GELU_BWD));
+    if (pre || gbwd) rp = buffer_rsrc(a.preact + (int64_t)row0 * a.ldp);
+    // column sums: per lane over its 16 rows of each 32-row block, then the
+    // two half-waves (lanes l and l ^ 32 hold the same column) added in a
+    // fixed order; rows past M do not count
+    const bool colsum = (KIND == EK_GELU_BWD || KIND == EK_GENERIC) && a.cs_part != nullptr;
     const uint32_t ldc_b = (uint32_t)(a.ldc * es);
     const uint32_t ldp_b = (uint32_t)(a.ldp * 4);
     const bool want_bias = (KIND == EK_BIAS || KIND == EK_BIAS_GELU || KIND == EK_BIAS_GELU_PRE) ||
                            (KIND == EK_GENERIC && (a.epi & EPI_BIAS));
     const int row_lim = a.M - row0 - 4 * h;  // rows 4h + u of the tile exist iff u < row_lim
+    // Kinds that read memory per element (the old C, the pre-activation) load
+    // a whole 32 x 32 block's values before they are needed: the next block's
+    // loads go out before this block's stores, so the load latency is paid
+    // about once per wave tile rather than once per element.
+    constexpr bool READS = KIND == EK_ACCUM || KIND == EK_GELU_BWD || KIND == EK_GENERIC;
+    const bool rd_c = KIND == EK_ACCUM || (KIND == EK_GENERIC && (a.epi & EPI_BETA));
+    const bool rd_p = gbwd;
+    constexpr int NB = MI * NI;  // 32 x 32 blocks, in the order j-major, i-minor
 
+    float bias_j[NI];
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
         const int col = col0 + 32 * j + l32;
+        bias_j[j] = (want_bias && (!CHECK || col < a.N)) ? a.bias[col] : 0.0f;
+    }
+    // byte offsets of element (g, r) of block (j, i): per-lane part and the
+    // wave-uniform row part; out-of-range elements get kOob
+    auto offsets = [&](int j, int i, int g, int r, uint32_t& oc, uint32_t& op, uint32_t& sc, uint32_t& sp) {
+        const int col = col0 + 32 * j + l32;
+        const int u = 32 * i + 8 * g + r;
+        sc = (uint32_t)u * ldc_b;
+        sp = (uint32_t)u * ldp_b;
+        oc = (uint32_t)(4 * h) * ldc_b + (uint32_t)(col * es);
+        op = (uint32_t)(4 * h) * ldp_b + (uint32_t)(col * 4);
+        if (CHECK) {
+            const bool ok = col < a.N && u < row_lim;
+            oc = ok ? oc : kOob;
+            op = ok ? op : kOob;
+        }
+    };
+    float cur_c[16], cur_p[16], nxt_c[16], nxt_p[16];
+    auto fetch = [&](int bk, float (&dc)[16], float (&dp)[16]) {
+        const int j = bk / MI, i = bk % MI;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            uint32_t oc, op, sc, sp;
+            offsets(j, i, e >> 2, e & 3, oc, op, sc, sp);
+            dc[e] = rd_c ? (f16out ? ld_f16(rc, oc, sc) : ld_f32(rc, oc, sc)) : 0.0f;
+            dp[e] = rd_p ? ld_f32(rp, op, sp) : 0.0f;
+        }
+    };
+    if constexpr (READS) fetch(0, cur_c, cur_p);
+
+#pragma unroll
+    for (int bk = 0; bk < NB; ++bk) {
+        const int j = bk / MI, i = bk % MI;
+        const int col = col0 + 32 * j + l32;
         const bool col_ok = !CHECK || col < a.N;
-        float bj = 0.0f;
-        if (want_bias && col_ok) bj = a.bias[col];
-        const uint32_t vc = (uint32_t)(4 * h) * ldc_b + (uint32_t)(col * es);
-        const uint32_t vp = (uint32_t)(4 * h) * ldp_b + (uint32_t)(col * 4);
+        const float bj = bias_j[j];
+        if constexpr (READS) {
+            if (bk + 1 < NB) fetch(bk + 1, nxt_c, nxt_p);
+        }
+        float csum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < MI; ++i) {
+        for (int g = 0; g < 4; ++g) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int u = 32 * i + 8 * g + r;  // wave-uniform row step
-                    const uint32_t sc = (uint32_t)u * ldc_b;
-                    const uint32_t sp = (uint32_t)u * ldp_b;
-                    uint32_t oc = vc, op = vp;
-                    if (CHECK) {
-                        const bool ok = col_ok && (u < row_lim);
-                        oc = ok ? vc : kOob;
-                        op = ok ? vp : kOob;
-                    }
-                    float v = acc[i][j][4 * g + r];
-                    if constexpr (KIND == EK_PLAIN) {
+            for (int r = 0; r < 4; ++r) {
+                const int e = 4 * g + r;
+                uint32_t oc, op, sc, sp;
+                offsets(j, i, g, r, oc, op, sc, sp);
+                float v = acc[i][j][e];
+                if constexpr (KIND == EK_PLAIN) {
+                    st_f32(v, rc, oc, sc);
+                } else if constexpr (KIND == EK_BIAS) {
+                    st_f32(v + bj, rc, oc, sc);
+                } else if constexpr (KIND == EK_BIAS_GELU) {
+                    st_f32(gelu_tanh(v + bj), rc, oc, sc);
+                } else if constexpr (KIND == EK_BIAS_GELU_PRE) {
+                    v += bj;
+                    st_f32(v, rp, op, sp);
+                    st_f32(gelu_tanh(v), rc, oc, sc);
+                } else if constexpr (KIND == EK_ACCUM) {
+                    st_f32(cur_c[e] + v, rc, oc, sc);
+                } else if constexpr (KIND == EK_GELU_BWD) {
+                    v *= gelu_tanh_grad(cur_p[e]);
+                    st_f32(v, rc, oc, sc);
+                    if (!CHECK || oc != kOob) csum += v;
+                } else {
+                    const int epi = a.epi;
+                    if (epi & EPI_ALPHA) v *= a.alpha;
+                    if (epi & EPI_BETA) v += a.beta * cur_c[e];
+                    v += bj;
+                    if (epi & EPI_PREACT) st_f32(v, rp, op, sp);
+                    if (epi & EPI_GELU) v = gelu_tanh(v);
+                    if (epi & EPI_GELU_BWD) v *= gelu_tanh_grad(cur_p[e]);
+                    if (f16out)
+                        st_f16(v, rc, oc, sc);
+                    else
                         st_f32(v, rc, oc, sc);
-                    } else if constexpr (KIND == EK_BIAS) {
-                        st_f32(v + bj, rc, oc, sc);
-                    } else if constexpr (KIND == EK_BIAS_GELU) {
-                        st_f32(gelu_tanh(v + bj), rc, oc, sc);
-                    } else if constexpr (KIND == EK_BIAS_GELU_PRE) {
-                        v += bj;
-                        st_f32(v, rp, op, sp);
-                        st_f32(gelu_tanh(v), rc, oc, sc);
-                    } else if constexpr (KIND == EK_ACCUM) {
-                        st_f32(ld_f32(rc, oc, sc) + v, rc, oc, sc);
-                    } else {
-                        const int epi = a.epi;
-                        if (epi & EPI_ALPHA) v *= a.alpha;
-                        if (epi & EPI_BETA) v += a.beta * (f16out ? ld_f16(rc, oc, sc) : ld_f32(rc, oc, sc));
-                        v += bj;
-                        if (epi & EPI_PREACT) st_f32(v, rp, op, sp);
-                        if (epi & EPI_GELU) v = gelu_tanh(v);
-                        if (f16out)
-                            st_f16(v, rc, oc, sc);
-                        else
-                            st_f32(v, rc, oc, sc);
-                    }
+                    if (!CHECK || oc != kOob) csum += v;
                 }
             }
-            // One 32 x 32 block at a time: keeps the 16 row offsets of a block
-            // short-lived instead of all 32 * MI of them in SGPRs at once.
-            __builtin_amdgcn_sched_barrier(0);
         }
+        if (colsum) {
+            csum += __shfl_xor(csum, 32);
+            if (h == 0 && col_ok) a.cs_part[(int64_t)((row0 >> 5) + i) * a.N + col] = csum;
+        }
+        if constexpr (READS) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                cur_c[e] = nxt_c[e];
+                cur_p[e] = nxt_p[e];
+            }
+        }
+        // One 32 x 32 block at a time: keeps the 16 row offsets of a block
+        // short-lived instead of all 32 * MI of them in SGPRs at once.
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 

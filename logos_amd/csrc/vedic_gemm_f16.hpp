@@ -370,6 +370,7 @@ static hipError_t launch_f16_kind(const GemmArgs& a, hipStream_t s) {
         case EK_BIAS_GELU: return launch_f16<OP, Cfg, EK_BIAS_GELU>(a, s);
         case EK_BIAS_GELU_PRE: return launch_f16<OP, Cfg, EK_BIAS_GELU_PRE>(a, s);
         case EK_ACCUM: return launch_f16<OP, Cfg, EK_ACCUM>(a, s);
+        case EK_GELU_BWD: return launch_f16<OP, Cfg, EK_GELU_BWD>(a, s);
         default: return launch_f16<OP, Cfg, EK_GENERIC>(a, s);
     }
 }

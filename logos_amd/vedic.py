@@ -8,6 +8,8 @@ Names and argument meaning follow the reference:
   gemm_nt(dY, W) / gemm_tn(X, dY)  the NT/TN backward products (include/Backprop.hpp:48-63,
                                    cuda/train_gpu.cu:210-545)
   gemm_bias_gelu(X, W, b)          FeedForward::forward's first half (include/FeedForward.hpp:112-114)
+  gemm_nt_gelu_bwd(dY, W, H)       ffn_da + gelu_bwd + bias_grad (cuda/train_gpu.cu:263-345), fused
+  bias_grad(dY)                    bias_grad_kernel (cuda/train_gpu.cu:263-273), deterministic
   add_bias / gelu_ / cast_*        add_bias_kernel, cuda_gelu, cuda_cast_fp32_to_fp16 ...
   verify(A, B, C)                  cuda_vedic_verify (cuda/VedicGEMM.cu:765-814)
 
@@ -24,12 +26,14 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from ._lib import DT_F16, DT_F32, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU, EPI_NONE, OP_NN, OP_NT, OP_TN
+from ._lib import (DT_F16, DT_F32, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU, EPI_GELU_BWD, EPI_NONE, OP_NN, OP_NT,
+                   OP_TN)
 
 __all__ = [
-    "OP_NN", "OP_NT", "OP_TN", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU", "EPI_GELU",
+    "OP_NN", "OP_NT", "OP_TN", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU", "EPI_GELU", "EPI_GELU_BWD",
     "gemm", "vedic_gemm", "vedic_gemm_bias", "gemm_fp16_fp32out", "gemm_fp16_fp16out",
-    "gemm_bias_gelu", "gemm_nt", "gemm_tn", "add_bias", "gelu_", "cast_fp32_to_fp16",
+    "gemm_bias_gelu", "gemm_nt", "gemm_tn", "gemm_nt_gelu_bwd", "bias_grad", "add_bias", "gelu_",
+    "cast_fp32_to_fp16",
     "cast_fp16_to_fp32", "verify", "VerifyResult", "uses_vendor_blas", "backend_name",
 ]
 
@@ -72,8 +76,13 @@ def _mat(t: torch.Tensor, name: str) -> tuple[int, int, int]:
 def gemm(op: int, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor | None = None, *,
          alpha: float = 1.0, beta: float = 0.0, bias: torch.Tensor | None = None,
          epilogue: int = EPI_NONE, preact: torch.Tensor | None = None,
-         out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
-    """General GEMM: C = epi(alpha * op(A) op(B) + beta * C + bias) (see include/logos_vedic.h)."""
+         out_dtype: torch.dtype = torch.float32, colsum: torch.Tensor | None = None,
+         colsum_beta: float = 0.0) -> torch.Tensor:
+    """General GEMM: C = epi(alpha * op(A) op(B) + beta * C + bias) (see include/logos_vedic.h).
+
+    epilogue=EPI_GELU_BWD multiplies by gelu_tanh'(preact) (preact is then an
+    input).  colsum (N float32 values) receives colsum_beta * colsum + the
+    column sums of the final C."""
     if A.dtype != B.dtype or A.dtype not in _DT:
         raise ValueError(f"A and B must share dtype float16 or float32 (got {A.dtype}, {B.dtype})")
     ar, ac, lda = _mat(A, "A")
@@ -106,12 +115,16 @@ def gemm(op: int, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor | None = Non
         pr, pc, ldp = _mat(preact, "preact")
         if (pr, pc) != (M, N) or preact.dtype != torch.float32:
             raise ValueError(f"preact must be float32 {M}x{N}")
+    if colsum is not None:
+        if colsum.dtype != torch.float32 or colsum.numel() != N or not colsum.is_cuda or not colsum.is_contiguous():
+            raise ValueError(f"colsum must be {N} contiguous float32 values on the GPU")
     d = _lib.GemmDesc(
         op=op, in_dtype=_DT[A.dtype], out_dtype=_DT[C.dtype], M=M, N=N, K=K,
         A=A.data_ptr(), lda=lda, B=B.data_ptr(), ldb=ldb, C=C.data_ptr(), ldc=ldc,
         alpha=alpha, beta=beta, bias=bias.data_ptr() if bias is not None else None,
         epilogue=epilogue, preact=preact.data_ptr() if preact is not None else None,
         ld_preact=ldp, stream=_stream(),
+        colsum=colsum.data_ptr() if colsum is not None else None, colsum_beta=colsum_beta,
     )
     _check(_lib.load().vedic_gemm(ctypes.byref(d)))
     return C
@@ -164,6 +177,30 @@ def gemm_tn(X: torch.Tensor, dY: torch.Tensor, out: torch.Tensor | None = None,
             beta: float = 0.0) -> torch.Tensor:
     """dW = X^T . dY (+ beta dW); X stored [K x M], dY [K x N]."""
     return gemm(OP_TN, X, dY, out, beta=beta)
+
+
+def gemm_nt_gelu_bwd(dY: torch.Tensor, W: torch.Tensor, H: torch.Tensor, out: torch.Tensor | None = None,
+                     db: torch.Tensor | None = None) -> torch.Tensor:
+    """dH = (dY . W^T) * gelu_tanh'(H), W stored [N x K], H the cached
+    pre-activation [M x N]; db (if given) += column sums of dH (the bias
+    gradient).  One fused launch for ffn_da + gelu_bwd + bias_grad."""
+    return gemm(OP_NT, dY, W, out, epilogue=EPI_GELU_BWD, preact=H, colsum=db,
+                colsum_beta=1.0)
+
+
+def bias_grad(dY: torch.Tensor, db: torch.Tensor | None = None, beta: float = 0.0) -> torch.Tensor:
+    """db = beta * db + column sums of dY (bias_grad_kernel), summed in a fixed order."""
+    M, N, ld = _mat(dY, "dY")
+    if ld != N or dY.dtype != torch.float32:
+        raise ValueError("dY must be a contiguous float32 matrix")
+    if db is None:
+        if beta != 0.0:
+            raise ValueError("beta != 0 needs an existing db")
+        db = torch.empty(N, dtype=torch.float32, device=dY.device)
+    if db.numel() != N or db.dtype != torch.float32 or not db.is_contiguous():
+        raise ValueError(f"db must be {N} contiguous float32 values")
+    _check(_lib.load().vedic_bias_grad(dY.data_ptr(), db.data_ptr(), M, N, beta, _stream()))
+    return db
 
 
 def add_bias(C: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:

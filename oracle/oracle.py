@@ -70,6 +70,8 @@ def _load_ref():
             "ref_reference_gemm": [_fp, _fp, _fp, _i, _i, _i],
             "ref_vedic_gemm_bias": [_fp, _fp, _fp, _fp, _i, _i, _i],
             "ref_gelu_inplace": [_fp, ctypes.c_longlong],
+            "ref_gelu_backward": [_fp, _fp, _fp, _i, _i],
+            "ref_bias_backward": [_fp, _fp, _i, _i],
             "ref_gemm_nt": [_fp, _fp, _fp, _i, _i, _i],
             "ref_gemm_tn": [_fp, _fp, _fp, _i, _i, _i, _i],
         }
@@ -270,6 +272,72 @@ def ref_gemm_tn(X, dY, accumulate_into=None) -> np.ndarray:
         out = np.empty((M, N), np.float32)
     if _load_ref().ref_gemm_tn(_p(X), _p(dY), _p(out), M, N, K, 1 if accumulate_into is not None else 0):
         raise ValueError("reference TN threw")
+    return out
+
+
+# ------------------------------------------------------------ backward epilogue
+#
+# GELU backward and the bias gradient (the FFN backward of
+# cuda/train_gpu.cu:579-621): d_ffn_H = d_ffn_A * gelu'(H) (gelu_bwd_kernel,
+# :334-345) and db[j] += sum_s dY[s][j] (bias_grad_kernel, :263-273).
+
+_GELU_C = 0.7978845608  # sqrt(2 / pi) as written in include/FeedForward.hpp:12
+_GELU_A = 0.044715
+
+
+def gelu_f64(x) -> np.ndarray:
+    """tanh-GELU in float64 (include/FeedForward.hpp:11-13)."""
+    x = np.asarray(x, np.float64)
+    return 0.5 * x * (1.0 + np.tanh(_GELU_C * (x + _GELU_A * x ** 3)))
+
+
+def gelu_grad_f64(x) -> np.ndarray:
+    """d/dx of gelu_f64, closed form in float64:
+    0.5 (1 + tanh u) + 0.5 x sech^2(u) c (1 + 3 a x^2), u = c (x + a x^3).
+    Pinned in tests by central differences of gelu_f64 and by its limits."""
+    x = np.asarray(x, np.float64)
+    u = _GELU_C * (x + _GELU_A * x ** 3)
+    th = np.tanh(u)
+    return 0.5 * (1.0 + th) + 0.5 * x * (1.0 - th * th) * _GELU_C * (1.0 + 3.0 * _GELU_A * x * x)
+
+
+def gelu_bwd_reference_f32(dA, H) -> np.ndarray:
+    """The reference's gelu_bwd_kernel (cuda/train_gpu.cu:334-345) restated in
+    float32 arithmetic, step for step: k = c (x + a x x x); th = tanh(k);
+    sech2 = 1 - th th; gp = 0.5 (1 + th) + 0.5 x sech2 c (1 + 3 a x x); dH = dA gp."""
+    x = np.asarray(H, np.float32)
+    f = np.float32
+    k = f(_GELU_C) * (x + f(_GELU_A) * x * x * x)
+    th = np.tanh(k).astype(np.float32)
+    sech2 = f(1.0) - th * th
+    gp = f(0.5) * (f(1.0) + th) + f(0.5) * x * sech2 * f(_GELU_C) * (f(1.0) + f(3.0) * f(_GELU_A) * x * x)
+    return (np.asarray(dA, np.float32) * gp).astype(np.float32)
+
+
+def colsum_f64(X) -> np.ndarray:
+    """Column sums in float64: the bias gradient db[j] = sum_s dY[s][j]."""
+    return np.asarray(X, np.float64).sum(axis=0)
+
+
+def ref_gelu_backward(H, dA) -> np.ndarray:
+    """The reference's own CPU gelu_backward (include/Backprop.hpp:71-89)."""
+    H = _f32(H)
+    H2 = H.reshape(1, -1) if H.ndim == 1 else H
+    dA2 = _f32(dA).reshape(H2.shape)
+    M, N = H2.shape
+    out = np.empty_like(H2)
+    if _load_ref().ref_gelu_backward(_p(H2), _p(dA2), _p(out), M, N):
+        raise ValueError("reference gelu_backward threw")
+    return out.reshape(H.shape)
+
+
+def ref_bias_backward(dY) -> np.ndarray:
+    """The reference's own CPU bias_backward (include/Backprop.hpp:93-101)."""
+    dY = _f32(dY)
+    M, N = dY.shape
+    out = np.empty(N, np.float32)
+    if _load_ref().ref_bias_backward(_p(dY), _p(out), M, N):
+        raise ValueError("reference bias_backward threw")
     return out
 
 

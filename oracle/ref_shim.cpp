@@ -11,8 +11,11 @@
 //   ref_gelu_inplace     -> gelu                 include/FeedForward.hpp:11-13
 //   ref_gemm_nt / _tn    -> Tensor::transpose + vedic_gemm, as
 //                           gemm_backward does (include/Backprop.hpp:48-63)
+//   ref_gelu_backward    -> gelu_backward        include/Backprop.hpp:71-89
+//   ref_bias_backward    -> bias_backward        include/Backprop.hpp:93-101
 #include "VedicGEMM.hpp"
 #include "FeedForward.hpp"
+#include "Backprop.hpp"
 
 #include <algorithm>
 #include <cstring>
@@ -83,6 +86,26 @@ int ref_gemm_tn(const float* X, const float* dY, float* dW, int M, int N, int K,
         } else {
             put(prod, dW);
         }
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+// dX[M x N] = dY * GELU'(X), X the pre-activation.
+int ref_gelu_backward(const float* X, const float* dY, float* dX, int M, int N) {
+    try {
+        put(gelu_backward(make(X, M, N), make(dY, M, N)), dX);
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+// db[N] = sum over the M rows of dY, row by row in fp32.
+int ref_bias_backward(const float* dY, float* db, int M, int N) {
+    try {
+        put(bias_backward(make(dY, M, N)), db);
         return 0;
     } catch (...) {
         return -1;

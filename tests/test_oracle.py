@@ -197,6 +197,78 @@ def test_gelu_special_values():
     assert np.allclose(y[3:], g(x[3:].astype(np.float64)), rtol=1e-6)
 
 
+def test_gelu_grad_closed_form_pinned():
+    """The fp64 GELU derivative against central differences of the fp64 GELU
+    (h = 1e-5: truncation ~1e-11, rounding ~1e-11), and its limits and
+    special values; a dropped term, a wrong sign or a missing factor 3 in the
+    x^2 term moves it by far more than the tolerance."""
+    x = np.concatenate([np.linspace(-8, 8, 4001), [-30.0, -5.5, 0.0, 1e-3, 2.5, 30.0]])
+    h = 1e-5
+    fd = (o.gelu_f64(x + h) - o.gelu_f64(x - h)) / (2 * h)
+    g = o.gelu_grad_f64(x)
+    assert np.max(np.abs(g - fd)) < 1e-8
+    assert o.gelu_grad_f64(0.0) == 0.5
+    assert abs(o.gelu_grad_f64(30.0) - 1.0) < 1e-15 and abs(o.gelu_grad_f64(-30.0)) < 1e-15
+    # the derivative overshoots 1 just right of x ~ 1.5 and dips below 0 near x ~ -1.5
+    assert o.gelu_grad_f64(2.0) > 1.0 and o.gelu_grad_f64(-1.5) < 0.0
+    # a planted mistake (factor 3 dropped) is caught by the same check
+    u = 0.7978845608 * (x + 0.044715 * x ** 3)
+    bad = 0.5 * (1 + np.tanh(u)) + 0.5 * x * (1 - np.tanh(u) ** 2) * 0.7978845608 * (1 + 0.044715 * x * x)
+    assert np.max(np.abs(bad - fd)) > 1e-3
+
+
+def test_gelu_bwd_reference_restatement():
+    """The fp32 restatement of the reference's gelu_bwd_kernel agrees with the
+    fp64 closed form to fp32 rounding (a few ulp of the result)."""
+    rng = np.random.default_rng(5)
+    H = (rng.standard_normal(20000) * 3).astype(np.float32)
+    dA = rng.standard_normal(20000).astype(np.float32)
+    got = o.gelu_bwd_reference_f32(dA, H)
+    want = dA.astype(np.float64) * o.gelu_grad_f64(H)
+    assert np.max(np.abs(got - want)) <= 1e-6 * np.max(np.abs(want))
+
+
+@pytest.mark.skipif(not o.ref_available(), reason="reference CPU build (oracle/_ref) not present")
+def test_gelu_bwd_and_bias_grad_against_reference_build():
+    """The fp32 restatement of GELU backward against the reference's own
+    gelu_backward (include/Backprop.hpp:71-89), and the fp64 column sums
+    against its bias_backward (:93-101).  The formula forms 0.5 (1 + tanh u)
+    and sech^2 u = 1 - tanh^2 u with tanh u near +-1 in the tails, so both
+    carry an absolute error of a few ulp of 1 times the factors that multiply
+    them, |dA| (1 + |x| c (1 + 3 a x^2)) (the reference's fp32 tanh saturates
+    to -1 below x ~ -5 and its derivative cancels to 0 there); the two tanh
+    implementations (numpy float32, libm tanhf) may also differ in the last
+    place.  The reference's row-by-row fp32 column sum is held to M u sum|x|."""
+    rng = np.random.default_rng(13)
+    H = (rng.standard_normal((300, 77)) * 3).astype(np.float32)
+    dA = rng.standard_normal((300, 77)).astype(np.float32)
+    ref = o.ref_gelu_backward(H, dA)
+    got = o.gelu_bwd_reference_f32(dA, H)
+    x = np.abs(H.astype(np.float64))
+    scale = 2.0 ** -23 * np.abs(dA) * (1 + x * 0.8 * (1 + 0.134145 * x * x))
+    assert np.all(np.abs(got - ref) <= 4 * scale + 4 * np.spacing(np.abs(ref)))
+    want64 = dA.astype(np.float64) * o.gelu_grad_f64(H)
+    assert np.all(np.abs(ref - want64) <= 4 * scale + 4 * np.spacing(np.abs(ref)))
+    dY = rng.standard_normal((2000, 33)).astype(np.float32)
+    db = o.ref_bias_backward(dY)
+    bound = 2000 * 2.0 ** -24 * np.abs(dY).astype(np.float64).sum(0)
+    assert np.all(np.abs(db - o.colsum_f64(dY)) <= bound)
+
+
+def test_colsum_blocked_order_bound():
+    """Column sums added block by block (as the GPU path does: 32- or 64-row
+    blocks, then the blocks in order) stay within the blocked-summation bound
+    of the fp64 sums."""
+    rng = np.random.default_rng(9)
+    X = rng.standard_normal((1000, 37)).astype(np.float32)
+    blocks = [X[i:i + 256].sum(axis=0, dtype=np.float32) for i in range(0, 1000, 256)]
+    got = np.zeros(37, np.float32)
+    for b in blocks:
+        got = (got + b).astype(np.float32)
+    bound = (256 + len(blocks)) * 2.0 ** -24 * np.abs(X).astype(np.float64).sum(axis=0)
+    assert np.all(np.abs(got - o.colsum_f64(X)) <= bound)
+
+
 def test_checksum_identity():
     rng = np.random.default_rng(7)
     A = rng.standard_normal((50, 30), dtype=np.float32)
