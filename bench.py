@@ -45,8 +45,8 @@ HBM_PEAK_GBS = 8000.0                   # MI355X HBM3E, GB/s (published)
 
 # One GEMM: (M, K, N, op, dtype, epilogue, beta).  op as stored:
 #   NN A[MxK] B[KxN]; NT A[MxK] B[NxK]; TN A[KxM] B[KxN].
-def _g(M, K, N, op="NN", dtype="fp16", epi="none", beta=0.0):
-    return dict(M=M, K=K, N=N, op=op, dtype=dtype, epi=epi, beta=beta)
+def _g(M, K, N, op="NN", dtype="fp16", epi="none", beta=0.0, checked=False):
+    return dict(M=M, K=K, N=N, op=op, dtype=dtype, epi=epi, beta=beta, checked=checked)
 
 
 # BASELINE.json configs; each workload is a list of GEMMs run back to back per step.
@@ -60,6 +60,9 @@ WORKLOADS = {
     "ffn_bwd_dh_gelu_nt_fp16": dict(cfg=3, gemms=[_g(8192, 1024, 4096, op="NT", epi="gelu_bwd")]),
     "lm_head_fp16": dict(cfg=4, gemms=[_g(8192, 1024, 8192)]),
     "lm_head_fp32": dict(cfg=4, gemms=[_g(8192, 1024, 8192, dtype="fp32")]),
+    # the LM-head GEMM with its Gunitasamuchayah check computed on the way (SURVEY next-row 3);
+    # synchronous per step, like the reference's verify
+    "lm_head_fp16_checked": dict(cfg=4, gemms=[_g(8192, 1024, 8192, checked=True)]),
     **{f"decode_fp16_m{m}": dict(cfg=4, hbm=True, gemms=[_g(m, 1024, 8192)]) for m in (1, 2, 4, 8, 16, 32)},
     **{f"decode_fp32_m{m}": dict(cfg=4, hbm=True, gemms=[_g(m, 1024, 8192, dtype="fp32")]) for m in (1, 32)},
     # one 219M-model block at d=1024, seq=8192: 4 forward GEMMs + their dX (NT) and dW (TN, beta=1)
@@ -264,15 +267,20 @@ def make_step(w: dict, dev, torch):
         hbm = (M * K + K * N) * es + M * N * 4 * (2 if g["beta"] else 1) + (N * 4 if g["epi"] != "none" else 0)
         if gbwd:
             hbm += M * N * 4 + N * 4  # H read, db read and written
+        if g["checked"]:
+            hbm += (M * K + K * N) * es  # one more pass over A and B for the prediction
         items.append((d, 2.0 * M * N * K, hbm))
-    ptrs = [ctypes.byref(d) for d, _, _ in items]
+    ptrs = [(ctypes.byref(d), g["checked"]) for (d, _, _), g in zip(items, w["gemms"])]
     gemm = lib.vedic_gemm
+    vres = _lib.VerifyResult()
 
     def step():
-        for p in ptrs:
-            rc = gemm(p)
+        for p, checked in ptrs:
+            rc = lib.vedic_gemm_checked(p, 0.05, ctypes.byref(vres)) if checked else gemm(p)
             if rc:
                 raise RuntimeError(f"vedic_gemm failed: {_lib.status_string(rc)}")
+            if checked and not vres.pass_:
+                raise RuntimeError(f"checksum failed: rel err {vres.relative_error}")
 
     step.keep = keep  # inputs stay alive with the closure
     return step, items

@@ -214,6 +214,16 @@ typedef struct {
 int vedic_verify(const float* A, const float* B, const float* C, int M, int K, int N,
                  float tolerance, vedic_verify_result_t* out, void* stream);
 
+/* The GEMM `desc` with the same check computed on the way (algorithm-based
+ * fault tolerance): sum(C) from column sums the GEMM's epilogue accumulates,
+ * so C is not read again, against colsum(op(A)) . rowsum(op(B)) (times alpha,
+ * plus M * sum(bias) with VEDIC_EPI_BIAS) from one pass over A and B, in
+ * double.  Any op and input dtype; fp32 C; epilogue NONE or BIAS; beta = 0;
+ * desc->colsum must be NULL.  Synchronous, like vedic_verify.  New: the
+ * reference verifies with a separate pass over C at checkpoints
+ * (cuda/train_gpu.cu:1695-1719). */
+int vedic_gemm_checked(const vedic_gemm_desc_t* desc, float tolerance, vedic_verify_result_t* out);
+
 /* ---- backend queries --------------------------------------------------- */
 
 /* Always 0: no vendor BLAS is linked.

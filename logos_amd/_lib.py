@@ -95,6 +95,7 @@ SIGNATURES = {
         c_int,
         [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_float, ctypes.POINTER(VerifyResult), c_vp],
     ),
+    "vedic_gemm_checked": (c_int, [ctypes.POINTER(GemmDesc), c_float, ctypes.POINTER(VerifyResult)]),
     "vedic_uses_vendor_blas": (c_int, []),
     "vedic_backend_name": (c_char_p, []),
     "vedic_status_string": (c_char_p, [c_int]),

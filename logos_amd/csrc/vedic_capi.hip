@@ -565,6 +565,109 @@ __global__ void arraysum_kernel(const float* __restrict__ x, int64_t n, double* 
     if (threadIdx.x == 0) out[blockIdx.x] = red[0];
 }
 
+// Sums in double over one dimension of a strided matrix of T (float or
+// binary16), for the checked GEMM: along_rows = true gives, for each column c,
+// sum_r X[r][c]; false gives, for each row r, sum_c X[r][c].  One thread per
+// output; rows are read as contiguous segments across threads when summing
+// columns, and with a fixed stride-64 tree when summing rows.
+// Column sums in two fixed-order levels: part[q][c] over the rows of chunk q
+// (kDsumChunk rows), then the chunks in ascending q.
+constexpr int kDsumChunk = 64;
+
+template <typename T>
+__global__ void dsum_cols_partial_kernel(const T* __restrict__ X, int64_t ld, int rows, int cols,
+                                         double* __restrict__ part) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= cols) return;
+    const int r0 = blockIdx.y * kDsumChunk, r1 = min(rows, r0 + kDsumChunk);
+    double s = 0.0;
+#pragma unroll 4
+    for (int r = r0; r < r1; ++r) s += (double)X[(int64_t)r * ld + c];
+    part[(int64_t)blockIdx.y * cols + c] = s;
+}
+
+// 32 columns per workgroup, 8 groups of 32 threads each adding a contiguous
+// run of chunks in ascending order, then the 8 group sums in ascending order.
+__global__ void __launch_bounds__(256) dsum_cols_reduce_kernel(const double* __restrict__ part, int nchunks,
+                                                               int cols, double* __restrict__ out) {
+    __shared__ double sh[8][32];
+    const int c = threadIdx.x & 31, g = threadIdx.x >> 5;
+    const int col = blockIdx.x * 32 + c;
+    const int q = (nchunks + 7) / 8;
+    const int q0 = min(nchunks, g * q), q1 = min(nchunks, q0 + q);
+    double s = 0.0;
+    if (col < cols)
+        for (int k = q0; k < q1; ++k) s += part[(int64_t)k * cols + col];
+    sh[g][c] = s;
+    __syncthreads();
+    if (g == 0 && col < cols) {
+        double t = sh[0][c];
+        for (int k = 1; k < 8; ++k) t += sh[k][c];
+        out[col] = t;
+    }
+}
+
+// res[0] = sum_j cs[j], res[1] = sum_k sa[k] sb[k], res[2] = sum_j bias[j]
+// (bias may be null), each by one workgroup with a fixed stride-256 order and
+// a fixed tree.
+__global__ void __launch_bounds__(256) checksum_finalize_kernel(const float* __restrict__ cs, int N,
+                                                                const double* __restrict__ sa,
+                                                                const double* __restrict__ sb, int K,
+                                                                const float* __restrict__ bias,
+                                                                double* __restrict__ res) {
+    __shared__ double red[3][256];
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0;
+    for (int j = threadIdx.x; j < N; j += 256) {
+        s0 += (double)cs[j];
+        if (bias) s2 += (double)bias[j];
+    }
+    for (int k = threadIdx.x; k < K; k += 256) s1 += sa[k] * sb[k];
+    red[0][threadIdx.x] = s0;
+    red[1][threadIdx.x] = s1;
+    red[2][threadIdx.x] = s2;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w)
+            for (int t = 0; t < 3; ++t) red[t][threadIdx.x] += red[t][threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x < 3) res[threadIdx.x] = red[threadIdx.x][0];
+}
+
+template <typename T>
+__global__ void dsum_rows_kernel(const T* __restrict__ X, int64_t ld, int cols, double* __restrict__ out) {
+    __shared__ double red[kEwThreads];
+    const int64_t base = (int64_t)blockIdx.x * ld;
+    double s = 0.0;
+    for (int c = threadIdx.x; c < cols; c += kEwThreads) s += (double)X[base + c];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = kEwThreads / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = red[0];
+}
+
+// Doubles of scratch launch_dsum needs for a column sum of `rows` x `cols`.
+static size_t dsum_scratch(int rows, int cols, bool along_rows) {
+    return along_rows ? (size_t)((rows + kDsumChunk - 1) / kDsumChunk) * cols : 0;
+}
+
+template <typename T>
+static void launch_dsum(const T* X, int64_t ld, int rows, int cols, bool along_rows, double* out, double* scratch,
+                        hipStream_t s) {
+    if (along_rows) {
+        const int nq = (rows + kDsumChunk - 1) / kDsumChunk;
+        hipLaunchKernelGGL(dsum_cols_partial_kernel<T>, dim3((unsigned)((cols + 255) / 256), (unsigned)nq),
+                           dim3(256), 0, s, X, ld, rows, cols, scratch);
+        hipLaunchKernelGGL(dsum_cols_reduce_kernel, dim3((unsigned)((cols + 31) / 32)), dim3(256), 0, s, scratch,
+                           nq, cols, out);
+    } else {
+        hipLaunchKernelGGL(dsum_rows_kernel<T>, dim3((unsigned)rows), dim3(kEwThreads), 0, s, X, ld, cols, out);
+    }
+}
+
 }  // namespace
 
 extern "C" int vedic_add_bias(float* C, const float* bias, int M, int N, void* stream) {
@@ -635,6 +738,72 @@ extern "C" int vedic_verify(const float* A, const float* B, const float* C, int 
     out->relative_error = fabsf(out->checksum_C - out->checksum_vedic) / (fabsf(out->checksum_vedic) + 1e-6f);
     out->pass = out->relative_error < tolerance;
     return VEDIC_STATUS_OK;
+}
+
+// The GEMM with its Gunitasamuchayah check computed on the way: the column
+// sums of C come from the GEMM's epilogue (C is not read again), and the
+// prediction colsum(op(A)) . rowsum(op(B)) from one pass over A and B.
+extern "C" int vedic_gemm_checked(const vedic_gemm_desc_t* d, float tolerance, vedic_verify_result_t* out) {
+    if (!d || !out) return VEDIC_STATUS_NULL_POINTER;
+    // the identity holds for alpha * A.B (+ bias): no beta, GELU or fp16 C
+    if (d->colsum || d->beta != 0.0f || d->out_dtype != VEDIC_DT_F32 ||
+        (d->epilogue != VEDIC_EPI_NONE && d->epilogue != VEDIC_EPI_BIAS) || d->preact)
+        return VEDIC_STATUS_BAD_EPILOGUE;
+    if (d->M <= 0 || d->N <= 0 || d->K <= 0) return VEDIC_STATUS_BAD_DIM;
+    if (!d->A || !d->B) return VEDIC_STATUS_NULL_POINTER;
+    hipStream_t s = static_cast<hipStream_t>(d->stream);
+    const int M = d->M, N = d->N, K = d->K;
+    const bool want_bias = d->epilogue == VEDIC_EPI_BIAS && d->bias;
+    const bool a_rows = d->op != VEDIC_OP_TN;  // A stored [M x K]: sum down its rows
+    const bool b_rows = d->op == VEDIC_OP_NT;  // B stored [N x K]: sum down its rows
+    const int ar = a_rows ? M : K, ac = a_rows ? K : M;
+    const int br = b_rows ? N : K, bc = b_rows ? K : N;
+    // workspace: colsum(C) [N] fp32 (padded to 8 bytes) | sa [K] | sb [K] |
+    // scratch of the column sums | 3 result doubles
+    const size_t fbytes = (sizeof(float) * (size_t)N + 7) / 8 * 8;
+    const size_t bytes = fbytes + sizeof(double) * ((size_t)K * 2 + 3);
+    const size_t scr_a = dsum_scratch(ar, ac, a_rows), scr_b = dsum_scratch(br, bc, b_rows);
+    char* ws = nullptr;
+    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), bytes + sizeof(double) * (scr_a + scr_b), s);
+    if (e != hipSuccess) return hip_status(e);
+    float* d_cs = reinterpret_cast<float*>(ws);
+    double* d_sa = reinterpret_cast<double*>(ws + fbytes);
+    double* d_sb = d_sa + K;
+    double* d_scr_a = d_sb + K;
+    double* d_scr_b = d_scr_a + scr_a;
+    vedic_gemm_desc_t g = *d;
+    g.colsum = d_cs;
+    g.colsum_beta = 0.0f;
+    int st = vedic_gemm(&g);
+    if (st == VEDIC_STATUS_OK) {
+        // sa[k] = sum_m op(A)[m][k]; sb[k] = sum_n op(B)[k][n]
+        if (d->in_dtype == VEDIC_DT_F16) {
+            launch_dsum(static_cast<const _Float16*>(d->A), d->lda, ar, ac, a_rows, d_sa, d_scr_a, s);
+            launch_dsum(static_cast<const _Float16*>(d->B), d->ldb, br, bc, b_rows, d_sb, d_scr_b, s);
+        } else {
+            launch_dsum(static_cast<const float*>(d->A), d->lda, ar, ac, a_rows, d_sa, d_scr_a, s);
+            launch_dsum(static_cast<const float*>(d->B), d->ldb, br, bc, b_rows, d_sb, d_scr_b, s);
+        }
+        double* d_res = d_scr_b + scr_b;  // 3 doubles
+        hipLaunchKernelGGL(checksum_finalize_kernel, dim3(1), dim3(256), 0, s, d_cs, N, d_sa, d_sb, K,
+                           want_bias ? d->bias : nullptr, d_res);
+        e = hipGetLastError();
+        double host[3] = {0.0, 0.0, 0.0};
+        if (e == hipSuccess) e = hipMemcpyAsync(host, d_res, sizeof(host), hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e == hipSuccess) {
+            const double pred = (double)d->alpha * host[1] + (double)M * host[2];
+            out->checksum_C = (float)host[0];
+            out->checksum_vedic = (float)pred;
+            out->relative_error =
+                fabsf(out->checksum_C - out->checksum_vedic) / (fabsf(out->checksum_vedic) + 1e-6f);
+            out->pass = out->relative_error < tolerance;
+        }
+        st = hip_status(e);
+    }
+    const hipError_t f = hipFreeAsync(ws, s);
+    if (st == VEDIC_STATUS_OK && f != hipSuccess) st = hip_status(f);
+    return st;
 }
 
 // --------------------------------------------------------------- queries

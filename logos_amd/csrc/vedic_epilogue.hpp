@@ -25,10 +25,12 @@ enum EpiKind : int {
     EK_ACCUM = 4,          // C = C + acc           (beta = 1, the dW accumulation)
     EK_GENERIC = 5,        // any flag combination (runtime flags)
     EK_GELU_BWD = 6,       // C = acc * gelu'(P)    (+ column sums if cs_part)
+    EK_LINEAR_CS = 7,      // C = alpha acc (+ b), with column sums
 };
 
 __host__ __device__ inline int epi_kind_of(int epi, float alpha, float beta) {
     if ((epi & ~EPI_COLSUM) == EPI_GELU_BWD) return EK_GELU_BWD;
+    if ((epi & EPI_COLSUM) && (epi & ~(EPI_COLSUM | EPI_ALPHA | EPI_BIAS)) == 0) return EK_LINEAR_CS;
     if (epi & EPI_COLSUM) return EK_GENERIC;
     if (epi == 0) return EK_PLAIN;
     if (epi == EPI_BIAS) return EK_BIAS;
@@ -81,11 +83,11 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, const float16_t (&ac
     // column sums: per lane over its 16 rows of each 32-row block, then the
     // two half-waves (lanes l and l ^ 32 hold the same column) added in a
     // fixed order; rows past M do not count
-    const bool colsum = (KIND == EK_GELU_BWD || KIND == EK_GENERIC) && a.cs_part != nullptr;
+    const bool colsum = (KIND == EK_GELU_BWD || KIND == EK_GENERIC || KIND == EK_LINEAR_CS) && a.cs_part != nullptr;
     const uint32_t ldc_b = (uint32_t)(a.ldc * es);
     const uint32_t ldp_b = (uint32_t)(a.ldp * 4);
     const bool want_bias = (KIND == EK_BIAS || KIND == EK_BIAS_GELU || KIND == EK_BIAS_GELU_PRE) ||
-                           (KIND == EK_GENERIC && (a.epi & EPI_BIAS));
+                           ((KIND == EK_GENERIC || KIND == EK_LINEAR_CS) && (a.epi & EPI_BIAS));
     const int row_lim = a.M - row0 - 4 * h;  // rows 4h + u of the tile exist iff u < row_lim
     // Kinds that read memory per element (the old C, the pre-activation) load
     // a whole 32 x 32 block's values before they are needed: the next block's
@@ -162,6 +164,10 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, const float16_t (&ac
                     st_f32(cur_c[e] + v, rc, oc, sc);
                 } else if constexpr (KIND == EK_GELU_BWD) {
                     v *= gelu_tanh_grad(cur_p[e]);
+                    st_f32(v, rc, oc, sc);
+                    if (!CHECK || oc != kOob) csum += v;
+                } else if constexpr (KIND == EK_LINEAR_CS) {
+                    v = __builtin_fmaf(v, a.alpha, bj);
                     st_f32(v, rc, oc, sc);
                     if (!CHECK || oc != kOob) csum += v;
                 } else {

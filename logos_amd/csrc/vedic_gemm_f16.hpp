@@ -371,6 +371,7 @@ static hipError_t launch_f16_kind(const GemmArgs& a, hipStream_t s) {
         case EK_BIAS_GELU_PRE: return launch_f16<OP, Cfg, EK_BIAS_GELU_PRE>(a, s);
         case EK_ACCUM: return launch_f16<OP, Cfg, EK_ACCUM>(a, s);
         case EK_GELU_BWD: return launch_f16<OP, Cfg, EK_GELU_BWD>(a, s);
+        case EK_LINEAR_CS: return launch_f16<OP, Cfg, EK_LINEAR_CS>(a, s);
         default: return launch_f16<OP, Cfg, EK_GENERIC>(a, s);
     }
 }

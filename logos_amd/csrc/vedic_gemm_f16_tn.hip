@@ -12,6 +12,7 @@ template __global__ void gemm_f16_kernel<2, CfgLarge::BM, CfgLarge::BN, CfgLarge
 template __global__ void gemm_f16_kernel<2, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_ACCUM>(GemmArgs);
 template __global__ void gemm_f16_kernel<2, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_GENERIC>(GemmArgs);
 template __global__ void gemm_f16_kernel<2, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_GELU_BWD>(GemmArgs);
+template __global__ void gemm_f16_kernel<2, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_LINEAR_CS>(GemmArgs);
 template __global__ void gemm_f16_kernel<2, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_PLAIN>(GemmArgs);
 template __global__ void gemm_f16_kernel<2, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_BIAS>(GemmArgs);
 template __global__ void gemm_f16_kernel<2, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_BIAS_GELU>(GemmArgs);
@@ -19,6 +20,7 @@ template __global__ void gemm_f16_kernel<2, CfgSmall::BM, CfgSmall::BN, CfgSmall
 template __global__ void gemm_f16_kernel<2, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_ACCUM>(GemmArgs);
 template __global__ void gemm_f16_kernel<2, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_GENERIC>(GemmArgs);
 template __global__ void gemm_f16_kernel<2, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_GELU_BWD>(GemmArgs);
+template __global__ void gemm_f16_kernel<2, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_LINEAR_CS>(GemmArgs);
 
 hipError_t launch_gemm_f16_direct_tn(const GemmArgs& a, hipStream_t s) {
     return launch_gemm_f16_direct_op<2>(a, s);

@@ -300,6 +300,7 @@ hipError_t launch_gemm_f32_direct_op(const GemmArgs& a, hipStream_t s) {
         case EK_BIAS_GELU_PRE: return launch_f32<OP, EK_BIAS_GELU_PRE>(a, s);
         case EK_ACCUM: return launch_f32<OP, EK_ACCUM>(a, s);
         case EK_GELU_BWD: return launch_f32<OP, EK_GELU_BWD>(a, s);
+        case EK_LINEAR_CS: return launch_f32<OP, EK_LINEAR_CS>(a, s);
         default: return launch_f32<OP, EK_GENERIC>(a, s);
     }
 }

@@ -34,7 +34,7 @@ __all__ = [
     "gemm", "vedic_gemm", "vedic_gemm_bias", "gemm_fp16_fp32out", "gemm_fp16_fp16out",
     "gemm_bias_gelu", "gemm_nt", "gemm_tn", "gemm_nt_gelu_bwd", "bias_grad", "add_bias", "gelu_",
     "cast_fp32_to_fp16",
-    "cast_fp16_to_fp32", "verify", "VerifyResult", "uses_vendor_blas", "backend_name",
+    "cast_fp16_to_fp32", "verify", "gemm_checked", "VerifyResult", "uses_vendor_blas", "backend_name",
 ]
 
 _DT = {torch.float32: DT_F32, torch.float16: DT_F16}
@@ -265,6 +265,39 @@ def verify(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, tolerance: float =
     _check(_lib.load().vedic_verify(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, K, N, tolerance,
                                     ctypes.byref(r), _stream()))
     return VerifyResult(r.checksum_C, r.checksum_vedic, r.relative_error, bool(r.pass_))
+
+
+def gemm_checked(op: int, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor | None = None, *,
+                 alpha: float = 1.0, bias: torch.Tensor | None = None,
+                 tolerance: float = 0.01) -> tuple[torch.Tensor, VerifyResult]:
+    """C = alpha op(A) op(B) (+ bias) with the Gunitasamuchayah check computed on
+    the way: sum(C) from the GEMM's own column sums (C is not read again)
+    against colsum(op(A)) . rowsum(op(B)).  Synchronous, like verify()."""
+    if A.dtype != B.dtype or A.dtype not in _DT:
+        raise ValueError("A and B must share dtype float16 or float32")
+    ar, ac, lda = _mat(A, "A")
+    br, bc, ldb = _mat(B, "B")
+    M, K, N, Kb = {OP_NN: (ar, ac, bc, br), OP_NT: (ar, ac, br, bc), OP_TN: (ac, ar, bc, br)}[op]
+    if Kb != K:
+        raise ValueError(f"VedicGEMM: inner dimensions differ (A gives K={K}, B gives K={Kb})")
+    if C is None:
+        C = torch.empty((M, N), dtype=torch.float32, device=A.device)
+    cr, cc, ldc = _mat(C, "C")
+    if (cr, cc) != (M, N) or C.dtype != torch.float32:
+        raise ValueError(f"C must be float32 {M}x{N}")
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != N):
+        raise ValueError(f"bias must be {N} float32 values")
+    bias = bias.contiguous() if bias is not None else None
+    d = _lib.GemmDesc(
+        op=op, in_dtype=_DT[A.dtype], out_dtype=DT_F32, M=M, N=N, K=K,
+        A=A.data_ptr(), lda=lda, B=B.data_ptr(), ldb=ldb, C=C.data_ptr(), ldc=ldc,
+        alpha=alpha, beta=0.0, bias=bias.data_ptr() if bias is not None else None,
+        epilogue=EPI_BIAS if bias is not None else EPI_NONE, preact=None, ld_preact=0, stream=_stream(),
+        colsum=None, colsum_beta=0.0,
+    )
+    r = _lib.VerifyResult()
+    _check(_lib.load().vedic_gemm_checked(ctypes.byref(d), tolerance, ctypes.byref(r)))
+    return C, VerifyResult(r.checksum_C, r.checksum_vedic, r.relative_error, bool(r.pass_))
 
 
 def uses_vendor_blas() -> bool:

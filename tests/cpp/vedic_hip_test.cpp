@@ -92,6 +92,12 @@ static double gelu64(double x) {
     return 0.5 * x * (1.0 + std::tanh(0.7978845608028654 * (x + 0.044715 * x * x * x)));
 }
 
+static double gelu_grad64(double x) {
+    const double c = 0.7978845608028654, a = 0.044715;
+    const double t = std::tanh(c * (x + a * x * x * x));
+    return 0.5 * (1.0 + t) + 0.5 * x * (1.0 - t * t) * c * (1.0 + 3.0 * a * x * x);
+}
+
 static void test_known_answers() {
     GPUTensor A = upload({1, 2, 3, 4}, 2, 2), B = upload({5, 6, 7, 8}, 2, 2), C = gpu_alloc(2, 2);
     cuda_vedic_gemm(A, B, C);
@@ -161,6 +167,45 @@ static void test_fp32_layouts() {
     for (size_t i = 0; i < tn.size(); ++i) tn[i] += pre[i];
     e = inf_rel(download(dW), tn);
     EXPECT(e <= 1e-5 * std::sqrt((double)M) * 2, "fp32 TN accumulate err %.3e", e);
+}
+
+// FFN backward through the activation, fused (cuda_vedic_gemm_nt_gelu_bwd), and
+// the deterministic bias gradient (cuda_bias_grad).
+static void test_backward_fusion() {
+    Rng r(77);
+    const int M = 150, N = 97, K = 60;
+    const double tol = 1e-5 * std::sqrt((double)K);
+    auto dy = rand_vec(r, (size_t)M * K), w = rand_vec(r, (size_t)N * K), h = rand_vec(r, (size_t)M * N, 3.0);
+    GPUTensor dY = upload(dy, M, K), W = upload(w, N, K), H = upload(h, M, N), dH = gpu_alloc(M, N);
+    GPUTensor db = upload(std::vector<float>(N, 1.0f), 1, N);
+    cuda_vedic_gemm_nt_gelu_bwd(dY, W, H, dH, db.data);
+    auto t = ref_gemm(NT, dy, w, M, N, K);
+    for (size_t i = 0; i < t.size(); ++i) t[i] *= gelu_grad64(h[i]);
+    auto got = download(dH);
+    double e = inf_rel(got, t);
+    EXPECT(e <= tol, "fp32 NT gelu-backward err %.3e", e);
+    // db = 1 + column sums of dH, against the sums of the returned dH
+    auto g = download(db);
+    for (int j = 0; j < N; ++j) {
+        double s = 1.0, a = 1.0;
+        for (int i = 0; i < M; ++i) {
+            s += got[(size_t)i * N + j];
+            a += std::fabs(got[(size_t)i * N + j]);
+        }
+        EXPECT(std::fabs(g[j] - s) <= 1e-6 * a, "bias grad column %d: %.9g vs %.9g", j, g[j], s);
+    }
+    // standalone: db2 = column sums of dY (beta = 0)
+    GPUTensor db2 = gpu_alloc(1, K);
+    cuda_bias_grad(dY.data, db2.data, M, K, 0.0f);
+    auto g2 = download(db2);
+    for (int j = 0; j < K; ++j) {
+        double s = 0.0, a = 0.0;
+        for (int i = 0; i < M; ++i) {
+            s += dy[(size_t)i * K + j];
+            a += std::fabs(dy[(size_t)i * K + j]);
+        }
+        EXPECT(std::fabs(g2[j] - s) <= 1e-6 * a + 1e-30, "bias_grad column %d", j);
+    }
 }
 
 static void test_fp16_path() {
@@ -284,6 +329,8 @@ int main() {
         std::printf("known answers done\n");
         test_fp32_layouts();
         std::printf("fp32 layouts done\n");
+        test_backward_fusion();
+        std::printf("backward fusion done\n");
         test_fp16_path();
         std::printf("fp16 path done\n");
         test_errors_and_verify();

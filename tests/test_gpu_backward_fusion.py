@@ -197,3 +197,58 @@ def test_bias_grad(shape, beta):
     db2 = dev(db0)
     vedic.bias_grad(dev(dY), db2, beta=beta)
     assert np.array_equal(host(db2), got)
+
+
+# ----------------------------------------------- the checksum in the epilogue
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("opname,layout", [("NN", 0), ("NT", 1), ("TN", 2)])
+def test_gemm_checked_sums(dtype, opname, layout):
+    """The checked GEMM: C identical to the plain call; checksum_C the sum of
+    the returned C (fp32 column sums, added in double); checksum_vedic the
+    prediction colsum(op(A)) . rowsum(op(B)) + M sum(bias), in double."""
+    vedic = V()
+    M, N, K = 300, 264, 520
+    rng = np.random.default_rng(zlib.crc32(f"checked-{dtype}-{opname}".encode()))
+    a_shape = (K, M) if layout == 2 else (M, K)
+    b_shape = (N, K) if layout == 1 else (K, N)
+    A = normal(rng, a_shape, absval=True)
+    B = normal(rng, b_shape, std=0.05, absval=True)
+    bias = normal(rng, (N,), std=0.1)
+    if dtype == "f16":
+        a, A = dev_f16(A)
+        b, B = dev_f16(B)
+    else:
+        a, b = dev(A), dev(B)
+    C, res = vedic.gemm_checked(layout, a, b, bias=dev(bias), alpha=0.5)
+    got = host(C)
+    plain = host(vedic.gemm(layout, a, b, bias=dev(bias), epilogue=vedic.EPI_BIAS, alpha=0.5))
+    assert np.array_equal(got, plain)
+    g64 = got.astype(np.float64)
+    assert abs(res.checksum_C - g64.sum()) <= 2 * (M // 32 + 64) * U * np.abs(g64).sum() + np.spacing(np.float32(res.checksum_C))
+    opA = A.T if layout == 2 else A
+    opB = B.T if layout == 1 else B
+    pred = 0.5 * (opA.astype(np.float64).sum(0) @ opB.astype(np.float64).sum(1)) + M * bias.astype(np.float64).sum()
+    assert abs(res.checksum_vedic - pred) <= 1e-6 * abs(pred)
+    assert res.passed and res.relative_error < 1e-4
+
+
+def test_gemm_checked_rejects_nonlinear_epilogues():
+    vedic = V()
+    from logos_amd import _lib
+    import ctypes
+    a = torch.ones((64, 64), dtype=torch.float16, device="cuda")
+    c = torch.empty((64, 64), device="cuda")
+    b = torch.zeros(64, device="cuda")
+    d = _lib.GemmDesc(op=0, in_dtype=1, out_dtype=0, M=64, N=64, K=64, A=a.data_ptr(), lda=64, B=a.data_ptr(),
+                      ldb=64, C=c.data_ptr(), ldc=64, alpha=1.0, beta=0.0, bias=b.data_ptr(),
+                      epilogue=_lib.EPI_BIAS_GELU, stream=torch.cuda.current_stream().cuda_stream)
+    r = _lib.VerifyResult()
+    assert _lib.load().vedic_gemm_checked(ctypes.byref(d), 0.01, ctypes.byref(r)) == _lib.STATUS_BAD_EPILOGUE
+    # and a fault in C shows: the same check over a C with one column dropped fails
+    A = torch.rand((256, 128), device="cuda") + 0.5
+    B = torch.rand((128, 192), device="cuda") + 0.5
+    C, res = vedic.gemm_checked(0, A, B)
+    assert res.passed
+    C[:, 7] = 0
+    assert not vedic.verify(A, B, C, tolerance=1e-3).passed
