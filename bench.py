@@ -45,8 +45,8 @@ HBM_PEAK_GBS = 8000.0                   # MI355X HBM3E, GB/s (published)
 
 # One GEMM: (M, K, N, op, dtype, epilogue, beta).  op as stored:
 #   NN A[MxK] B[KxN]; NT A[MxK] B[NxK]; TN A[KxM] B[KxN].
-def _g(M, K, N, op="NN", dtype="fp16", epi="none", beta=0.0, checked=False):
-    return dict(M=M, K=K, N=N, op=op, dtype=dtype, epi=epi, beta=beta, checked=checked)
+def _g(M, K, N, op="NN", dtype="fp16", epi="none", beta=0.0, checked=False, heads=0):
+    return dict(M=M, K=K, N=N, op=op, dtype=dtype, epi=epi, beta=beta, checked=checked, heads=heads)
 
 
 # BASELINE.json configs; each workload is a list of GEMMs run back to back per step.
@@ -58,6 +58,10 @@ WORKLOADS = {
     # FFN backward through the activation, fused (SURVEY next-row 1): dH = (dY . W2^T) * gelu'(H)
     # with db1 += colsum(dH), at config 3's NT shape and config 2's activation
     "ffn_bwd_dh_gelu_nt_fp16": dict(cfg=3, gemms=[_g(8192, 1024, 4096, op="NT", epi="gelu_bwd")]),
+    # the Q/K/V projection of one layer (SURVEY next-row 2): the reference's 48 per-head GEMMs
+    # (cuda/ModelGPU.cu:894-906) against one packed GEMM scattered into the same 48 head buffers
+    "qkv_per_head_fp16": dict(cfg=5, gemms=[_g(8192, 1024, 64) for _ in range(48)]),
+    "qkv_packed_scatter_fp16": dict(cfg=5, gemms=[_g(8192, 1024, 3072, heads=48)]),
     "lm_head_fp16": dict(cfg=4, gemms=[_g(8192, 1024, 8192)]),
     "lm_head_fp32": dict(cfg=4, gemms=[_g(8192, 1024, 8192, dtype="fp32")]),
     # the LM-head GEMM with its Gunitasamuchayah check computed on the way (SURVEY next-row 3);
@@ -269,14 +273,26 @@ def make_step(w: dict, dev, torch):
             hbm += M * N * 4 + N * 4  # H read, db read and written
         if g["checked"]:
             hbm += (M * K + K * N) * es  # one more pass over A and B for the prediction
+        heads = None
+        if g["heads"]:
+            hc = N // g["heads"]
+            hts = [torch.empty((M, hc), device=dev) for _ in range(g["heads"])]
+            keep += hts
+            heads = (ctypes.c_void_p * g["heads"])(*[t.data_ptr() for t in hts])
+            keep.append(heads)
         items.append((d, 2.0 * M * N * K, hbm))
-    ptrs = [(ctypes.byref(d), g["checked"]) for (d, _, _), g in zip(items, w["gemms"])]
+        g["_heads"] = heads
+    ptrs = [(ctypes.byref(d), g) for (d, _, _), g in zip(items, w["gemms"])]
     gemm = lib.vedic_gemm
     vres = _lib.VerifyResult()
 
     def step():
-        for p, checked in ptrs:
-            rc = lib.vedic_gemm_checked(p, 0.05, ctypes.byref(vres)) if checked else gemm(p)
+        for p, g in ptrs:
+            checked = g["checked"]
+            if g["heads"]:
+                rc = lib.vedic_gemm_scatter(p, g["_heads"], g["heads"], g["N"] // g["heads"])
+            else:
+                rc = lib.vedic_gemm_checked(p, 0.05, ctypes.byref(vres)) if checked else gemm(p)
             if rc:
                 raise RuntimeError(f"vedic_gemm failed: {_lib.status_string(rc)}")
             if checked and not vres.pass_:

@@ -305,6 +305,25 @@ inline void cuda_bias_grad(const float* dY, float* db, int seq, int cols, float 
     vedic_hip::check(vedic_bias_grad(dY, db, seq, cols, beta, stream), "cuda_bias_grad");
 }
 
+// Packed Q/K/V projection written into per-head buffers: heads[h] =
+// (X . Wqkv)[:, h*head_cols:(h+1)*head_cols], X [M x K] and Wqkv [K x N]
+// binary16 (Wqkv built by cuda_cast_pack_fp16), heads fp32 [M x head_cols].
+// One launch for the reference's per-head amp_gemm calls (cuda/ModelGPU.cu:894-906).
+inline void cuda_gemm_fp16_scatter(const __half* X, int M, int K, const __half* Wqkv, int N, float* const* heads,
+                                   int nheads, int head_cols, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_gemm_f16_scatter(X, M, K, Wqkv, N, heads, nheads, head_cols, stream),
+                     "cuda_gemm_fp16_scatter");
+}
+
+// Shadow-weight cast of several fp32 [rows x cols] matrices packed side by side
+// into one binary16 matrix (cuda/train_gpu.cu:1542-1547 per parameter, here
+// W_Q[0..H) W_K[0..H) W_V[0..H) of a layer into [D x 3 H DH]).
+inline void cuda_cast_pack_fp16(const float* const* src, int nsrc, int rows, int cols, __half* dst,
+                                hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_cast_pack_f16(src, nsrc, rows, cols, dst, (int64_t)nsrc * cols, stream),
+                     "cuda_cast_pack_fp16");
+}
+
 // --------------------------------------------------- elementwise helpers
 
 // C[i][j] += bias[j] (the add_bias_kernel launch, cuda/VedicGEMM.cu:96-102).

@@ -167,6 +167,21 @@ int vedic_gemm_tn_f32(const float* X, const float* dY, float* dW, int M, int N, 
 int vedic_gemm_tn_f16(const void* X, const void* dY, float* dW, int M, int N, int K, float beta,
                       void* stream);
 
+/* The GEMM of `desc` with the columns of C scattered to separate matrices:
+ * columns [h * head_cols, (h + 1) * head_cols) of C go to heads[h], a
+ * row-major [M x head_cols] fp32 matrix (desc->C and ldc are not used).
+ * head_cols a multiple of 32, nheads * head_cols = N, nheads <= 64;
+ * epilogue NONE or BIAS, alpha = 1, beta = 0, no colsum or preact; A and B
+ * aligned as for the 16-byte-load path (VEDIC_STATUS_BAD_LD otherwise).
+ * New: one packed Q/K/V projection (see vedic_cast_pack_f16) that still
+ * fills the per-head hc.Q / hc.K / hc.V buffers the reference's attention
+ * reads (cuda/ModelGPU.cu:894-906, 48 amp_gemm calls per layer). */
+int vedic_gemm_scatter(const vedic_gemm_desc_t* desc, float* const* heads, int nheads, int head_cols);
+
+/* fp16 convenience form: heads <- X[MxK] . W[KxN], X and W binary16. */
+int vedic_gemm_f16_scatter(const void* X, int M, int K, const void* W, int N, float* const* heads, int nheads,
+                           int head_cols, void* stream);
+
 /* FFN backward through the activation, fused:
  *     dH[MxN] = (dY[MxK] . W^T) * gelu_tanh'(H),   W stored [NxK],
  *     db[j]  += sum_i dH[i][j]                     (db nullable),
@@ -197,6 +212,15 @@ int vedic_gelu(float* x, int64_t n, void* stream);
 /* dst = binary16(clamp(src, -65504, 65504)), round to nearest even.
  * Replaces cuda_cast_fp32_to_fp16 (cuda/MixedPrecision.cuh:149-161,177-190). */
 int vedic_cast_f32_to_f16(const float* src, void* dst, int64_t n, void* stream);
+
+/* nsrc fp32 [rows x cols] matrices cast to binary16 (the clamp and rounding
+ * above) and packed side by side: dst[r][i * cols + c] = src[i][r][c], dst
+ * row-major with leading dimension ld_dst >= nsrc * cols; nsrc <= 64.  The
+ * shadow-weight cast of cuda/train_gpu.cu:1542-1547, with the per-head
+ * W_Q / W_K / W_V of a layer packed into one [D x 3 H DH] matrix for
+ * vedic_gemm_f16_scatter. */
+int vedic_cast_pack_f16(const float* const* src, int nsrc, int rows, int cols, void* dst, int64_t ld_dst,
+                        void* stream);
 
 /* dst = float(src).  Replaces cuda_cast_fp16_to_fp32 (cuda/MixedPrecision.cuh:164-172,192-196). */
 int vedic_cast_f16_to_f32(const void* src, float* dst, int64_t n, void* stream);

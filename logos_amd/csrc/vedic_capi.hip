@@ -226,15 +226,30 @@ static hipError_t launch_split(bool f16, int op, bool vec, const GemmArgs& a, in
 
 // ------------------------------------------------------------------ GEMM
 
-extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
+// The GEMM; with nheads > 0 the columns of C are scattered to heads[0..nheads)
+// (each [M x head_cols], row-major) instead of written to d->C.
+static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads, int head_cols) {
     if (!d) return VEDIC_STATUS_NULL_POINTER;
     if (d->M <= 0 || d->N <= 0 || d->K <= 0) return VEDIC_STATUS_BAD_DIM;
+    const bool scatter = nheads > 0;
+    if (scatter) {
+        if (!heads) return VEDIC_STATUS_NULL_POINTER;
+        if (nheads > kMaxHeads) return VEDIC_STATUS_TOO_LARGE;
+        if (head_cols <= 0 || head_cols % 32 != 0 || (int64_t)nheads * head_cols != d->N)
+            return VEDIC_STATUS_BAD_DIM;
+        for (int h = 0; h < nheads; ++h)
+            if (!heads[h]) return VEDIC_STATUS_NULL_POINTER;
+        // plain or bias epilogue into fp32 heads, nothing that reads or sums C
+        if (d->out_dtype != VEDIC_DT_F32 || d->beta != 0.0f || d->alpha != 1.0f || d->colsum || d->preact ||
+            (d->epilogue != VEDIC_EPI_NONE && d->epilogue != VEDIC_EPI_BIAS))
+            return VEDIC_STATUS_BAD_EPILOGUE;
+    }
     if (d->op < VEDIC_OP_NN || d->op > VEDIC_OP_TN) return VEDIC_STATUS_BAD_LAYOUT;
     if (d->in_dtype != VEDIC_DT_F32 && d->in_dtype != VEDIC_DT_F16) return VEDIC_STATUS_BAD_DTYPE;
     if (d->out_dtype != VEDIC_DT_F32 &&
         !(d->out_dtype == VEDIC_DT_F16 && d->in_dtype == VEDIC_DT_F16))
         return VEDIC_STATUS_BAD_DTYPE;
-    if (!d->A || !d->B || !d->C) return VEDIC_STATUS_NULL_POINTER;
+    if (!d->A || !d->B || (!d->C && !scatter)) return VEDIC_STATUS_NULL_POINTER;
     if (d->epilogue < VEDIC_EPI_NONE || d->epilogue > VEDIC_EPI_GELU_BWD) return VEDIC_STATUS_BAD_EPILOGUE;
     const bool want_bias = d->epilogue == VEDIC_EPI_BIAS || d->epilogue == VEDIC_EPI_BIAS_GELU;
     if (want_bias && !d->bias) return VEDIC_STATUS_BAD_EPILOGUE;
@@ -247,7 +262,7 @@ extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
     const bool b_kc = d->op == VEDIC_OP_NT;
     const int64_t a_row = a_kc ? d->K : d->M;
     const int64_t b_row = b_kc ? d->K : d->N;
-    if (d->lda < a_row || d->ldb < b_row || d->ldc < d->N) return VEDIC_STATUS_BAD_LD;
+    if (d->lda < a_row || d->ldb < b_row || (!scatter && d->ldc < d->N)) return VEDIC_STATUS_BAD_LD;
     if (d->preact && d->ld_preact < d->N) return VEDIC_STATUS_BAD_LD;
 
     GemmArgs a{};
@@ -258,8 +273,12 @@ extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
     a.preact = d->preact;
     a.lda = d->lda;
     a.ldb = d->ldb;
-    a.ldc = d->ldc;
+    a.ldc = scatter ? d->N : d->ldc;
     a.ldp = d->preact ? d->ld_preact : 0;
+    if (scatter) {
+        a.head_cols = head_cols;
+        for (int h = 0; h < nheads; ++h) a.heads[h] = heads[h];
+    }
     a.M = d->M;
     a.N = d->N;
     a.K = d->K;
@@ -286,12 +305,14 @@ extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
 
     // Tiles are addressed with 32-bit buffer offsets from the tile's first
     // row: a few hundred rows of any operand or output must stay below 2 GiB.
-    if (d->ldc >= kMaxLd || (d->preact && d->ld_preact >= kMaxLd)) return VEDIC_STATUS_TOO_LARGE;
+    if (a.ldc >= kMaxLd || (d->preact && d->ld_preact >= kMaxLd)) return VEDIC_STATUS_TOO_LARGE;
 
     const bool f16 = d->in_dtype == VEDIC_DT_F16;
     const bool direct = vec && d->lda < kMaxLd && d->ldb < kMaxLd;
+    // scattered C needs the kernels with a plain or bias epilogue kind
+    if (scatter && !direct) return VEDIC_STATUS_BAD_LD;
     const bool skinny = direct && d->op == VEDIC_OP_NN && d->M <= 32;
-    const int ks = skinny || (f16 && !direct) ? 1 : choose_ksplit(d->M, d->N, d->K, device_cu_count(), f16);
+    const int ks = skinny || scatter || (f16 && !direct) ? 1 : choose_ksplit(d->M, d->N, d->K, device_cu_count(), f16);
 
     hipStream_t s = static_cast<hipStream_t>(d->stream);
     hipError_t e = hipSuccess;
@@ -332,6 +353,13 @@ extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) {
         if (e == hipSuccess) e = f;
     }
     return hip_status(e);
+}
+
+extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) { return gemm_impl(d, nullptr, 0, 0); }
+
+extern "C" int vedic_gemm_scatter(const vedic_gemm_desc_t* d, float* const* heads, int nheads, int head_cols) {
+    if (nheads <= 0) return VEDIC_STATUS_BAD_DIM;
+    return gemm_impl(d, heads, nheads, head_cols);
 }
 
 static vedic_gemm_desc_t make_desc(int op, int dt, int M, int N, int K, const void* A, int64_t lda,
@@ -429,6 +457,12 @@ extern "C" int vedic_gemm_tn_f16(const void* X, const void* dY, float* dW, int M
     return vedic_gemm(&d);
 }
 
+extern "C" int vedic_gemm_f16_scatter(const void* X, int M, int K, const void* W, int N, float* const* heads,
+                                      int nheads, int head_cols, void* stream) {
+    vedic_gemm_desc_t d = make_desc(VEDIC_OP_NN, VEDIC_DT_F16, M, N, K, X, K, W, N, nullptr, 1.f, 0.f, stream);
+    return vedic_gemm_scatter(&d, heads, nheads, head_cols);
+}
+
 extern "C" int vedic_gemm_nt_gelu_bwd_f16(const void* dY, const void* W, const float* H, float* dH, float* db,
                                           int M, int N, int K, void* stream) {
     vedic_gemm_desc_t d = make_desc(VEDIC_OP_NT, VEDIC_DT_F16, M, N, K, dY, K, W, K, dH, 1.f, 0.f, stream);
@@ -508,6 +542,27 @@ __global__ void cast_f32_f16_kernel(const float* __restrict__ src, _Float16* __r
         for (int64_t i = n8 * 8 + t; i < n; i += stride) dst[i] = to_half_clamped(src[i]);
     } else {
         for (int64_t i = t; i < n; i += stride) dst[i] = to_half_clamped(src[i]);
+    }
+}
+
+// Several fp32 [rows x cols] matrices cast to binary16 (same clamp and
+// rounding as the plain cast) and packed side by side: dst[r][i cols + c] =
+// src_i[r][c].  One thread per destination element, consecutive threads on
+// consecutive destination columns.
+constexpr int kMaxPack = 64;
+struct PackSources {
+    const float* p[kMaxPack];
+};
+
+__global__ void cast_pack_f16_kernel(PackSources src, int nsrc, int rows, int cols, _Float16* __restrict__ dst,
+                                     int64_t ld) {
+    const int64_t width = (int64_t)nsrc * cols;
+    const int64_t total = width * rows;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = e / width, w = e - r * width;
+        const int i = (int)(w / cols), c = (int)(w - (int64_t)i * cols);
+        dst[r * ld + w] = to_half_clamped(src.p[i][r * cols + c]);
     }
 }
 
@@ -692,6 +747,23 @@ extern "C" int vedic_cast_f32_to_f16(const float* src, void* dst, int64_t n, voi
     const int vec = aligned16(src) && aligned16(dst);
     hipLaunchKernelGGL(cast_f32_f16_kernel, dim3(ew_blocks(n, 8)), dim3(kEwThreads), 0,
                        static_cast<hipStream_t>(stream), src, static_cast<_Float16*>(dst), n, vec);
+    return hip_status(hipGetLastError());
+}
+
+extern "C" int vedic_cast_pack_f16(const float* const* src, int nsrc, int rows, int cols, void* dst,
+                                   int64_t ld_dst, void* stream) {
+    if (nsrc <= 0 || rows <= 0 || cols <= 0) return VEDIC_STATUS_BAD_DIM;
+    if (nsrc > kMaxPack) return VEDIC_STATUS_TOO_LARGE;
+    if (!src || !dst) return VEDIC_STATUS_NULL_POINTER;
+    if (ld_dst < (int64_t)nsrc * cols) return VEDIC_STATUS_BAD_LD;
+    PackSources ps{};
+    for (int i = 0; i < nsrc; ++i) {
+        if (!src[i]) return VEDIC_STATUS_NULL_POINTER;
+        ps.p[i] = src[i];
+    }
+    const int64_t n = (int64_t)nsrc * cols * rows;
+    hipLaunchKernelGGL(cast_pack_f16_kernel, dim3(ew_blocks(n, 4)), dim3(kEwThreads), 0,
+                       static_cast<hipStream_t>(stream), ps, nsrc, rows, cols, static_cast<_Float16*>(dst), ld_dst);
     return hip_status(hipGetLastError());
 }
 

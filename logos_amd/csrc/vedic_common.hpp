@@ -72,6 +72,8 @@ enum : int {
     EPI_COLSUM = 128,   // column sums of C into cs_part (per 32-row block)
 };
 
+constexpr int kMaxHeads = 64;  // scatter targets per GEMM
+
 struct GemmArgs {
     const void* A;
     const void* B;
@@ -94,6 +96,11 @@ struct GemmArgs {
     // 32-row block b of C and column j, the sum of the block's rows (rows < M)
     // to cs_part[b * N + j]; a fixed-order pass then adds the blocks.
     float* cs_part;
+    // Scattered C (head_cols > 0): columns [h * head_cols, (h + 1) * head_cols)
+    // of C go to heads[h], a row-major [M x head_cols] matrix; head_cols is a
+    // multiple of 32, so every 32 x 32 block lies in one head.  fp32 C.
+    int head_cols;
+    float* heads[kMaxHeads];
 };
 
 }  // namespace vedic

@@ -65,18 +65,19 @@ __device__ __forceinline__ float ld_f16(__amdgpu_buffer_rsrc_t rs, uint32_t voff
     return (float)__builtin_bit_cast(_Float16, b);
 }
 
-// Writes a (32*MI) x (32*NI) wave tile whose top-left output is (row0, col0).
+// Writes a (32*MI) x (32*NI) wave tile whose top-left output is (row0, col0)
+// of the matrix at Cp (a.C, or a split-K slab of the workspace).
 // CHECK: the tile may extend past M or N.  Offsets are 32-bit: the caller
 // guarantees (32*MI) * ld * 4 < 2^31 for ldc and ldp.
 template <int KIND, bool CHECK, int MI, int NI>
-__device__ __forceinline__ void epilogue(const GemmArgs& a, const float16_t (&acc)[MI][NI], int row0, int col0,
-                                         int lane) {
+__device__ __forceinline__ void epilogue(const GemmArgs& a, void* Cp, const float16_t (&acc)[MI][NI], int row0,
+                                         int col0, int lane) {
     const int l32 = lane & 31, h = lane >> 5;
     const bool f16out = (KIND == EK_GENERIC) && (a.epi & EPI_F16OUT);
     const int es = f16out ? 2 : 4;
-    const char* cbase = static_cast<const char*>(a.C) + ((int64_t)row0 * a.ldc) * es;
-    const __amdgpu_buffer_rsrc_t rc = buffer_rsrc(cbase);
-    __amdgpu_buffer_rsrc_t rp = rc;
+    const char* cbase = static_cast<const char*>(Cp) + ((int64_t)row0 * a.ldc) * es;
+    const __amdgpu_buffer_rsrc_t rc_tile = buffer_rsrc(cbase);
+    __amdgpu_buffer_rsrc_t rp = rc_tile;
     const bool pre = (KIND == EK_BIAS_GELU_PRE) || (KIND == EK_GENERIC && (a.epi & EPI_PREACT));
     const bool gbwd = (KIND == EK_GELU_BWD) || (KIND == EK_GENERIC && (a.epi & EPI_GELU_BWD));
     if (pre || gbwd) rp = buffer_rsrc(a.preact + (int64_t)row0 * a.ldp);
@@ -104,14 +105,21 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, const float16_t (&ac
         const int col = col0 + 32 * j + l32;
         bias_j[j] = (want_bias && (!CHECK || col < a.N)) ? a.bias[col] : 0.0f;
     }
+    // Scattered C (plain and bias kinds only; the host allows it for no
+    // other): block column c0 lies in head c0 / head_cols, whose matrix
+    // starts a new resource, and C offsets are relative to it.
+    constexpr bool CAN_SCATTER = KIND == EK_PLAIN || KIND == EK_BIAS;
+    const bool scatter = CAN_SCATTER && a.head_cols > 0;
     // byte offsets of element (g, r) of block (j, i): per-lane part and the
-    // wave-uniform row part; out-of-range elements get kOob
-    auto offsets = [&](int j, int i, int g, int r, uint32_t& oc, uint32_t& op, uint32_t& sc, uint32_t& sp) {
+    // wave-uniform row part; out-of-range elements get kOob.  ldcb and ccol:
+    // the row pitch and this lane's column byte offset in the block's target.
+    auto offsets = [&](int j, int i, int g, int r, uint32_t ldcb, uint32_t ccol, uint32_t& oc, uint32_t& op,
+                       uint32_t& sc, uint32_t& sp) {
         const int col = col0 + 32 * j + l32;
         const int u = 32 * i + 8 * g + r;
-        sc = (uint32_t)u * ldc_b;
+        sc = (uint32_t)u * ldcb;
         sp = (uint32_t)u * ldp_b;
-        oc = (uint32_t)(4 * h) * ldc_b + (uint32_t)(col * es);
+        oc = (uint32_t)(4 * h) * ldcb + ccol;
         op = (uint32_t)(4 * h) * ldp_b + (uint32_t)(col * 4);
         if (CHECK) {
             const bool ok = col < a.N && u < row_lim;
@@ -125,8 +133,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, const float16_t (&ac
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
             uint32_t oc, op, sc, sp;
-            offsets(j, i, e >> 2, e & 3, oc, op, sc, sp);
-            dc[e] = rd_c ? (f16out ? ld_f16(rc, oc, sc) : ld_f32(rc, oc, sc)) : 0.0f;
+            offsets(j, i, e >> 2, e & 3, ldc_b, (uint32_t)((col0 + 32 * j + l32) * es), oc, op, sc, sp);
+            dc[e] = rd_c ? (f16out ? ld_f16(rc_tile, oc, sc) : ld_f32(rc_tile, oc, sc)) : 0.0f;
             dp[e] = rd_p ? ld_f32(rp, op, sp) : 0.0f;
         }
     };
@@ -141,6 +149,14 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, const float16_t (&ac
         if constexpr (READS) {
             if (bk + 1 < NB) fetch(bk + 1, nxt_c, nxt_p);
         }
+        __amdgpu_buffer_rsrc_t rc = rc_tile;
+        uint32_t ldcb = ldc_b, ccol = (uint32_t)(col * es);
+        if (scatter) {
+            const int c0 = col0 + 32 * j, hd = c0 / a.head_cols;
+            rc = buffer_rsrc(a.heads[hd < kMaxHeads ? hd : 0] + (int64_t)row0 * a.head_cols);
+            ldcb = (uint32_t)(a.head_cols * 4);
+            ccol = (uint32_t)((c0 - hd * a.head_cols + l32) * 4);
+        }
         float csum = 0.0f;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -148,7 +164,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, const float16_t (&ac
             for (int r = 0; r < 4; ++r) {
                 const int e = 4 * g + r;
                 uint32_t oc, op, sc, sp;
-                offsets(j, i, g, r, oc, op, sc, sp);
+                offsets(j, i, g, r, ldcb, ccol, oc, op, sc, sp);
                 float v = acc[i][j][e];
                 if constexpr (KIND == EK_PLAIN) {
                     st_f32(v, rc, oc, sc);

@@ -301,8 +301,9 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
         }
 
         const int row0 = m0 + wm * WM, col0 = n0 + wn * WN;
-        GemmArgs ea = args;
-        if (args.ksplit > 1) ea.C = static_cast<float*>(args.C) + it.s * args.c_split_stride;
+        // split-K: this slice's raw partial goes to its own slab of the workspace
+        void* const cp = args.ksplit > 1 ? static_cast<void*>(static_cast<float*>(args.C) + it.s * args.c_split_stride)
+                                       : args.C;
         w += G;
         const bool more = w < nwork;
         if (more) {
@@ -317,9 +318,9 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
         }
         const bool full = (row0 + WM <= args.M) && (col0 + WN <= args.N);
         if (KIND != EK_GENERIC && full)
-            epilogue<KIND, false, MI, NI>(ea, acc, row0, col0, lane);
+            epilogue<KIND, false, MI, NI>(args, cp, acc, row0, col0, lane);
         else
-            epilogue<KIND, true, MI, NI>(ea, acc, row0, col0, lane);
+            epilogue<KIND, true, MI, NI>(args, cp, acc, row0, col0, lane);
         if (!more) break;
     }
     wait_vmcnt<0>();  // the trailing zero loads still write LDS

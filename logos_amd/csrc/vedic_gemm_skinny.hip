@@ -219,12 +219,14 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs a) {
         v += red[(48 + e) * 64 + lane];
         sum[0][0][e] = v;
     }
-    epilogue<KIND, true, 1, 1>(a, sum, 0, n0, lane);
+    epilogue<KIND, true, 1, 1>(a, a.C, sum, 0, n0, lane);
 }
 
 template __global__ void gemm_skinny_kernel<SkinnyF16, EK_PLAIN>(GemmArgs);
+template __global__ void gemm_skinny_kernel<SkinnyF16, EK_BIAS>(GemmArgs);
 template __global__ void gemm_skinny_kernel<SkinnyF16, EK_GENERIC>(GemmArgs);
 template __global__ void gemm_skinny_kernel<SkinnyF32, EK_PLAIN>(GemmArgs);
+template __global__ void gemm_skinny_kernel<SkinnyF32, EK_BIAS>(GemmArgs);
 template __global__ void gemm_skinny_kernel<SkinnyF32, EK_GENERIC>(GemmArgs);
 
 template <class Sk>
@@ -232,6 +234,8 @@ static hipError_t launch_skinny(const GemmArgs& a, hipStream_t s) {
     const dim3 grid((a.N + 31) / 32);
     if (a.epi_kind == EK_PLAIN)
         hipLaunchKernelGGL((gemm_skinny_kernel<Sk, EK_PLAIN>), grid, dim3(256), 0, s, a);
+    else if (a.epi_kind == EK_BIAS)
+        hipLaunchKernelGGL((gemm_skinny_kernel<Sk, EK_BIAS>), grid, dim3(256), 0, s, a);
     else
         hipLaunchKernelGGL((gemm_skinny_kernel<Sk, EK_GENERIC>), grid, dim3(256), 0, s, a);
     return hipGetLastError();

@@ -32,7 +32,8 @@ from ._lib import (DT_F16, DT_F32, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU, EPI_GELU_B
 __all__ = [
     "OP_NN", "OP_NT", "OP_TN", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU", "EPI_GELU", "EPI_GELU_BWD",
     "gemm", "vedic_gemm", "vedic_gemm_bias", "gemm_fp16_fp32out", "gemm_fp16_fp16out",
-    "gemm_bias_gelu", "gemm_nt", "gemm_tn", "gemm_nt_gelu_bwd", "bias_grad", "add_bias", "gelu_",
+    "gemm_bias_gelu", "gemm_nt", "gemm_tn", "gemm_nt_gelu_bwd", "bias_grad", "gemm_scatter",
+    "cast_pack_fp16", "add_bias", "gelu_",
     "cast_fp32_to_fp16",
     "cast_fp16_to_fp32", "verify", "gemm_checked", "VerifyResult", "uses_vendor_blas", "backend_name",
 ]
@@ -201,6 +202,57 @@ def bias_grad(dY: torch.Tensor, db: torch.Tensor | None = None, beta: float = 0.
         raise ValueError(f"db must be {N} contiguous float32 values")
     _check(_lib.load().vedic_bias_grad(dY.data_ptr(), db.data_ptr(), M, N, beta, _stream()))
     return db
+
+
+def gemm_scatter(X: torch.Tensor, W: torch.Tensor, heads: list[torch.Tensor],
+                 bias: torch.Tensor | None = None) -> list[torch.Tensor]:
+    """heads[h] = (X . W + bias)[:, h*hc:(h+1)*hc] for equal-width heads (hc a
+    multiple of 32): the packed Q/K/V projection written straight into the
+    per-head buffers."""
+    if X.dtype != W.dtype or X.dtype not in _DT:
+        raise ValueError("X and W must share dtype float16 or float32")
+    M, K, lda = _mat(X, "X")
+    Kb, N, ldb = _mat(W, "W")
+    if Kb != K:
+        raise ValueError(f"VedicGEMM: inner dimensions differ ({K} vs {Kb})")
+    if not heads:
+        raise ValueError("no heads")
+    hc = heads[0].shape[-1]
+    for t in heads:
+        if tuple(t.shape) != (M, hc) or t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda:
+            raise ValueError(f"every head must be a contiguous float32 [{M} x {hc}] GPU matrix")
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != N):
+        raise ValueError(f"bias must be {N} float32 values")
+    bias = bias.contiguous() if bias is not None else None
+    d = _lib.GemmDesc(
+        op=OP_NN, in_dtype=_DT[X.dtype], out_dtype=DT_F32, M=M, N=N, K=K,
+        A=X.data_ptr(), lda=lda, B=W.data_ptr(), ldb=ldb, C=None, ldc=N,
+        alpha=1.0, beta=0.0, bias=bias.data_ptr() if bias is not None else None,
+        epilogue=EPI_BIAS if bias is not None else EPI_NONE, preact=None, ld_preact=0, stream=_stream(),
+        colsum=None, colsum_beta=0.0,
+    )
+    ptrs = (ctypes.c_void_p * len(heads))(*[t.data_ptr() for t in heads])
+    _check(_lib.load().vedic_gemm_scatter(ctypes.byref(d), ptrs, len(heads), hc))
+    return heads
+
+
+def cast_pack_fp16(srcs: list[torch.Tensor], out: torch.Tensor | None = None) -> torch.Tensor:
+    """binary16 copy of fp32 [rows x cols] matrices packed side by side
+    (out[:, i*cols:(i+1)*cols] = srcs[i]), with the reference cast's clamp."""
+    if not srcs:
+        raise ValueError("no sources")
+    rows, cols = srcs[0].shape
+    for t in srcs:
+        if tuple(t.shape) != (rows, cols) or t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda:
+            raise ValueError(f"every source must be a contiguous float32 [{rows} x {cols}] GPU matrix")
+    if out is None:
+        out = torch.empty((rows, len(srcs) * cols), dtype=torch.float16, device=srcs[0].device)
+    r, c, ld = _mat(out, "out")
+    if r != rows or c != len(srcs) * cols or out.dtype != torch.float16:
+        raise ValueError("out must be float16 [rows x nsrc*cols]")
+    ptrs = (ctypes.c_void_p * len(srcs))(*[t.data_ptr() for t in srcs])
+    _check(_lib.load().vedic_cast_pack_f16(ptrs, len(srcs), rows, cols, out.data_ptr(), ld, _stream()))
+    return out
 
 
 def add_bias(C: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:

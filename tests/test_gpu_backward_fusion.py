@@ -252,3 +252,72 @@ def test_gemm_checked_rejects_nonlinear_epilogues():
     assert res.passed
     C[:, 7] = 0
     assert not vedic.verify(A, B, C, tolerance=1e-3).passed
+
+
+# -------------------------------------------- packed Q/K/V: cast + pack, scatter
+
+def test_cast_pack_bitexact():
+    """48 per-head fp32 weights [1024 x 64] packed into one binary16 [1024 x 3072]
+    (and into a padded leading dimension): bit-exact against the oracle's
+    binary16 rounding of the concatenation, clamp included."""
+    vedic = V()
+    rng = np.random.default_rng(51)
+    srcs = [normal(rng, (1024, 64), std=0.02) for _ in range(48)]
+    srcs[5][3, 7] = 1e6   # clamps to +65504
+    srcs[40][0, 0] = -7e4  # clamps to -65504
+    packed = vedic.cast_pack_fp16([dev(s_) for s_ in srcs])
+    want = o.f16_round(np.concatenate(srcs, axis=1))
+    assert np.array_equal(host(packed), want)
+    buf = torch.full((1024, 3072 + 8), 2.0, dtype=torch.float16, device="cuda")
+    vedic.cast_pack_fp16([dev(s_) for s_ in srcs], buf[:, :3072])
+    got = host(buf)
+    assert np.array_equal(got[:, :3072], want) and np.all(got[:, 3072:] == 2.0)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("M", [8192, 300, 7])
+def test_gemm_scatter_heads(dtype, M):
+    """The packed projection scattered into per-head buffers: every head equals
+    the matching columns of the unscattered product (bit for bit where both run
+    the same kernel; the unscattered fp32 product at M = 300 has few tiles and
+    is split over K, which scattered output never is), and the per-head product
+    X . W_h of the fp64 oracle within tolerance.  M = 8192 takes the 256 x 256
+    tiles, 300 the 128 x 128 tiles, 7 the decode kernel."""
+    vedic = V()
+    H, DH, K = 16, 64, 1024
+    rng = np.random.default_rng(zlib.crc32(f"scatter-{dtype}-{M}".encode()))
+    X = normal(rng, (M, K))
+    Wp = normal(rng, (K, 3 * H * DH), std=0.02)
+    bias = normal(rng, (3 * H * DH,), std=0.01)
+    if dtype == "f16":
+        x, X = dev_f16(X)
+        w, Wp = dev_f16(Wp)
+        tol = FP16_TOL
+    else:
+        x, w = dev(X), dev(Wp)
+        tol = fp32_tol(K)
+    heads = [torch.full((M, DH), 9.0, device="cuda") for _ in range(3 * H)]
+    vedic.gemm_scatter(x, w, heads, bias=dev(bias))
+    full = host(vedic.gemm(vedic.OP_NN, x, w, bias=dev(bias), epilogue=vedic.EPI_BIAS))
+    rows = np.unique(np.concatenate([[0, M - 1], rng.choice(M, min(M, 24), replace=False)]))
+    for h in range(3 * H):
+        got = host(heads[h])
+        ref_cols = full[:, h * DH:(h + 1) * DH]
+        if dtype == "f32" and M == 300:
+            assert o.inf_rel_err(got, ref_cols.astype(np.float64)) <= 2 * tol, f"head {h}"
+        else:
+            assert np.array_equal(got, ref_cols), f"head {h}"
+        if h % 7 == 0:
+            want, _ = o.gemm_f64(o.NN, np.ascontiguousarray(X[rows]), np.ascontiguousarray(Wp[:, h * DH:(h + 1) * DH]),
+                                 bias=bias[h * DH:(h + 1) * DH])
+            assert o.inf_rel_err(got[rows], want) <= tol
+
+
+def test_gemm_scatter_rejections():
+    vedic = V()
+    x = torch.zeros((64, 64), dtype=torch.float16, device="cuda")
+    w = torch.zeros((64, 96), dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):  # 48-column heads: not a multiple of 32
+        vedic.gemm_scatter(x, w, [torch.zeros((64, 48), device="cuda") for _ in range(2)])
+    with pytest.raises(ValueError):  # head widths do not add up to N
+        vedic.gemm_scatter(x, w, [torch.zeros((64, 32), device="cuda") for _ in range(2)])
