@@ -187,8 +187,8 @@ int vedic_gemm_f16_scatter(const void* X, int M, int K, const void* W, int N, fl
  *     db[j]  += sum_i dH[i][j]                     (db nullable),
  * with H the cached pre-activation [MxN] (the `preact` output of
  * vedic_gemm_bias_gelu_*).  Replaces ffn_da + gelu_bwd + bias_grad
- * (cuda/train_gpu.cu:323-332, 334-345, 263-273, launched at :590-600 and
- * :619-621): one pass over dH instead of three, and no atomics. */
+ * (cuda/train_gpu.cu:323-332, 334-345, 263-273, launched at :590-597 and
+ * :617-618): one pass over dH instead of three, and no atomics. */
 int vedic_gemm_nt_gelu_bwd_f16(const void* dY, const void* W, const float* H, float* dH, float* db, int M,
                                int N, int K, void* stream);
 int vedic_gemm_nt_gelu_bwd_f32(const float* dY, const float* W, const float* H, float* dH, float* db, int M,
