@@ -45,8 +45,8 @@ HBM_PEAK_GBS = 8000.0                   # MI355X HBM3E, GB/s (published)
 
 # One GEMM: (M, K, N, op, dtype, epilogue, beta).  op as stored:
 #   NN A[MxK] B[KxN]; NT A[MxK] B[NxK]; TN A[KxM] B[KxN].
-def _g(M, K, N, op="NN", dtype="fp16", epi="none", beta=0.0, checked=False, heads=0):
-    return dict(M=M, K=K, N=N, op=op, dtype=dtype, epi=epi, beta=beta, checked=checked, heads=heads)
+def _g(M, K, N, op="NN", dtype="fp16", epi="none", beta=0.0, checked=False, heads=0, alpha=1.0):
+    return dict(M=M, K=K, N=N, op=op, dtype=dtype, epi=epi, beta=beta, checked=checked, heads=heads, alpha=alpha)
 
 
 # BASELINE.json configs; each workload is a list of GEMMs run back to back per step.
@@ -55,16 +55,25 @@ WORKLOADS = {
     "ffn_up_fp16_bias_gelu": dict(cfg=2, gemms=[_g(8192, 1024, 4096, epi="bias_gelu")]),
     "ffn_down_dx_nt_fp16": dict(cfg=3, gemms=[_g(8192, 1024, 4096, op="NT")]),
     "ffn_down_dw_tn_fp16": dict(cfg=3, gemms=[_g(4096, 8192, 1024, op="TN", beta=1.0)]),
-    # FFN backward through the activation, fused (SURVEY next-row 1): dH = (dY . W2^T) * gelu'(H)
+    # FFN backward through the activation, fused: dH = (dY . W2^T) * gelu'(H)
     # with db1 += colsum(dH), at config 3's NT shape and config 2's activation
     "ffn_bwd_dh_gelu_nt_fp16": dict(cfg=3, gemms=[_g(8192, 1024, 4096, op="NT", epi="gelu_bwd")]),
-    # the Q/K/V projection of one layer (SURVEY next-row 2): the reference's 48 per-head GEMMs
+    # the Q/K/V projection of one layer: the reference's 48 per-head GEMMs
     # (cuda/ModelGPU.cu:894-906) against one packed GEMM scattered into the same 48 head buffers
     "qkv_per_head_fp16": dict(cfg=5, gemms=[_g(8192, 1024, 64) for _ in range(48)]),
     "qkv_packed_scatter_fp16": dict(cfg=5, gemms=[_g(8192, 1024, 3072, heads=48)]),
+    # one attention head's GEMMs at seq = 8192, DH = 64, strict fp32 as in the reference
+    # (cuda/train_gpu.cu:422-479, 672-692): scores = Q K^T / sqrt(DH) (NT, alpha),
+    # out = P V (NN), dP = dO V^T (NT), dV += P^T dO (TN, beta = 1), dQ = dS K (NN), dK = dS^T Q (TN);
+    # the softmax and its backward stay with the caller
+    "attn_head_fwd_bwd_fp32": dict(cfg=5, gemms=[
+        _g(8192, 64, 8192, op="NT", dtype="fp32", alpha=0.125), _g(8192, 8192, 64, dtype="fp32"),
+        _g(8192, 64, 8192, op="NT", dtype="fp32"), _g(8192, 8192, 64, op="TN", dtype="fp32", beta=1.0),
+        _g(8192, 8192, 64, dtype="fp32"), _g(8192, 8192, 64, op="TN", dtype="fp32"),
+    ]),
     "lm_head_fp16": dict(cfg=4, gemms=[_g(8192, 1024, 8192)]),
     "lm_head_fp32": dict(cfg=4, gemms=[_g(8192, 1024, 8192, dtype="fp32")]),
-    # the LM-head GEMM with its Gunitasamuchayah check computed on the way (SURVEY next-row 3);
+    # the LM-head GEMM with its Gunitasamuchayah check computed on the way;
     # synchronous per step, like the reference's verify
     "lm_head_fp16_checked": dict(cfg=4, gemms=[_g(8192, 1024, 8192, checked=True)]),
     **{f"decode_fp16_m{m}": dict(cfg=4, hbm=True, gemms=[_g(m, 1024, 8192)]) for m in (1, 2, 4, 8, 16, 32)},
@@ -263,7 +272,7 @@ def make_step(w: dict, dev, torch):
             op={"NN": _lib.OP_NN, "NT": _lib.OP_NT, "TN": _lib.OP_TN}[op],
             in_dtype=_lib.DT_F16 if g["dtype"] == "fp16" else _lib.DT_F32, out_dtype=_lib.DT_F32,
             M=M, N=N, K=K, A=A.data_ptr(), lda=A.shape[1], B=B.data_ptr(), ldb=B.shape[1],
-            C=C.data_ptr(), ldc=N, alpha=1.0, beta=g["beta"],
+            C=C.data_ptr(), ldc=N, alpha=g["alpha"], beta=g["beta"],
             bias=bias.data_ptr() if g["epi"] in ("bias", "bias_gelu") else None, epilogue=epi,
             preact=H.data_ptr() if gbwd else None, ld_preact=N if gbwd else 0, stream=stream.cuda_stream,
             colsum=db.data_ptr() if gbwd else None, colsum_beta=1.0)
