@@ -175,7 +175,9 @@ static int choose_ksplit(int M, int N, int K, int cus, bool f16) {
         if (big >= cus) return 1;  // the 256 x 256 kernel fills the GPU
     }
     const int min_slice = f16 ? 1024 : 128;
-    const int64_t tiles = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+    // fp32 products with N <= 64 run on 256 x 64 tiles
+    const int64_t tiles = (!f16 && N <= 64) ? (int64_t)((M + 255) / 256)
+                                            : (int64_t)((M + 127) / 128) * ((N + 127) / 128);
     if (tiles * 2 > cus || K < 2 * min_slice) return 1;
     int s = (int)(cus / tiles);
     s = s < 8 ? s : 8;

@@ -271,10 +271,16 @@ struct CfgF32 {
     static constexpr int BM = 128, BN = 128, ST = VEDIC_F32_STAGES, WGM = 2, WGN = 2;
     static constexpr int PER_CU = ST <= 2 ? 2 : 1;  // resident workgroups per CU (LDS: ST x 32 KiB)
 };
+// Narrow outputs (N <= 64, e.g. an attention head's P V, dQ, dK, dV at
+// DH = 64): 256 x 64 tiles, four waves of 64 x 64 stacked in M, so no MFMA
+// work lands on columns past N.  Two stages of 40 KiB, two workgroups per CU.
+struct CfgF32Narrow {
+    static constexpr int BM = 256, BN = 64, ST = 2, WGM = 4, WGN = 1;
+    static constexpr int PER_CU = 2;
+};
 
-template <int OP, int KIND>
+template <int OP, int KIND, class Cfg>
 static hipError_t launch_f32(GemmArgs a, hipStream_t s) {
-    using Cfg = CfgF32;
     a.tiles_m = (a.M + Cfg::BM - 1) / Cfg::BM;
     a.tiles_n = (a.N + Cfg::BN - 1) / Cfg::BN;
     if (a.group_m <= 0) a.group_m = 8;
@@ -292,18 +298,25 @@ static hipError_t launch_f32(GemmArgs a, hipStream_t s) {
 
 // Requires: A, B 16-byte aligned; lda, ldb multiples of 4 and < 2^22; the
 // contiguous extent of each operand a multiple of 4 (checked by the caller).
+template <int OP, class Cfg>
+static hipError_t launch_f32_kind(const GemmArgs& a, hipStream_t s) {
+    switch (a.epi_kind) {
+        case EK_PLAIN: return launch_f32<OP, EK_PLAIN, Cfg>(a, s);
+        case EK_BIAS: return launch_f32<OP, EK_BIAS, Cfg>(a, s);
+        case EK_BIAS_GELU: return launch_f32<OP, EK_BIAS_GELU, Cfg>(a, s);
+        case EK_BIAS_GELU_PRE: return launch_f32<OP, EK_BIAS_GELU_PRE, Cfg>(a, s);
+        case EK_ACCUM: return launch_f32<OP, EK_ACCUM, Cfg>(a, s);
+        case EK_GELU_BWD: return launch_f32<OP, EK_GELU_BWD, Cfg>(a, s);
+        case EK_LINEAR_CS: return launch_f32<OP, EK_LINEAR_CS, Cfg>(a, s);
+        default: return launch_f32<OP, EK_GENERIC, Cfg>(a, s);
+    }
+}
+
+// Narrow tiles when N fits one 64-wide tile column.
 template <int OP>
 hipError_t launch_gemm_f32_direct_op(const GemmArgs& a, hipStream_t s) {
-    switch (a.epi_kind) {
-        case EK_PLAIN: return launch_f32<OP, EK_PLAIN>(a, s);
-        case EK_BIAS: return launch_f32<OP, EK_BIAS>(a, s);
-        case EK_BIAS_GELU: return launch_f32<OP, EK_BIAS_GELU>(a, s);
-        case EK_BIAS_GELU_PRE: return launch_f32<OP, EK_BIAS_GELU_PRE>(a, s);
-        case EK_ACCUM: return launch_f32<OP, EK_ACCUM>(a, s);
-        case EK_GELU_BWD: return launch_f32<OP, EK_GELU_BWD>(a, s);
-        case EK_LINEAR_CS: return launch_f32<OP, EK_LINEAR_CS>(a, s);
-        default: return launch_f32<OP, EK_GENERIC>(a, s);
-    }
+    if (a.N <= CfgF32Narrow::BN) return launch_f32_kind<OP, CfgF32Narrow>(a, s);
+    return launch_f32_kind<OP, CfgF32>(a, s);
 }
 
 }  // namespace vedic

@@ -5,8 +5,11 @@
 
 namespace vedic {
 
-#define VEDIC_F32_INST(KIND) \
-    template __global__ void gemm_f32_kernel<0, CfgF32::BM, CfgF32::BN, CfgF32::ST, CfgF32::WGM, CfgF32::WGN, KIND>(GemmArgs);
+#define VEDIC_F32_INST(KIND)                                                                                  \
+    template __global__ void gemm_f32_kernel<0, CfgF32::BM, CfgF32::BN, CfgF32::ST, CfgF32::WGM, CfgF32::WGN, KIND>(  \
+        GemmArgs);                                                                                                \
+    template __global__ void gemm_f32_kernel<0, CfgF32Narrow::BM, CfgF32Narrow::BN, CfgF32Narrow::ST,              \
+                                             CfgF32Narrow::WGM, CfgF32Narrow::WGN, KIND>(GemmArgs);
 VEDIC_F32_INST(EK_PLAIN)
 VEDIC_F32_INST(EK_BIAS)
 VEDIC_F32_INST(EK_BIAS_GELU)

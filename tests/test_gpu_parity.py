@@ -419,3 +419,24 @@ def test_split_k_fp32_epilogues():
     Apad[:, :K] = A
     got = host(vedic.gemm(vedic.OP_NN, dev(Apad)[:, :K], dev(B)))
     check(got, o.NN, A, B, tol=tol, label="split-K fp32 unaligned")
+
+
+# ------------------------------------------------ narrow fp32 outputs (N <= 64)
+
+@pytest.mark.parametrize("opname", list(OPS))
+@pytest.mark.parametrize("shape", [(1000, 64, 300), (513, 40, 1000), (256, 8, 64), (300, 64, 5000), (77, 36, 130)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_narrow_fp32(opname, shape):
+    """fp32 products with N <= 64 take 256 x 64 tiles (with split-K where the
+    tile column has few tiles and K is long): ragged M and N, every layout,
+    beta = 1 accumulation."""
+    vedic = V()
+    layout = OPS[opname]
+    M, N, K = shape
+    rng = np.random.default_rng(zlib.crc32(f"narrow-{opname}-{shape}".encode()))
+    A, B = _operands(rng, layout, M, N, K)
+    C0 = normal(rng, (M, N))
+    got = host(vedic.gemm(layout, dev(A), dev(B)))
+    check(got, layout, A, B, tol=fp32_tol(K), label=f"narrow {opname} {shape}")
+    got = host(vedic.gemm(layout, dev(A), dev(B), dev(C0), beta=1.0))
+    check(got, layout, A, B, tol=fp32_tol(K), beta=1.0, C0=C0, label=f"narrow acc {opname} {shape}")
