@@ -143,15 +143,23 @@ __device__ __forceinline__ half8_t read_frag(const char* lds, int rc0, int kk, i
     }
 }
 
+// Scheduling-group masks (LLVM AMDGPU sched_group_barrier).
+constexpr int kSgMfma = 0x008, kSgVmem = 0x010, kSgDsRead = 0x100;
+
 // The MFMAs of one stage.  Fragments are double buffered across the BK / 16
 // k steps: the reads for step kk + 1 are interleaved with the MFMAs of step kk
 // (scheduling-group barriers), so LDS latency hides behind the matrix pipe.
-template <bool A_KC, bool B_KC, int BM, int BN, int BK, int MI, int NI>
+// NV > 0: the NV direct loads of a later stage, issued just before this call
+// in the same basic block, are placed one after every EVERY-th MFMA, so that
+// no wave blocks on a full texture-address queue while its MFMAs wait.
+template <bool A_KC, bool B_KC, int BM, int BN, int BK, int MI, int NI, int NV = 0, int EVERY = 1>
 __device__ __forceinline__ void mfma_stage(const char* la, const char* lb, int ar0, int bc0, int lane,
                                            float16_t (&acc)[MI][NI]) {
     constexpr int KS = BK / 16;
     constexpr int NR = (A_KC ? MI : 2 * MI) + (B_KC ? NI : 2 * NI);  // LDS reads per k step
     constexpr int NM = MI * NI;                                      // MFMAs per k step
+    static_assert(NV <= KS * NM, "at most one load per MFMA");
+    constexpr int EV = NV == 0 || NV * EVERY <= KS * NM ? EVERY : KS * NM / NV;  // spacing that fits
     half8_t af[2][MI], bf[2][NI];
 #pragma unroll
     for (int i = 0; i < MI; ++i) af[0][i] = read_frag<A_KC, BM, BK>(la, ar0 + 32 * i, 0, lane);
@@ -172,18 +180,34 @@ __device__ __forceinline__ void mfma_stage(const char* la, const char* lb, int a
             for (int j = 0; j < NI; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[c][i], bf[c][j], acc[i][j], 0, 0, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+    if constexpr (NV == 0) {
+        __builtin_amdgcn_sched_group_barrier(kSgDsRead, NR, 0);
 #pragma unroll
-    for (int kk = 0; kk + 1 < KS; ++kk) {
+        for (int kk = 0; kk + 1 < KS; ++kk) {
 #pragma unroll
-        for (int x = 0; x < (NR < NM ? NR : NM); ++x) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            for (int x = 0; x < (NR < NM ? NR : NM); ++x) {
+                __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+            }
+            if (NR > NM) __builtin_amdgcn_sched_group_barrier(kSgDsRead, NR > NM ? NR - NM : 1, 0);
+            if (NM > NR) __builtin_amdgcn_sched_group_barrier(kSgMfma, NM > NR ? NM - NR : 1, 0);
         }
-        if (NR > NM) __builtin_amdgcn_sched_group_barrier(0x100, NR > NM ? NR - NM : 1, 0);
-        if (NM > NR) __builtin_amdgcn_sched_group_barrier(0x008, NM > NR ? NM - NR : 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSgMfma, NM, 0);
+    } else {
+        // Same order, with load v after MFMA (v + 1) * EV - 1 of the stage.
+        __builtin_amdgcn_sched_group_barrier(kSgDsRead, NR, 0);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+#pragma unroll
+            for (int x = 0; x < NM; ++x) {
+                const int m = kk * NM + x;
+                __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+                if (kk + 1 < KS && x < NR) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+                if ((m + 1) % EV == 0 && (m + 1) / EV <= NV) __builtin_amdgcn_sched_group_barrier(kSgVmem, 1, 0);
+            }
+            if (kk + 1 < KS && NR > NM) __builtin_amdgcn_sched_group_barrier(kSgDsRead, NR > NM ? NR - NM : 1, 0);
+        }
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
 }
 
 // Logical tile t -> (tm, tn): GROUP_M tile rows at a time, column-major inside.
@@ -237,6 +261,10 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
     constexpr int L = SA::NLD + SB::NLD;  // load instructions per wave per stage
     static_assert(ST >= 2 && ST <= 4, "2 to 4 LDS stages");
     static_assert((ST - 2) * L < 64, "vmcnt range");
+    // 256 x 256 tiles: the stage's direct loads are spread one per MFMA instead
+    // of issued together (2-3 % faster: fewer waves held at a full
+    // texture-address queue); 128 x 128 tiles measured slower that way.
+    constexpr bool kInterleave = BM * BN >= 256 * 256;
 
     // One LDS object per stage (A then B): reads of one stage provably do not
     // alias the direct loads into another.  The compiler follows only a few
@@ -295,8 +323,18 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
                 wait_vmcnt<(ST - 2) * L>();  // stage kt has landed; ST - 2 later stages in flight
                 stage_barrier();
                 const int sl = (s + ST - 1) % ST;
-                VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
-                if (kt < nk) mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI>(As[s], Bs[s], wm * WM, wn * WN, lane, acc);
+                if constexpr (kInterleave) {
+                    // the loads and the MFMAs in one block, one load after each of the first L MFMAs
+                    if (kt < nk) {
+                        VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
+                        mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI, L, 1>(As[s], Bs[s], wm * WM, wn * WN, lane, acc);
+                    } else {
+                        VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
+                    }
+                } else {
+                    VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
+                    if (kt < nk) mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI>(As[s], Bs[s], wm * WM, wn * WN, lane, acc);
+                }
             }
         }
 
