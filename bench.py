@@ -88,6 +88,18 @@ WORKLOADS = {
         _g(1024, 8192, 4096, op="TN", beta=1.0), _g(4096, 8192, 1024, op="TN", beta=1.0),
     ]),
 }
+# Fused attention forward (cuda_flash_attention_fwd, cuda/VedicGEMM.cu:1065-1104) at the
+# reference's call: seq 8192, DH 64, 16 heads, causal, scale 1/sqrt(DH), fp32.  "per_head"
+# makes the reference's 16 one-head calls (cuda/ModelGPU.cu:959); "16heads" one launch.
+def _fa(seq=8192, dh=64, heads=16, batched=True, causal=1, shunyam=0, window=0, stride=1):
+    return dict(seq=seq, dh=dh, heads=heads, batched=batched, causal=causal, shunyam=shunyam, window=window,
+                stride=stride, dtype="fp32")
+
+
+WORKLOADS.update({
+    "flash_attn_fwd_fp32_16heads": dict(cfg=5, attn=_fa()),
+    "flash_attn_fwd_fp32_per_head": dict(cfg=5, attn=_fa(batched=False)),
+})
 COPY_WORKLOAD = "copy_256mib"  # calibration for the FETCH_SIZE / WRITE_SIZE counters
 
 
@@ -127,7 +139,9 @@ def _pmc_kib(dirpath: str, counter: str, kernel_substr: str):
 
 def summarize_traffic(args):
     fetch_dir, write_dir, cfetch_dir, cwrite_dir = args.summarize_traffic
-    kern = "gemm_f16_kernel" if WORKLOADS[args.workload]["gemms"][0]["dtype"] == "fp16" else "gemm_mfma_kernel"
+    w = WORKLOADS[args.workload]
+    kern = ("flash_attn_kernel" if "attn" in w
+            else "gemm_f16_kernel" if w["gemms"][0]["dtype"] == "fp16" else "gemm_f32_kernel")
     fetch, nf = _pmc_kib(fetch_dir, "FETCH_SIZE", kern)
     write, nw = _pmc_kib(write_dir, "WRITE_SIZE", kern)
     # torch's copy_ of 256 MiB (the runtime's copyBuffer blit) reads and writes exactly 256 MiB
@@ -164,6 +178,53 @@ def traffic_from_profiles(workload: str):
 
 
 # ------------------------------------------------------------------ CPU leg
+
+def attn_pairs(a: dict, q_begin: int = 0, q_end: int | None = None) -> int:
+    """(query, key) pairs the mask allows, summed over query rows [q_begin, q_end)."""
+    from oracle import oracle as o
+
+    seq = a["seq"]
+    q_end = seq if q_end is None else q_end
+    if not a["shunyam"] or seq <= a["window"]:
+        if a["causal"]:
+            return sum(q + 1 for q in range(q_begin, q_end))
+        return (q_end - q_begin) * seq
+    return int(o.attention_mask(seq, a["causal"], a["shunyam"], a["window"], a["stride"])[q_begin:q_end].sum())
+
+
+def cpu_baseline_attn(w: dict, seconds: float, seed: int = 7):
+    """The reference's flash_attention_kernel restated on the CPU (oracle/, one
+    thread, as one CUDA thread computes one query row there), on the last
+    query rows of one head: the rows with the most keys; flops are counted over
+    the allowed (query, key) pairs, 4 DH per pair, as on the GPU."""
+    from oracle import oracle as o
+
+    a = w["attn"]
+    seq, dh = a["seq"], a["dh"]
+    rng = np.random.default_rng(seed)
+    Q, K, V = (rng.standard_normal((seq, dh), dtype=np.float32) for _ in range(3))
+    rows = max(1, min(seq, int(2.0e9 * seconds / (4.0 * dh * seq))))  # ~2 GFLOP/s single thread
+    q0 = seq - rows
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        o.flash_attention_rows(Q, K, V, 1.0 / np.sqrt(dh), q0, seq, a["causal"], a["shunyam"], a["window"],
+                               a["stride"])
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    flops = reps * 4.0 * dh * attn_pairs(a, q0, seq)
+    return {
+        "value": flops / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"query rows {q0}..{seq - 1} of one head x{reps} ({flops / 1e9:.1f} GFLOP in {dt:.1f} s), "
+                  f"single thread, -O3 -march=x86-64",
+        "threads_available": os.cpu_count(),
+    }
+
 
 def cpu_baseline(w: dict, seconds: float, seed: int = 7):
     """The reference CPU path (single thread) on a row sample of the workload's
@@ -328,8 +389,85 @@ def time_steps(step, steps, warmup, torch):
     return ev0.elapsed_time(ev1) / steps, wall
 
 
+def make_attn_step(w: dict, dev, torch):
+    """Seeded Q/K/V for every head and the step: one multi-head launch, or one
+    launch per head as the reference calls it."""
+    from logos_amd import _lib
+
+    lib = _lib.load()
+    a = w["attn"]
+    seq, dh, H = a["seq"], a["dh"], a["heads"]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x4C4F474F ^ (w["cfg"] << 8))
+    stream = torch.cuda.current_stream().cuda_stream
+    qs, ks, vs, outs = [], [], [], []
+    for _ in range(H):
+        qs.append(torch.randn((seq, dh), generator=gen, device=dev))
+        ks.append(torch.randn((seq, dh), generator=gen, device=dev))
+        vs.append(torch.randn((seq, dh), generator=gen, device=dev))
+        outs.append(torch.empty((seq, dh), device=dev))
+    arr = lambda ts: (ctypes.c_void_p * H)(*[t.data_ptr() for t in ts])
+    pq, pk, pv, po = arr(qs), arr(ks), arr(vs), arr(outs)
+    scale = 1.0 / float(dh) ** 0.5
+    flags = (a["causal"], a["shunyam"], a["window"], a["stride"])
+
+    def step():
+        if a["batched"]:
+            rc = lib.vedic_flash_attention_fwd_heads(pq, pk, pv, po, H, seq, dh, scale, *flags, stream)
+            if rc:
+                raise RuntimeError(f"flash attention failed: {_lib.status_string(rc)}")
+            return
+        for h in range(H):
+            rc = lib.vedic_flash_attention_fwd(qs[h].data_ptr(), ks[h].data_ptr(), vs[h].data_ptr(),
+                                               outs[h].data_ptr(), None, seq, dh, scale, *flags, stream)
+            if rc:
+                raise RuntimeError(f"flash attention failed: {_lib.status_string(rc)}")
+
+    step.keep = (qs, ks, vs, outs, pq, pk, pv, po)
+    flops = 4.0 * dh * attn_pairs(a) * H
+    hbm = 4 * seq * dh * 4 * H  # Q, K, V read once, out written
+    launches = 1 if a["batched"] else H
+    return step, flops, hbm, launches
+
+
+def run_attn_workload(name, args, torch, dev, with_cpu):
+    w = WORKLOADS[name]
+    a = w["attn"]
+    step, flops, hbm, launches = make_attn_step(w, dev, torch)
+    ms, wall = time_steps(step, args.steps, args.warmup, torch)
+    tflops = flops / (ms * 1e-3) / 1e12
+    roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK["fp32"], "unit": "TFLOP/s",
+            "frac": round(tflops / PEAK["fp32"], 4), "traffic": traffic_from_profiles(name),
+            "algorithmic_flops_per_launch": flops / launches, "algorithmic_bytes_per_launch": hbm / launches,
+            "kernel_avg_us": round(ms * 1e3 / launches, 3)}
+    cpu = cpu_baseline_attn(w, args.cpu_seconds) if with_cpu else None
+    return {
+        "metric": f"attention forward TFLOP/s, {name}, 1 GPU",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded torch.randn Q, K, V ~ N(0,1))",
+        "config": {"workload": name, "baseline_config": w["cfg"], "seq": a["seq"], "dh": a["dh"],
+                   "heads": a["heads"], "launches": launches, "causal": a["causal"], "shunyam": a["shunyam"],
+                   "scale": "1/sqrt(dh)", "flops": "4 dh per allowed (query, key) pair"},
+        "pct_of_peak": round(100.0 * tflops / PEAK["fp32"], 2),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "wall_s": round(wall, 4),
+    }
+
+
 def run_workload(name, args, torch, dev, with_cpu):
     w = WORKLOADS[name]
+    if "attn" in w:
+        return run_attn_workload(name, args, torch, dev, with_cpu)
     step, items = make_step(w, dev, torch)
     ms, wall = time_steps(step, args.steps, args.warmup, torch)
     flops = sum(f for _, f, _ in items)

@@ -324,6 +324,33 @@ inline void cuda_cast_pack_fp16(const float* const* src, int nsrc, int rows, int
                      "cuda_cast_pack_fp16");
 }
 
+// --------------------------------------------------- attention
+
+// cuda_flash_attention_fwd (cuda/VedicGEMM.cuh:236, cuda/VedicGEMM.cu:1065-1104):
+// out = softmax(scale Q K^T + mask) V for one head, fp32 [seq x DH].  As in the
+// reference, DH > 128 throws std::runtime_error; this build also needs DH 64
+// or 128 and attn_ptr == nullptr (std::invalid_argument otherwise).
+inline void cuda_flash_attention_fwd(const float* Q, const float* K, const float* V, float* out, float* attn_ptr,
+                                     int seq, int DH, float scale, bool causal, bool shunyam, int window, int stride,
+                                     hipStream_t stream = nullptr) {
+    if (DH > 128)
+        throw std::runtime_error("cuda_flash_attention_fwd: DH=" + std::to_string(DH) +
+                                 " is above the supported maximum of 128");
+    vedic_hip::check(vedic_flash_attention_fwd(Q, K, V, out, attn_ptr, seq, DH, scale, causal ? 1 : 0,
+                                               shunyam ? 1 : 0, window, stride, stream),
+                     "cuda_flash_attention_fwd");
+}
+
+// All heads of a layer in one launch (new: the reference calls the one-head
+// kernel per head, cuda/ModelGPU.cu:888-968).
+inline void cuda_flash_attention_fwd_heads(const float* const* Q, const float* const* K, const float* const* V,
+                                           float* const* out, int nheads, int seq, int DH, float scale, bool causal,
+                                           bool shunyam, int window, int stride, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_flash_attention_fwd_heads(Q, K, V, out, nheads, seq, DH, scale, causal ? 1 : 0,
+                                                     shunyam ? 1 : 0, window, stride, stream),
+                     "cuda_flash_attention_fwd_heads");
+}
+
 // --------------------------------------------------- elementwise helpers
 
 // C[i][j] += bias[j] (the add_bias_kernel launch, cuda/VedicGEMM.cu:96-102).

@@ -57,7 +57,8 @@ typedef enum {
     VEDIC_STATUS_BAD_EPILOGUE = 5, /* unknown epilogue / bias missing */
     VEDIC_STATUS_BAD_DTYPE = 6,    /* unsupported dtype combination */
     VEDIC_STATUS_HIP_ERROR = 7,    /* HIP runtime or launch error */
-    VEDIC_STATUS_TOO_LARGE = 8     /* size beyond a documented limit */
+    VEDIC_STATUS_TOO_LARGE = 8,    /* size beyond a documented limit */
+    VEDIC_STATUS_UNSUPPORTED = 9   /* a case this build does not provide (documented per call) */
 } vedic_status_t;
 
 typedef enum {
@@ -247,6 +248,32 @@ int vedic_verify(const float* A, const float* B, const float* C, int M, int K, i
  * reference verifies with a separate pass over C at checkpoints
  * (cuda/train_gpu.cu:1695-1719). */
 int vedic_gemm_checked(const vedic_gemm_desc_t* desc, float tolerance, vedic_verify_result_t* out);
+
+/* ---- attention ------------------------------------------------------------ */
+
+/* Fused attention forward of one head, fp32:
+ *   out[seq x dh] = softmax(scale * Q K^T + mask) V,   Q, K, V [seq x dh] row-major
+ * mask: key > query when `causal`; when `shunyam` and seq > window, also every
+ * key outside [query - window, query] that is not a multiple of `stride`.
+ * Masked scores are left out of the sums; a row whose sum is <= 1e-9 is 0.
+ * Replaces cuda_flash_attention_fwd (cuda/VedicGEMM.cuh:236, cuda/VedicGEMM.cu:1065-1104;
+ * kernel :898-1063), called per head at cuda/ModelGPU.cu:959-968.
+ * Limits: dh 64 or 128 (others VEDIC_STATUS_UNSUPPORTED; dh > 128 BAD_DIM,
+ * where the reference throws); `attn` (the reference's optional copy of the
+ * probabilities, NULL at its only call site) must be NULL (UNSUPPORTED
+ * otherwise); 16-byte-aligned Q, K, V, out; stride >= 1 when the sparse mask
+ * applies; seq * dh < 2^29.  A call on a single head splits long key ranges
+ * over several workgroups and takes a stream-ordered workspace (hipMallocAsync
+ * on `stream`, freed the same way) for the partial results. */
+int vedic_flash_attention_fwd(const float* Q, const float* K, const float* V, float* out, float* attn, int seq,
+                              int dh, float scale, int causal, int shunyam, int window, int stride, void* stream);
+
+/* The same for nheads (1..64) heads in one launch: Q[h], K[h], V[h], out[h]
+ * per head, every head [seq x dh].  New: the reference calls the one-head
+ * kernel once per head (cuda/ModelGPU.cu:888-968). */
+int vedic_flash_attention_fwd_heads(const float* const* Q, const float* const* K, const float* const* V,
+                                    float* const* out, int nheads, int seq, int dh, float scale, int causal,
+                                    int shunyam, int window, int stride, void* stream);
 
 /* ---- backend queries --------------------------------------------------- */
 

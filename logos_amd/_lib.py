@@ -26,6 +26,7 @@ STATUS_BAD_EPILOGUE = 5
 STATUS_BAD_DTYPE = 6
 STATUS_HIP_ERROR = 7
 STATUS_TOO_LARGE = 8
+STATUS_UNSUPPORTED = 9
 
 OP_NN, OP_NT, OP_TN = 0, 1, 2
 EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU, EPI_GELU_BWD = 0, 1, 2, 3, 4
@@ -99,6 +100,13 @@ SIGNATURES = {
         [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_float, ctypes.POINTER(VerifyResult), c_vp],
     ),
     "vedic_gemm_checked": (c_int, [ctypes.POINTER(GemmDesc), c_float, ctypes.POINTER(VerifyResult)]),
+    "vedic_flash_attention_fwd": (
+        c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_vp]),
+    "vedic_flash_attention_fwd_heads": (
+        c_int,
+        [ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), c_int, c_int,
+         c_int, c_float, c_int, c_int, c_int, c_int, c_vp],
+    ),
     "vedic_uses_vendor_blas": (c_int, []),
     "vedic_backend_name": (c_char_p, []),
     "vedic_status_string": (c_char_p, [c_int]),

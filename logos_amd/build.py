@@ -30,6 +30,7 @@ SOURCES = [
     "vedic_gemm_f32_tn.hip",
     "vedic_gemm_mfma.hip",
     "vedic_gemm_skinny.hip",
+    "vedic_flash_attn.hip",
     "vedic_capi.hip",
 ]
 

@@ -8,6 +8,7 @@
 #include <atomic>
 
 #include "../../include/logos_vedic.h"
+#include "vedic_flash_attn.hpp"
 #include "vedic_common.hpp"
 #include "vedic_epilogue.hpp"
 
@@ -882,6 +883,72 @@ extern "C" int vedic_gemm_checked(const vedic_gemm_desc_t* d, float tolerance, v
 
 // --------------------------------------------------------------- queries
 
+// ------------------------------------------------------------ attention
+
+static int flash_impl(const float* const* Q, const float* const* K, const float* const* V, float* const* out,
+                      int nheads, int seq, int dh, float scale, int causal, int shunyam, int window, int stride,
+                      void* stream) {
+    if (nheads < 1 || seq < 1 || dh < 1 || dh > 128) return VEDIC_STATUS_BAD_DIM;
+    if (nheads > kMaxHeads) return VEDIC_STATUS_TOO_LARGE;
+    if (dh != 64 && dh != 128) return VEDIC_STATUS_UNSUPPORTED;
+    if ((int64_t)seq * dh >= (int64_t(1) << 29)) return VEDIC_STATUS_TOO_LARGE;
+    const bool sparse = shunyam && seq > window;
+    if (sparse && stride < 1) return VEDIC_STATUS_BAD_DIM;
+    if (!Q || !K || !V || !out) return VEDIC_STATUS_NULL_POINTER;
+    FlashArgs a{};
+    for (int h = 0; h < nheads; ++h) {
+        if (!Q[h] || !K[h] || !V[h] || !out[h]) return VEDIC_STATUS_NULL_POINTER;
+        if (!aligned16(Q[h]) || !aligned16(K[h]) || !aligned16(V[h]) || !aligned16(out[h]))
+            return VEDIC_STATUS_UNSUPPORTED;
+        a.q[h] = Q[h];
+        a.k[h] = K[h];
+        a.v[h] = V[h];
+        a.o[h] = out[h];
+    }
+    a.nheads = nheads;
+    a.seq = seq;
+    a.nqg = (seq + kFaQ - 1) / kFaQ;
+    a.causal = causal ? 1 : 0;
+    a.sparse = sparse ? 1 : 0;
+    a.window = window;
+    a.stride = sparse ? stride : 1;
+    a.scale = scale;
+    // Whole key range per work item, unless that leaves fewer than two work
+    // items per CU: then halve the key chunk (multiples of 128, at least 512)
+    // and merge the chunks afterwards.
+    const int full = a.nqg * kFaQ;
+    int chunk = full;
+    int64_t items = flash_items_per_head(seq, chunk, a.causal);
+    const int64_t target = 2 * (int64_t)device_cu_count();
+    while (items * nheads < target && chunk > 512) {
+        chunk = std::max(512, (chunk / 2 + kFaQ - 1) / kFaQ * kFaQ);
+        items = flash_items_per_head(seq, chunk, a.causal);
+    }
+    a.chunk = chunk;
+    a.items = (int)items;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (chunk >= full) return hip_status(launch_flash_attn(a, dh, s));
+    const size_t bytes = sizeof(float) * (size_t)flash_slot_floats(dh) * (size_t)items * nheads;
+    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&a.part), bytes, s);
+    if (e != hipSuccess) return hip_status(e);
+    e = launch_flash_attn(a, dh, s);
+    const hipError_t f = hipFreeAsync(a.part, s);
+    return hip_status(e != hipSuccess ? e : f);
+}
+
+extern "C" int vedic_flash_attention_fwd(const float* Q, const float* K, const float* V, float* out, float* attn,
+                                         int seq, int dh, float scale, int causal, int shunyam, int window,
+                                         int stride, void* stream) {
+    if (attn != nullptr) return VEDIC_STATUS_UNSUPPORTED;
+    return flash_impl(&Q, &K, &V, &out, 1, seq, dh, scale, causal, shunyam, window, stride, stream);
+}
+
+extern "C" int vedic_flash_attention_fwd_heads(const float* const* Q, const float* const* K, const float* const* V,
+                                               float* const* out, int nheads, int seq, int dh, float scale,
+                                               int causal, int shunyam, int window, int stride, void* stream) {
+    return flash_impl(Q, K, V, out, nheads, seq, dh, scale, causal, shunyam, window, stride, stream);
+}
+
 extern "C" int vedic_uses_vendor_blas(void) { return 0; }
 
 extern "C" const char* vedic_backend_name(void) { return "hip-native-gfx950"; }
@@ -899,6 +966,7 @@ extern "C" const char* vedic_status_string(int status) {
         case VEDIC_STATUS_BAD_DTYPE: return "unsupported dtype combination";
         case VEDIC_STATUS_HIP_ERROR: return "HIP runtime error";
         case VEDIC_STATUS_TOO_LARGE: return "size beyond the documented limit";
+        case VEDIC_STATUS_UNSUPPORTED: return "case not provided by this build (see the entry point's limits)";
     }
     return "unknown status";
 }

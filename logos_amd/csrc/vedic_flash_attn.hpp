@@ -1,0 +1,50 @@
+// vedic_flash_attn.hpp -- work decomposition of the fused attention forward
+// (vedic_flash_attn.hip), shared with the C ABI that sizes and launches it.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vedic_common.hpp"
+
+namespace vedic {
+
+constexpr int kFaQ = 128;     // queries per work item (four waves x 32)
+constexpr int kFaKeys = 32;   // keys per LDS block
+constexpr int kFaStages = 3;  // LDS blocks in flight
+constexpr float kFaMasked = -1e30f;
+
+struct FlashArgs {
+    const float* q[kMaxHeads];
+    const float* k[kMaxHeads];
+    const float* v[kMaxHeads];
+    float* o[kMaxHeads];
+    float* part;  // chunk partials: [heads][items][kFaQ * DH + 2 * kFaQ]; null when unsplit
+    int nheads, seq, nqg;
+    int chunk;  // keys per work item, a multiple of kFaQ
+    int items;  // work items per head
+    int causal, sparse, window, stride;
+    float scale;
+};
+
+// Keys a query group sees: causal groups stop at their last query.
+__host__ __device__ inline int fa_kend(const FlashArgs& a, int g) {
+    return a.causal ? min(a.seq, kFaQ * (g + 1)) : a.seq;
+}
+__host__ __device__ inline int fa_nchunks(const FlashArgs& a, int g) {
+    return (fa_kend(a, g) + a.chunk - 1) / a.chunk;
+}
+// Work items of the query groups before g.  Causal: group g has
+// ceil(128 (g + 1) / chunk) = g / R + 1 chunks (R = chunk / 128; the seq clamp
+// of the last group changes no count because chunk is a multiple of 128).
+__host__ __device__ inline int64_t fa_prefix(const FlashArgs& a, int g) {
+    if (!a.causal) return (int64_t)g * fa_nchunks(a, 0);
+    const int64_t R = a.chunk / kFaQ, q = g / R, r = g % R;
+    return g + R * q * (q - 1) / 2 + q * r;
+}
+
+int64_t flash_items_per_head(int seq, int chunk, int causal);
+int flash_slot_floats(int dh);
+hipError_t launch_flash_attn(const FlashArgs& a, int dh, hipStream_t s);
+
+}  // namespace vedic

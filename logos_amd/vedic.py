@@ -12,6 +12,7 @@ Names and argument meaning follow the reference:
   bias_grad(dY)                    bias_grad_kernel (cuda/train_gpu.cu:263-273), deterministic
   add_bias / gelu_ / cast_*        add_bias_kernel, cuda_gelu, cuda_cast_fp32_to_fp16 ...
   verify(A, B, C)                  cuda_vedic_verify (cuda/VedicGEMM.cu:765-814)
+  flash_attention_fwd(Q, K, V)     cuda_flash_attention_fwd (cuda/VedicGEMM.cu:1065-1104)
 
 Operands are torch tensors resident on the GPU (torch is used for device
 memory and streams only); every call runs on torch's current stream.  Shape
@@ -36,6 +37,7 @@ __all__ = [
     "cast_pack_fp16", "add_bias", "gelu_",
     "cast_fp32_to_fp16",
     "cast_fp16_to_fp32", "verify", "gemm_checked", "VerifyResult", "uses_vendor_blas", "backend_name",
+    "flash_attention_fwd", "flash_attention_fwd_heads",
 ]
 
 _DT = {torch.float32: DT_F32, torch.float16: DT_F16}
@@ -47,7 +49,7 @@ def _check(status: int) -> None:
     msg = _lib.status_string(status)
     if status in (_lib.STATUS_BAD_DIM, _lib.STATUS_BAD_LD, _lib.STATUS_BAD_LAYOUT,
                   _lib.STATUS_BAD_EPILOGUE, _lib.STATUS_BAD_DTYPE, _lib.STATUS_NULL_POINTER,
-                  _lib.STATUS_TOO_LARGE):
+                  _lib.STATUS_TOO_LARGE, _lib.STATUS_UNSUPPORTED):
         raise ValueError(f"VedicGEMM: {msg}")
     code = _lib.load().vedic_last_hip_error()
     raise RuntimeError(f"VedicGEMM: {msg} (hipError {code})")
@@ -359,3 +361,65 @@ def uses_vendor_blas() -> bool:
 
 def backend_name() -> str:
     return _lib.load().vedic_backend_name().decode()
+
+
+def _head(t: torch.Tensor, name: str, seq: int | None = None, dh: int | None = None) -> tuple[int, int]:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda or t.dtype != torch.float32 or t.dim() != 2 \
+            or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous float32 [seq x dh] GPU matrix")
+    s, d = t.shape
+    if (seq is not None and s != seq) or (dh is not None and d != dh):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected [{seq} x {dh}]")
+    return s, d
+
+
+def flash_attention_fwd(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, out: torch.Tensor | None = None,
+                        scale: float | None = None, causal: bool = True, shunyam: bool = False, window: int = 0,
+                        stride: int = 1, attn: torch.Tensor | None = None) -> torch.Tensor:
+    """out = softmax(scale Q K^T + mask) V for one head, fp32 [seq x dh] (dh 64
+    or 128): cuda_flash_attention_fwd (cuda/VedicGEMM.cu:1065-1104).  scale
+    defaults to 1/sqrt(dh), the caller's value (cuda/ModelGPU.cu:963).  The
+    mask drops keys after the query (causal) and, with shunyam and seq >
+    window, keys outside [query - window, query] that are not multiples of
+    stride.  `attn` (the reference's optional probability copy) must be None."""
+    seq, dh = _head(Q, "Q")
+    _head(K, "K", seq, dh)
+    _head(V, "V", seq, dh)
+    if out is None:
+        out = torch.empty_like(Q)
+    _head(out, "out", seq, dh)
+    if scale is None:
+        scale = 1.0 / float(dh) ** 0.5
+    ap = None if attn is None else attn.data_ptr()
+    _check(_lib.load().vedic_flash_attention_fwd(Q.data_ptr(), K.data_ptr(), V.data_ptr(), out.data_ptr(), ap, seq,
+                                                 dh, float(scale), int(causal), int(shunyam), int(window),
+                                                 int(stride), _stream()))
+    return out
+
+
+def flash_attention_fwd_heads(Qs: list[torch.Tensor], Ks: list[torch.Tensor], Vs: list[torch.Tensor],
+                              outs: list[torch.Tensor] | None = None, scale: float | None = None,
+                              causal: bool = True, shunyam: bool = False, window: int = 0,
+                              stride: int = 1) -> list[torch.Tensor]:
+    """flash_attention_fwd for several heads (all [seq x dh]) in one launch."""
+    n = len(Qs)
+    if n == 0 or len(Ks) != n or len(Vs) != n:
+        raise ValueError("Qs, Ks and Vs must be non-empty lists of the same length")
+    seq, dh = _head(Qs[0], "Q[0]")
+    for i in range(n):
+        _head(Qs[i], f"Q[{i}]", seq, dh)
+        _head(Ks[i], f"K[{i}]", seq, dh)
+        _head(Vs[i], f"V[{i}]", seq, dh)
+    if outs is None:
+        outs = [torch.empty_like(q) for q in Qs]
+    if len(outs) != n:
+        raise ValueError("outs must have one tensor per head")
+    for i in range(n):
+        _head(outs[i], f"out[{i}]", seq, dh)
+    if scale is None:
+        scale = 1.0 / float(dh) ** 0.5
+    arr = lambda ts: (ctypes.c_void_p * n)(*[t.data_ptr() for t in ts])
+    _check(_lib.load().vedic_flash_attention_fwd_heads(arr(Qs), arr(Ks), arr(Vs), arr(outs), n, seq, dh,
+                                                       float(scale), int(causal), int(shunyam), int(window),
+                                                       int(stride), _stream()))
+    return outs

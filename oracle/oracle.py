@@ -47,6 +47,8 @@ def _load():
             "oracle_f16_to_f32": [_u16p, _fp, _i64],
             "oracle_gemm_f64": [_i, _fp, _fp, _fp, _i, _i, _i, _i, _dp, _dp, _i],
             "oracle_checksum": [_fp, _fp, _fp, _i, _i, _i, _dp, _dp],
+            "oracle_flash_attention": [_fp, _fp, _fp, _fp, _i, _i, ctypes.c_float, _i, _i, _i, _i],
+            "oracle_flash_attention_rows": [_fp, _fp, _fp, _fp, _i, _i, ctypes.c_float, _i, _i, _i, _i, _i, _i],
         }
         for name, args in sig.items():
             fn = getattr(lib, name)
@@ -360,3 +362,62 @@ def fp32_tolerance(K: int) -> float:
 
 
 FP16_TOLERANCE = 2e-3
+
+
+# ------------------------------------------------------------ attention
+
+def attention_mask(seq, causal=True, shunyam=False, window=0, stride=1) -> np.ndarray:
+    """allowed[q, k] of the reference's flash_attention_kernel
+    (cuda/VedicGEMM.cu:984-995): key < seq; not (causal and k > q); with
+    shunyam and seq > window, k in [q - window, q] or k % stride == 0."""
+    q = np.arange(seq)[:, None]
+    k = np.arange(seq)[None, :]
+    ok = np.ones((seq, seq), dtype=bool)
+    if causal:
+        ok &= k <= q
+    if shunyam and seq > window:
+        ok &= ((k >= q - window) & (k <= q)) | (k % stride == 0)
+    return ok
+
+
+def flash_attention_f64(Q, K, V, scale, causal=True, shunyam=False, window=0, stride=1, rows=None):
+    """float64 closed form: softmax over the allowed keys of scale * Q K^T,
+    times V; a row with no allowed key is 0.  rows: optional query subset."""
+    Q = np.asarray(Q, dtype=np.float64)
+    K = np.asarray(K, dtype=np.float64)
+    V = np.asarray(V, dtype=np.float64)
+    seq = K.shape[0]
+    idx = np.arange(seq) if rows is None else np.asarray(rows)
+    mask = attention_mask(seq, causal, shunyam, window, stride)[idx]
+    S = scale * (Q[idx] @ K.T)
+    S = np.where(mask, S, -np.inf)
+    m = S.max(axis=1, keepdims=True)
+    m = np.where(np.isfinite(m), m, 0.0)
+    P = np.where(mask, np.exp(S - m), 0.0)
+    den = P.sum(axis=1, keepdims=True)
+    return np.where(den > 0, (P @ V) / np.where(den > 0, den, 1.0), 0.0)
+
+
+def flash_attention(Q, K, V, scale, causal=True, shunyam=False, window=0, stride=1) -> np.ndarray:
+    """The reference's flash_attention_kernel restated on the CPU (fp32)."""
+    Q, K, V = _f32(Q), _f32(K), _f32(V)
+    seq, dh = Q.shape
+    out = np.empty_like(Q)
+    rc = _load().oracle_flash_attention(_p(Q), _p(K), _p(V), _p(out), seq, dh, float(scale), int(causal),
+                                        int(shunyam), int(window), int(stride))
+    if rc != 0:
+        raise ValueError(f"oracle_flash_attention failed ({rc})")
+    return out
+
+
+def flash_attention_rows(Q, K, V, scale, q_begin, q_end, causal=True, shunyam=False, window=0, stride=1):
+    """flash_attention for query rows q_begin .. q_end - 1 only (rows of the
+    result outside that range are left 0): a bounded CPU sample."""
+    Q, K, V = _f32(Q), _f32(K), _f32(V)
+    seq, dh = Q.shape
+    out = np.zeros_like(Q)
+    rc = _load().oracle_flash_attention_rows(_p(Q), _p(K), _p(V), _p(out), seq, dh, float(scale), int(causal),
+                                             int(shunyam), int(window), int(stride), int(q_begin), int(q_end))
+    if rc != 0:
+        raise ValueError(f"oracle_flash_attention_rows failed ({rc})")
+    return out

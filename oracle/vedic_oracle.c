@@ -45,6 +45,20 @@
  *     explicit transpose.
  *   - gelu is checked against an independent float64 evaluation and its
  *     closed-form special values (gelu(0)=0, gelu(x)->x, gelu(-x)->0).
+ *
+ *  3. oracle_flash_attention <- cuda/VedicGEMM.cu:898-1063 (flash_attention_kernel):
+ *     16-query blocks, 16-key tiles, running max and sum, expf, masked scores
+ *     at -1e30 left out of the sums, division by the sum at the end.  The
+ *     reference is a CUDA kernel, which nvcc compiles with multiply-add
+ *     contraction on by default; its two multiply-accumulate loops (the Q.K
+ *     dot and O += e V) are therefore written with fmaf, the rest as plain
+ *     fp32 operations.  CUDA's expf and glibc's differ in the last ulp, so
+ *     this is the reference's algorithm, not its bits.  Pinned in
+ *     tests/test_oracle.py against a float64 closed form (softmax over the
+ *     allowed keys, then times V), against one-hot V (the output is then the
+ *     probability row itself, which exposes the mask and the weights), zero K
+ *     (uniform weights over the allowed keys: the mean of their V rows) and
+ *     a sparse pattern that leaves each query exactly the keys {0, q}.
  */
 #include <math.h>
 #include <pthread.h>
@@ -358,4 +372,75 @@ int oracle_checksum(const float* A, const float* B, const float* C, int M, int K
     *sum_c = s;
     *predicted = pred;
     return 0;
+}
+
+/* ------------------------------------------------------ flash attention */
+
+#define ORACLE_FA_TILE 16 /* FA_TILE, cuda/VedicGEMM.cu:898 */
+
+/* out[seq x dh] = softmax(scale Q K^T + mask) V for one head, the reference's
+ * flash_attention_kernel (cuda/VedicGEMM.cu:901-1063) run on the CPU: each
+ * query row (one CUDA thread there) scans the keys in tiles of 16; masks:
+ * key >= seq, causal key > query, and with shunyam && seq > window keys
+ * outside [query - window, query] that are not multiples of stride
+ * (:984-995). */
+int oracle_flash_attention_rows(const float* Q, const float* K, const float* V, float* out, int seq, int dh,
+                                float scale, int causal, int shunyam, int window, int stride, int q_begin,
+                                int q_end) {
+    if (seq <= 0 || dh <= 0 || q_begin < 0 || q_end > seq || q_begin > q_end) return -1;
+    const int sparse = shunyam && seq > window;
+    if (sparse && stride <= 0) return -2;
+    float* o = (float*)malloc(sizeof(float) * (size_t)dh);
+    if (!o) return -3;
+    const int tiles = (seq + ORACLE_FA_TILE - 1) / ORACLE_FA_TILE;
+    for (int q = q_begin; q < q_end; ++q) {
+        const float* qi = Q + (int64_t)q * dh;
+        float m = -1e30f, l = 0.0f;
+        for (int d = 0; d < dh; ++d) o[d] = 0.0f;
+        for (int t = 0; t < tiles; ++t) {
+            float s[ORACLE_FA_TILE];
+            float tile_max = -1e30f;
+            for (int j = 0; j < ORACLE_FA_TILE; ++j) {
+                const int k = t * ORACLE_FA_TILE + j;
+                int masked = k >= seq || (causal && k > q);
+                if (!masked && sparse) {
+                    const int in_window = k >= q - window && k <= q;
+                    const int global = k % stride == 0;
+                    masked = !in_window && !global;
+                }
+                if (masked) {
+                    s[j] = -1e30f;
+                    continue;  /* masked keys stay out of the tile max */
+                }
+                const float* ki = K + (int64_t)k * dh;
+                float dot = 0.0f;
+                for (int d = 0; d < dh; ++d) dot = fmaf(qi[d], ki[d], dot);
+                s[j] = dot * scale;
+                tile_max = fmaxf(tile_max, s[j]);
+            }
+            const float m_new = fmaxf(m, tile_max);
+            const float shift = expf(m - m_new);
+            for (int d = 0; d < dh; ++d) o[d] *= shift;
+            float l_new = l * shift;
+            for (int j = 0; j < ORACLE_FA_TILE; ++j) {
+                if (s[j] <= -1e29f) continue;
+                const float e = expf(s[j] - m_new);
+                l_new += e;
+                const float* vi = V + (int64_t)(t * ORACLE_FA_TILE + j) * dh;
+                for (int d = 0; d < dh; ++d) o[d] = fmaf(e, vi[d], o[d]);
+            }
+            m = m_new;
+            l = l_new;
+        }
+        const float inv = l > 1e-9f ? 1.0f / l : 0.0f;
+        for (int d = 0; d < dh; ++d) out[(int64_t)q * dh + d] = o[d] * inv;
+    }
+    free(o);
+    return 0;
+}
+
+/* All query rows (rows q_begin .. q_end - 1 above: a bounded sample for timing). */
+int oracle_flash_attention(const float* Q, const float* K, const float* V, float* out, int seq, int dh,
+                           float scale, int causal, int shunyam, int window, int stride) {
+    return oracle_flash_attention_rows(Q, K, V, out, seq, dh, scale, causal, shunyam, window, stride, 0, seq);
 }

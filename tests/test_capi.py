@@ -88,3 +88,24 @@ def test_python_mirror_rejects_cpu_tensors():
 
     with pytest.raises(ValueError):
         vedic.vedic_gemm(torch.ones(2, 2), torch.ones(2, 2))
+
+
+def test_flash_attention_validation():
+    """Argument checks of the attention entry points, all before any device
+    call: the reference throws for DH > 128 (cuda/VedicGEMM.cu:1074-1080)."""
+    lib = _lib.load()
+    p = 1 << 12  # aligned stand-in addresses; never dereferenced
+    f = lib.vedic_flash_attention_fwd
+    assert f(p, p, p, p, None, 0, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_BAD_DIM
+    assert f(p, p, p, p, None, 16, 256, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_BAD_DIM
+    assert f(p, p, p, p, None, 16, 32, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED
+    assert f(p, p, p, p, p, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED  # attn copy
+    assert f(p, p, p, None, None, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_NULL_POINTER
+    assert f(p + 4, p, p, p, None, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED  # misaligned
+    assert f(p, p, p, p, None, 16, 64, 0.125, 1, 1, 4, 0, None) == _lib.STATUS_BAD_DIM  # stride 0, sparse on
+    assert f(p, p, p, p, None, 1 << 23, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_TOO_LARGE
+    arr = (ctypes.c_void_p * 65)(*([p] * 65))
+    g = lib.vedic_flash_attention_fwd_heads
+    assert g(arr, arr, arr, arr, 65, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_TOO_LARGE
+    assert g(arr, arr, arr, arr, 0, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_BAD_DIM
+    assert _lib.status_string(_lib.STATUS_UNSUPPORTED).startswith("case not provided")

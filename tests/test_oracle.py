@@ -287,3 +287,106 @@ def test_rejects_bad_dims():
         o.vedic_gemm(np.ones((2, 3)), np.ones((2, 3)))
     with pytest.raises(ValueError):
         o.vedic_gemm_bias(np.ones((2, 3)), np.ones((3, 4)), np.ones(3))
+
+
+# ------------------------------------------------------------ attention
+
+def _mask_brute(seq, causal, shunyam, window, stride):
+    """The reference kernel's conditions (cuda/VedicGEMM.cu:984-995) one pair at a time."""
+    ok = np.zeros((seq, seq), dtype=bool)
+    for q in range(seq):
+        for k in range(seq):
+            if causal and k > q:
+                continue
+            if shunyam and seq > window:
+                in_window = q - window <= k <= q
+                if not in_window and k % stride != 0:
+                    continue
+            ok[q, k] = True
+    return ok
+
+
+MASKS = [(1, 0, 0, 1), (0, 0, 0, 1), (1, 1, 8, 4), (0, 1, 5, 7), (1, 1, 0, 1000), (1, 1, 100, 3)]
+
+
+@pytest.mark.parametrize("causal,shunyam,window,stride", MASKS)
+def test_attention_mask_matches_reference_conditions(causal, shunyam, window, stride):
+    for seq in (1, 9, 40):
+        assert np.array_equal(o.attention_mask(seq, causal, shunyam, window, stride),
+                              _mask_brute(seq, causal, shunyam, window, stride))
+
+
+@pytest.mark.parametrize("causal,shunyam,window,stride", MASKS)
+@pytest.mark.parametrize("seq,dh", [(1, 64), (37, 64), (70, 128)])
+def test_flash_restatement_against_f64(seq, dh, causal, shunyam, window, stride):
+    rng = np.random.default_rng(seq * 7 + dh + window)
+    Q, K, V = (rng.standard_normal((seq, dh), dtype=np.float32) for _ in range(3))
+    scale = 1.0 / np.sqrt(dh)
+    got = o.flash_attention(Q, K, V, scale, causal, shunyam, window, stride)
+    want = o.flash_attention_f64(Q, K, V, scale, causal, shunyam, window, stride)
+    assert o.inf_rel_err(got, want) <= o.fp32_tolerance(dh)
+
+
+def test_flash_one_hot_values_expose_the_weights():
+    """V = [I | 0]: output row q is the probability row itself, so the mask and
+    every weight are visible; the weights are checked against an independent
+    per-row softmax."""
+    seq, dh = 48, 64
+    rng = np.random.default_rng(3)
+    Q = rng.standard_normal((seq, dh), dtype=np.float32)
+    K = rng.standard_normal((seq, dh), dtype=np.float32)
+    V = np.zeros((seq, dh), np.float32)
+    V[:, :seq] = np.eye(seq, dtype=np.float32)
+    scale = 0.125
+    for causal, shunyam, window, stride in MASKS:
+        P = o.flash_attention(Q, K, V, scale, causal, shunyam, window, stride)[:, :seq]
+        allowed = _mask_brute(seq, causal, shunyam, window, stride)
+        assert np.all((P > 0) == allowed)
+        for q in range(seq):
+            ks = np.nonzero(allowed[q])[0]
+            s = scale * (Q[q].astype(np.float64) @ K[ks].T.astype(np.float64))
+            w = np.exp(s - s.max())
+            np.testing.assert_allclose(P[q, ks], w / w.sum(), rtol=2e-6, atol=1e-7)
+
+
+def test_flash_zero_keys_average_the_allowed_values():
+    seq, dh = 50, 64
+    rng = np.random.default_rng(4)
+    Q = rng.standard_normal((seq, dh), dtype=np.float32)
+    K = np.zeros((seq, dh), np.float32)
+    V = rng.standard_normal((seq, dh), dtype=np.float32)
+    for causal, shunyam, window, stride in MASKS:
+        allowed = _mask_brute(seq, causal, shunyam, window, stride)
+        want = np.stack([V[allowed[q]].astype(np.float64).mean(axis=0) for q in range(seq)])
+        got = o.flash_attention(Q, K, V, 0.125, causal, shunyam, window, stride)
+        assert o.inf_rel_err(got, want) <= 1e-6
+
+
+def test_flash_two_key_pattern():
+    """causal + shunyam with window 0 and a stride past seq leaves each query
+    the keys {0, q}: a two-term softmax in closed form."""
+    seq, dh = 30, 64
+    rng = np.random.default_rng(5)
+    Q, K, V = (rng.standard_normal((seq, dh), dtype=np.float32) for _ in range(3))
+    got = o.flash_attention(Q, K, V, 0.2, 1, 1, 0, 1000)
+    Q64, K64, V64 = (x.astype(np.float64) for x in (Q, K, V))
+    for q in range(seq):
+        if q == 0:
+            want = V64[0]
+        else:
+            s0, sq = 0.2 * Q64[q] @ K64[0], 0.2 * Q64[q] @ K64[q]
+            w0 = 1.0 / (1.0 + np.exp(sq - s0))
+            want = w0 * V64[0] + (1.0 - w0) * V64[q]
+        np.testing.assert_allclose(got[q], want, rtol=1e-5, atol=1e-6)
+
+
+def test_flash_catches_a_dropped_scale():
+    """The f64 closed form tells a planted mistake (the scale left out of the
+    restatement's scores, emulated by scaling Q instead of the scores with the
+    wrong factor) from the right answer."""
+    seq, dh = 40, 64
+    rng = np.random.default_rng(6)
+    Q, K, V = (rng.standard_normal((seq, dh), dtype=np.float32) for _ in range(3))
+    right = o.flash_attention_f64(Q, K, V, 0.125)
+    wrong = o.flash_attention(Q, K, V, 1.0)
+    assert o.inf_rel_err(wrong, right) > 1e-2
