@@ -31,6 +31,8 @@
 // the chunks in ascending order.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "vedic_flash_attn.hpp"
 #include "vedic_gemm_f16.hpp"
 
@@ -65,24 +67,28 @@ __device__ __forceinline__ void fa_issue(const float* K, const float* V, int key
 }
 
 template <int DH>
-__global__ void __launch_bounds__(256) flash_attn_kernel(FlashArgs a) {
+constexpr int fa_stage_bytes() {
+    return 2 * kFaKeys * DH * 4;  // one stage: a K block, then a V block
+}
+
+// One work item (`item` in decreasing size order) with the workgroup's three
+// LDS stages t0, t1, t2.
+template <int DH>
+__device__ __forceinline__ void fa_item(const FlashArgs& a, int item, char* t0, char* t1, char* t2) {
     constexpr int KB = kFaKeys * DH * 4;  // bytes of one K (or V) block
-    constexpr int SB = 2 * KB;            // one stage: K block, then V block
+    constexpr int SB = fa_stage_bytes<DH>();
     constexpr int NLD = SB / 1024 / 4;    // 1 KiB direct loads per wave per stage
     constexpr int CPR = DH / 4;           // 16-byte chunks per row
     constexpr int HALF = DH / 2;
     static_assert(DH == 64 || DH == 128, "head dimension 64 or 128");
-    __shared__ __attribute__((aligned(1024))) char t0[SB];
-    __shared__ __attribute__((aligned(1024))) char t1[SB];
-    __shared__ __attribute__((aligned(1024))) char t2[SB];
     char* const stg[3] = {t0, t1, t2};
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
 
     // Work item: heads interleaved, query groups from the last (largest) down.
-    const int head = blockIdx.x % a.nheads;
-    const int64_t asc = (int64_t)a.items - 1 - blockIdx.x / a.nheads;
+    const int head = item % a.nheads;
+    const int64_t asc = (int64_t)a.items - 1 - item / a.nheads;
     int lo = 0, hi = a.nqg - 1;  // largest g with prefix(g) <= asc
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
@@ -139,6 +145,8 @@ __global__ void __launch_bounds__(256) flash_attn_kernel(FlashArgs a) {
     float16_t o[DH / 32];
 #pragma unroll
     for (int d = 0; d < DH / 32; ++d) o[d] = float16_t{};
+    // Scores are kept in base 2: s log2(e), so every exponential is one v_exp_f32.
+    const float sc2 = a.scale * 1.4426950408889634f;
     float m_run = kFaMasked, l_run = 0.0f;
     const bool wave_live = q0 < a.seq;  // waves past seq only help load
 
@@ -161,18 +169,18 @@ __global__ void __launch_bounds__(256) flash_attn_kernel(FlashArgs a) {
         float mx = kFaMasked;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            float v = s[i] * a.scale;
+            float v = s[i] * sc2;
             if (need_mask) v = fa_allowed_score(a, v, key0 + 8 * (i >> 2) + 4 * h + (i & 3), query);
             s[i] = v;
             mx = fmaxf(mx, v);
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float m_new = fmaxf(m_run, mx);
-        const float alpha = expf(m_run - m_new);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
         float ls = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const float p = s[i] <= -1e29f ? 0.0f : expf(s[i] - m_new);
+            const float p = s[i] <= -1e29f ? 0.0f : __builtin_amdgcn_exp2f(s[i] - m_new);
             s[i] = p;
             ls += p;
         }
@@ -251,33 +259,66 @@ __global__ void __launch_bounds__(256) flash_attn_kernel(FlashArgs a) {
     }
 }
 
+// One work item per workgroup, or (a.queue set) a grid of resident workgroups
+// that take items from a counter until none is left: items run largest first,
+// so the tail of the key-split one-head case stays balanced.
+// DH 64: registers held to three waves per SIMD, the occupancy its 48 KB of
+// LDS allows (three workgroups per CU).
+template <int DH, bool QUEUE>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DH == 64 ? 3 : 1)))
+flash_attn_kernel(FlashArgs a) {
+    constexpr int SB = fa_stage_bytes<DH>();
+    __shared__ __attribute__((aligned(1024))) char t0[SB];
+    __shared__ __attribute__((aligned(1024))) char t1[SB];
+    __shared__ __attribute__((aligned(1024))) char t2[SB];
+    __shared__ int next;
+    if constexpr (!QUEUE) {
+        fa_item<DH>(a, blockIdx.x, t0, t1, t2);
+        return;
+    }
+    const int total = a.items * a.nheads;
+    while (true) {
+        if (threadIdx.x == 0) next = atomicAdd(a.queue, 1);
+        __syncthreads();
+        const int item = next;
+        __syncthreads();  // every wave has its item before `next` is written again
+        if (item >= total) break;
+        fa_item<DH>(a, item, t0, t1, t2);
+        __syncthreads();  // every wave is done with the stage buffers
+    }
+}
+
+__global__ void flash_queue_reset(int* queue) {
+    if (threadIdx.x == 0) *queue = 0;
+}
+
 // Combines the chunk partials of every split query group, chunks in
-// ascending order: M = max m_c, L = sum l_c e^(m_c - M), O = sum O_c e^(m_c - M) / L.
+// ascending order: M = max m_c, L = sum l_c 2^(m_c - M), O = sum O_c 2^(m_c - M) / L
+// (row maxima in base 2, as the attention kernel keeps them).
 template <int DH>
 __global__ void __launch_bounds__(256) flash_merge_kernel(FlashArgs a) {
-    const int g = blockIdx.x, head = blockIdx.y;
+    // one thread per 4 output values; grid (kFaQ DH / 1024, query groups, heads)
+    const int g = blockIdx.y, head = blockIdx.z;
     const int nch = fa_nchunks(a, g);
     if (nch == 1) return;
-    const int64_t first = fa_prefix(a, g);
+    const int idx = blockIdx.x * 256 + threadIdx.x;  // < kFaQ * DH / 4
+    const int qi = idx / (DH / 4), d4 = idx % (DH / 4);
+    const int query = g * kFaQ + qi;
+    if (query >= a.seq) return;
     constexpr int SLOT = kFaQ * DH + 2 * kFaQ;
-    const float* base = a.part + ((int64_t)head * a.items + first) * SLOT;
-    for (int idx = threadIdx.x; idx < kFaQ * DH / 4; idx += 256) {
-        const int qi = idx / (DH / 4), d4 = idx % (DH / 4);
-        const int query = g * kFaQ + qi;
-        if (query >= a.seq) continue;
-        float M = kFaMasked;
-        for (int c = 0; c < nch; ++c) M = fmaxf(M, base[c * SLOT + kFaQ * DH + qi]);
-        float L = 0.0f;
-        float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int c = 0; c < nch; ++c) {
-            const float* sl = base + (int64_t)c * SLOT;
-            const float w = expf(sl[kFaQ * DH + qi] - M);
-            L += sl[kFaQ * DH + kFaQ + qi] * w;
-            acc += *reinterpret_cast<const float4_t*>(sl + qi * DH + 4 * d4) * w;
-        }
-        const float inv = L > 1e-9f ? 1.0f / L : 0.0f;
-        *reinterpret_cast<float4_t*>(a.o[head] + (int64_t)query * DH + 4 * d4) = acc * inv;
+    const float* base = a.part + ((int64_t)head * a.items + fa_prefix(a, g)) * SLOT;
+    float M = kFaMasked;
+    for (int c = 0; c < nch; ++c) M = fmaxf(M, base[(int64_t)c * SLOT + kFaQ * DH + qi]);
+    float L = 0.0f;
+    float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = 0; c < nch; ++c) {
+        const float* sl = base + (int64_t)c * SLOT;
+        const float w = __builtin_amdgcn_exp2f(sl[kFaQ * DH + qi] - M);
+        L += sl[kFaQ * DH + kFaQ + qi] * w;
+        acc += *reinterpret_cast<const float4_t*>(sl + qi * DH + 4 * d4) * w;
     }
+    const float inv = L > 1e-9f ? 1.0f / L : 0.0f;
+    *reinterpret_cast<float4_t*>(a.o[head] + (int64_t)query * DH + 4 * d4) = acc * inv;
 }
 
 int64_t flash_items_per_head(int seq, int chunk, int causal) {
@@ -292,12 +333,22 @@ int64_t flash_items_per_head(int seq, int chunk, int causal) {
 int flash_slot_floats(int dh) { return kFaQ * dh + 2 * kFaQ; }
 
 hipError_t launch_flash_attn(const FlashArgs& a, int dh, hipStream_t s) {
-    const dim3 grid((unsigned)(a.items * a.nheads));
-    if (dh == 64) hipLaunchKernelGGL(flash_attn_kernel<64>, grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL(flash_attn_kernel<128>, grid, dim3(256), 0, s, a);
+    dim3 grid((unsigned)(a.items * a.nheads));
+    if (a.queue != nullptr) {
+        hipLaunchKernelGGL(flash_queue_reset, dim3(1), dim3(64), 0, s, a.queue);
+        grid = dim3((unsigned)std::min(a.items * a.nheads, a.queue_grid));
+    }
+    const bool q = a.queue != nullptr;
+    if (dh == 64) {
+        if (q) hipLaunchKernelGGL((flash_attn_kernel<64, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((flash_attn_kernel<64, false>), grid, dim3(256), 0, s, a);
+    } else {
+        if (q) hipLaunchKernelGGL((flash_attn_kernel<128, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((flash_attn_kernel<128, false>), grid, dim3(256), 0, s, a);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.part == nullptr) return e;
-    const dim3 mgrid((unsigned)a.nqg, (unsigned)a.nheads);
+    const dim3 mgrid((unsigned)(kFaQ * dh / 4 / 256), (unsigned)a.nqg, (unsigned)a.nheads);
     if (dh == 64) hipLaunchKernelGGL(flash_merge_kernel<64>, mgrid, dim3(256), 0, s, a);
     else hipLaunchKernelGGL(flash_merge_kernel<128>, mgrid, dim3(256), 0, s, a);
     return hipGetLastError();

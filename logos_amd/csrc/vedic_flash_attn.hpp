@@ -20,6 +20,8 @@ struct FlashArgs {
     const float* v[kMaxHeads];
     float* o[kMaxHeads];
     float* part;  // chunk partials: [heads][items][kFaQ * DH + 2 * kFaQ]; null when unsplit
+    int* queue;   // work-item counter (persistent grid of queue_grid workgroups); null: one item per workgroup
+    int queue_grid;
     int nheads, seq, nqg;
     int chunk;  // keys per work item, a multiple of kFaQ
     int items;  // work items per head
