@@ -176,11 +176,17 @@ static int choose_ksplit(int M, int N, int K, int cus, bool f16) {
         if (big >= cus) return 1;  // the 256 x 256 kernel fills the GPU
     }
     const int min_slice = f16 ? 1024 : 128;
-    // fp32 products with N <= 64 run on 256 x 64 tiles
-    const int64_t tiles = (!f16 && N <= 64) ? (int64_t)((M + 255) / 256)
-                                            : (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+    // fp32 products run on 256 x 64 tiles when N <= 64 and on 64 x 64 tiles
+    // when 128 x 128 ones would cover at most half the CUs (f32_small_tiles)
+    const int64_t tiles = (!f16 && N <= 64)                ? (int64_t)((M + 255) / 256)
+                          : (!f16 && f32_small_tiles(M, N, cus)) ? (int64_t)((M + 63) / 64) * ((N + 63) / 64)
+                                                                  : (int64_t)((M + 127) / 128) * ((N + 127) / 128);
     if (tiles * 2 > cus || K < 2 * min_slice) return 1;
-    int s = (int)(cus / tiles);
+#ifndef VEDIC_F32_SMALL_SLOTS
+#define VEDIC_F32_SMALL_SLOTS 1
+#endif
+    const int64_t slots = (!f16 && N > 64 && f32_small_tiles(M, N, cus)) ? (int64_t)VEDIC_F32_SMALL_SLOTS * cus : cus;
+    int s = (int)(slots / tiles);
     s = s < 8 ? s : 8;
     s = s < K / min_slice ? s : K / min_slice;
     return s >= 2 ? s : 1;

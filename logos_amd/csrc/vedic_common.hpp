@@ -74,6 +74,13 @@ enum : int {
 
 constexpr int kMaxHeads = 64;  // scatter targets per GEMM
 
+// Tile choice of the fp32 GEMM, shared by the kernel launch and the split-K
+// planner: 64 x 64 tiles when N > 64 (narrower outputs take 256 x 64 tiles)
+// and 128 x 128 tiles would cover at most half the CUs.
+inline bool f32_small_tiles(int M, int N, int cus) {
+    return N > 64 && (int64_t)((M + 127) / 128) * ((N + 127) / 128) * 2 <= cus;
+}
+
 struct GemmArgs {
     const void* A;
     const void* B;

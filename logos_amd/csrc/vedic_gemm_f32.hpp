@@ -312,10 +312,23 @@ static hipError_t launch_f32_kind(const GemmArgs& a, hipStream_t s) {
     }
 }
 
-// Narrow tiles when N fits one 64-wide tile column.
+// Few output tiles (128 x 128 tiles for at most half the CUs, e.g. the
+// 512 x 1024 output of BASELINE config 1): 64 x 64 tiles, four waves of
+// 32 x 32, four 16 KiB stages, two workgroups per CU -- four times the
+// workgroups, and deeper contraction slices once the product is split.
+struct CfgF32Small {
+    static constexpr int BM = 64, BN = 64, ST = 4, WGM = 2, WGN = 2;
+    static constexpr int PER_CU = 2;
+};
+
+static_assert(CfgF32Narrow::BN == 64, "f32_small_tiles assumes the narrow tile's 64 columns");
+
+// Narrow tiles when N fits one 64-wide tile column; small ones when 128 x 128
+// tiles would leave most CUs idle.
 template <int OP>
 hipError_t launch_gemm_f32_direct_op(const GemmArgs& a, hipStream_t s) {
     if (a.N <= CfgF32Narrow::BN) return launch_f32_kind<OP, CfgF32Narrow>(a, s);
+    if (f32_small_tiles(a.M, a.N, device_cu_count())) return launch_f32_kind<OP, CfgF32Small>(a, s);
     return launch_f32_kind<OP, CfgF32>(a, s);
 }
 

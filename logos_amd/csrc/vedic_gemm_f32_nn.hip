@@ -9,7 +9,9 @@ namespace vedic {
     template __global__ void gemm_f32_kernel<0, CfgF32::BM, CfgF32::BN, CfgF32::ST, CfgF32::WGM, CfgF32::WGN, KIND>(  \
         GemmArgs);                                                                                                \
     template __global__ void gemm_f32_kernel<0, CfgF32Narrow::BM, CfgF32Narrow::BN, CfgF32Narrow::ST,              \
-                                             CfgF32Narrow::WGM, CfgF32Narrow::WGN, KIND>(GemmArgs);
+                                             CfgF32Narrow::WGM, CfgF32Narrow::WGN, KIND>(GemmArgs);                 \
+    template __global__ void gemm_f32_kernel<0, CfgF32Small::BM, CfgF32Small::BN, CfgF32Small::ST,                 \
+                                             CfgF32Small::WGM, CfgF32Small::WGN, KIND>(GemmArgs);
 VEDIC_F32_INST(EK_PLAIN)
 VEDIC_F32_INST(EK_BIAS)
 VEDIC_F32_INST(EK_BIAS_GELU)
