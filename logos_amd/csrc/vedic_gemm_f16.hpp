@@ -375,14 +375,62 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
 #ifndef VEDIC_F16_LARGE_ST
 #define VEDIC_F16_LARGE_ST 2
 #endif
+#ifndef VEDIC_F16_SMALL_PER_CU
+#define VEDIC_F16_SMALL_PER_CU 1
+#endif
+#ifndef VEDIC_F16_MID_EFF
+#define VEDIC_F16_MID_EFF 90
+#endif
+#ifndef VEDIC_F16_SMALL_EFF
+#define VEDIC_F16_SMALL_EFF 75
+#endif
 struct CfgLarge {  // 256 x 256, eight waves of 128 x 64
     static constexpr int BM = 256, BN = 256, BK = VEDIC_F16_LARGE_BK, ST = VEDIC_F16_LARGE_ST, WGM = 2, WGN = 4;
+    static constexpr int PER_CU = 1;
 };
-struct CfgSmall {  // 128 x 128, four waves of 64 x 64
-    static constexpr int BM = 128, BN = 128, BK = 64, ST = 2, WGM = 2, WGN = 2;
+#ifndef VEDIC_F16_SMALL_WGN
+#define VEDIC_F16_SMALL_WGN 2
+#endif
+#ifndef VEDIC_F16_SMALL_ST
+#define VEDIC_F16_SMALL_ST 3
+#endif
+struct CfgSmall {  // 128 x 128, four waves of 64 x 64, two workgroups per CU (2 x 64 KiB of LDS)
+    static constexpr int BM = 128, BN = 128, BK = 64, ST = VEDIC_F16_SMALL_ST, WGM = 2, WGN = VEDIC_F16_SMALL_WGN;
+    static constexpr int PER_CU = VEDIC_F16_SMALL_PER_CU;
+};
+#ifndef VEDIC_F16_MID_ST
+#define VEDIC_F16_MID_ST 3
+#endif
+struct CfgMid {  // 256 x 128, eight waves of 64 x 64
+    static constexpr int BM = 256, BN = 128, BK = 64, ST = VEDIC_F16_MID_ST, WGM = 4, WGN = 2;
+    static constexpr int PER_CU = 1;
 };
 
 int device_cu_count();
+
+// Tile configuration for an M x N product on `cus` CUs: the one with the
+// least estimated time, rounds of resident tiles x the work one CU does per
+// round / the configuration's relative efficiency (in percent, measured).
+// 0: 256 x 256, 1: 256 x 128, 2: 128 x 128.
+inline int f16_tile_config(int M, int N, int cus) {
+    struct C { int bm, bn, per_cu, eff; };
+    const C cfgs[3] = {{256, 256, 1, 100}, {256, 128, 1, VEDIC_F16_MID_EFF}, {128, 128, VEDIC_F16_SMALL_PER_CU, VEDIC_F16_SMALL_EFF}};
+    int best = 0;
+    double best_t = 0.0;
+    for (int i = 0; i < 3; ++i) {
+        const int64_t tiles = (int64_t)((M + cfgs[i].bm - 1) / cfgs[i].bm) * ((N + cfgs[i].bn - 1) / cfgs[i].bn);
+        const int64_t slots = (int64_t)cus * cfgs[i].per_cu;
+        const int64_t rounds = (tiles + slots - 1) / slots;
+        // a round's per-CU work: min(per_cu, tiles resident per CU) tiles
+        const int64_t per_cu = tiles < slots ? (tiles + cus - 1) / cus : cfgs[i].per_cu;
+        const double t_est = (double)rounds * per_cu * cfgs[i].bm * cfgs[i].bn * 100.0 / cfgs[i].eff;
+        if (i == 0 || t_est < best_t) {
+            best = i;
+            best_t = t_est;
+        }
+    }
+    return best;
+}
 
 template <int OP, class Cfg, int KIND>
 static hipError_t launch_f16(GemmArgs a, hipStream_t s) {
@@ -394,8 +442,8 @@ static hipError_t launch_f16(GemmArgs a, hipStream_t s) {
         a.kslice = a.K;
     }
     const int nwork = a.tiles_m * a.tiles_n * a.ksplit;
-    const int cus = device_cu_count();
-    const int grid = nwork < cus ? nwork : cus;
+    const int slots = device_cu_count() * Cfg::PER_CU;
+    const int grid = nwork < slots ? nwork : slots;
     hipLaunchKernelGGL((gemm_f16_kernel<OP, Cfg::BM, Cfg::BN, Cfg::BK, Cfg::ST, Cfg::WGM, Cfg::WGN, KIND>),
                        dim3(grid), dim3(Cfg::WGM * Cfg::WGN * 64), 0, s, a);
     return hipGetLastError();
@@ -419,9 +467,11 @@ static hipError_t launch_f16_kind(const GemmArgs& a, hipStream_t s) {
 // contiguous extent of each operand a multiple of 8 (checked by the caller).
 template <int OP>
 hipError_t launch_gemm_f16_direct_op(const GemmArgs& a, hipStream_t s) {
-    const int64_t big = (int64_t)((a.M + 255) / 256) * ((a.N + 255) / 256);
-    if (big >= device_cu_count()) return launch_f16_kind<OP, CfgLarge>(a, s);
-    return launch_f16_kind<OP, CfgSmall>(a, s);
+    switch (a.ksplit > 1 ? 2 : f16_tile_config(a.M, a.N, device_cu_count())) {
+        case 0: return launch_f16_kind<OP, CfgLarge>(a, s);
+        case 1: return launch_f16_kind<OP, CfgMid>(a, s);
+        default: return launch_f16_kind<OP, CfgSmall>(a, s);
+    }
 }
 
 }  // namespace vedic
