@@ -91,14 +91,18 @@ WORKLOADS = {
 # Fused attention forward (cuda_flash_attention_fwd, cuda/VedicGEMM.cu:1065-1104) at the
 # reference's call: seq 8192, DH 64, 16 heads, causal, scale 1/sqrt(DH), fp32.  "per_head"
 # makes the reference's 16 one-head calls (cuda/ModelGPU.cu:959); "16heads" one launch.
-def _fa(seq=8192, dh=64, heads=16, batched=True, causal=1, shunyam=0, window=0, stride=1):
+# The backward workloads time the fused backward (dQ, dK, dV from Q, K, V, O, dO and
+# the forward's lse; the reference's cuda/train_gpu.cu:672-740) with the forward done once
+# outside the timed region.
+def _fa(seq=8192, dh=64, heads=16, batched=True, causal=1, shunyam=0, window=0, stride=1, bwd=False):
     return dict(seq=seq, dh=dh, heads=heads, batched=batched, causal=causal, shunyam=shunyam, window=window,
-                stride=stride, dtype="fp32")
+                stride=stride, dtype="fp32", bwd=bwd)
 
 
 WORKLOADS.update({
     "flash_attn_fwd_fp32_16heads": dict(cfg=5, attn=_fa()),
     "flash_attn_fwd_fp32_per_head": dict(cfg=5, attn=_fa(batched=False)),
+    "flash_attn_bwd_fp32_16heads": dict(cfg=5, attn=_fa(bwd=True)),
 })
 COPY_WORKLOAD = "copy_256mib"  # calibration for the FETCH_SIZE / WRITE_SIZE counters
 
@@ -202,6 +206,23 @@ def cpu_baseline_attn(w: dict, seconds: float, seed: int = 7):
     a = w["attn"]
     seq, dh = a["seq"], a["dh"]
     rng = np.random.default_rng(seed)
+    if a["bwd"]:
+        # the reference's backward keeps two seq x seq matrices: time it on one head at seq 2048
+        s2 = 2048
+        Q, K, V, dO = (rng.standard_normal((s2, dh), dtype=np.float32) for _ in range(4))
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            o.attention_backward_reference(Q, K, V, dO, 1.0 / np.sqrt(dh))
+            reps += 1
+            if time.perf_counter() - t0 >= seconds:
+                break
+        dt = time.perf_counter() - t0
+        flops = reps * 10.0 * dh * s2 * (s2 + 1) / 2
+        return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+                "sample": f"one head at seq {s2} x{reps} ({flops / 1e9:.1f} GFLOP counted as 10 DH per causal "
+                          f"pair in {dt:.1f} s), single thread, -O3 -march=x86-64",
+                "threads_available": os.cpu_count()}
     Q, K, V = (rng.standard_normal((seq, dh), dtype=np.float32) for _ in range(3))
     rows = max(1, min(seq, int(2.0e9 * seconds / (4.0 * dh * seq))))  # ~2 GFLOP/s single thread
     q0 = seq - rows
@@ -410,10 +431,29 @@ def make_attn_step(w: dict, dev, torch):
     pq, pk, pv, po = arr(qs), arr(ks), arr(vs), arr(outs)
     scale = 1.0 / float(dh) ** 0.5
     flags = (a["causal"], a["shunyam"], a["window"], a["stride"])
+    if a["bwd"]:
+        lses = [torch.empty((seq,), device=dev) for _ in range(H)]
+        douts = [torch.randn((seq, dh), generator=gen, device=dev) for _ in range(H)]
+        grads = [[torch.empty((seq, dh), device=dev) for _ in range(H)] for _ in range(3)]
+        pl, pdo = arr(lses), arr(douts)
+        pg = [arr(g) for g in grads]
+        rc = lib.vedic_flash_attention_fwd_heads(pq, pk, pv, po, pl, H, seq, dh, scale, *flags, stream)
+        if rc:
+            raise RuntimeError(f"flash attention failed: {_lib.status_string(rc)}")
+
+        def bstep():
+            rc = lib.vedic_flash_attention_bwd_heads(pq, pk, pv, po, pdo, pl, pg[0], pg[1], pg[2], H, seq, dh, scale,
+                                                     *flags, stream)
+            if rc:
+                raise RuntimeError(f"flash attention backward failed: {_lib.status_string(rc)}")
+
+        bstep.keep = (qs, ks, vs, outs, lses, douts, grads, pq, pk, pv, po, pl, pdo, pg)
+        flops = 10.0 * dh * attn_pairs(a) * H  # S, dP, dV, dQ, dK once each
+        return bstep, flops, 9 * seq * dh * 4 * H, 2
 
     def step():
         if a["batched"]:
-            rc = lib.vedic_flash_attention_fwd_heads(pq, pk, pv, po, H, seq, dh, scale, *flags, stream)
+            rc = lib.vedic_flash_attention_fwd_heads(pq, pk, pv, po, None, H, seq, dh, scale, *flags, stream)
             if rc:
                 raise RuntimeError(f"flash attention failed: {_lib.status_string(rc)}")
             return
@@ -442,7 +482,7 @@ def run_attn_workload(name, args, torch, dev, with_cpu):
             "kernel_avg_us": round(ms * 1e3 / launches, 3)}
     cpu = cpu_baseline_attn(w, args.cpu_seconds) if with_cpu else None
     return {
-        "metric": f"attention forward TFLOP/s, {name}, 1 GPU",
+        "metric": f"attention {'backward' if a['bwd'] else 'forward'} TFLOP/s, {name}, 1 GPU",
         "value": round(tflops, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -456,7 +496,8 @@ def run_attn_workload(name, args, torch, dev, with_cpu):
         "data": "synthetic (seeded torch.randn Q, K, V ~ N(0,1))",
         "config": {"workload": name, "baseline_config": w["cfg"], "seq": a["seq"], "dh": a["dh"],
                    "heads": a["heads"], "launches": launches, "causal": a["causal"], "shunyam": a["shunyam"],
-                   "scale": "1/sqrt(dh)", "flops": "4 dh per allowed (query, key) pair"},
+                   "scale": "1/sqrt(dh)",
+                   "flops": f"{10 if a['bwd'] else 4} dh per allowed (query, key) pair"},
         "pct_of_peak": round(100.0 * tflops / PEAK["fp32"], 2),
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -341,14 +341,44 @@ inline void cuda_flash_attention_fwd(const float* Q, const float* K, const float
                      "cuda_flash_attention_fwd");
 }
 
+// With the per-row log-sum-exp the backward needs (new).
+inline void cuda_flash_attention_fwd_lse(const float* Q, const float* K, const float* V, float* out, float* lse,
+                                         int seq, int DH, float scale, bool causal, bool shunyam, int window,
+                                         int stride, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_flash_attention_fwd_lse(Q, K, V, out, lse, seq, DH, scale, causal ? 1 : 0,
+                                                   shunyam ? 1 : 0, window, stride, stream),
+                     "cuda_flash_attention_fwd_lse");
+}
+
 // All heads of a layer in one launch (new: the reference calls the one-head
-// kernel per head, cuda/ModelGPU.cu:888-968).
+// kernel per head, cuda/ModelGPU.cu:888-968); lse may be nullptr.
 inline void cuda_flash_attention_fwd_heads(const float* const* Q, const float* const* K, const float* const* V,
-                                           float* const* out, int nheads, int seq, int DH, float scale, bool causal,
-                                           bool shunyam, int window, int stride, hipStream_t stream = nullptr) {
-    vedic_hip::check(vedic_flash_attention_fwd_heads(Q, K, V, out, nheads, seq, DH, scale, causal ? 1 : 0,
+                                           float* const* out, float* const* lse, int nheads, int seq, int DH,
+                                           float scale, bool causal, bool shunyam, int window, int stride,
+                                           hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_flash_attention_fwd_heads(Q, K, V, out, lse, nheads, seq, DH, scale, causal ? 1 : 0,
                                                      shunyam ? 1 : 0, window, stride, stream),
                      "cuda_flash_attention_fwd_heads");
+}
+
+// Fused backward of one head (new; replaces cuda/train_gpu.cu:672-740):
+// dQ, dK, dV from Q, K, V, O, dO and the forward's lse.
+inline void cuda_flash_attention_bwd(const float* Q, const float* K, const float* V, const float* O, const float* dO,
+                                     const float* lse, float* dQ, float* dK, float* dV, int seq, int DH, float scale,
+                                     bool causal, bool shunyam, int window, int stride, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_flash_attention_bwd(Q, K, V, O, dO, lse, dQ, dK, dV, seq, DH, scale, causal ? 1 : 0,
+                                               shunyam ? 1 : 0, window, stride, stream),
+                     "cuda_flash_attention_bwd");
+}
+
+inline void cuda_flash_attention_bwd_heads(const float* const* Q, const float* const* K, const float* const* V,
+                                           const float* const* O, const float* const* dO, const float* const* lse,
+                                           float* const* dQ, float* const* dK, float* const* dV, int nheads, int seq,
+                                           int DH, float scale, bool causal, bool shunyam, int window, int stride,
+                                           hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_flash_attention_bwd_heads(Q, K, V, O, dO, lse, dQ, dK, dV, nheads, seq, DH, scale,
+                                                     causal ? 1 : 0, shunyam ? 1 : 0, window, stride, stream),
+                     "cuda_flash_attention_bwd_heads");
 }
 
 // --------------------------------------------------- elementwise helpers

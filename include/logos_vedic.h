@@ -268,12 +268,46 @@ int vedic_gemm_checked(const vedic_gemm_desc_t* desc, float tolerance, vedic_ver
 int vedic_flash_attention_fwd(const float* Q, const float* K, const float* V, float* out, float* attn, int seq,
                               int dh, float scale, int causal, int shunyam, int window, int stride, void* stream);
 
+/* vedic_flash_attention_fwd that also writes lse[seq]: for each query row,
+ * ln of its softmax denominator, ln(sum over allowed keys of e^(scale q.k))
+ * (+inf for a row with no allowed key) -- what the backward below needs.
+ * New: the reference keeps no such statistic and recomputes the whole
+ * probability matrix for its backward (cuda/train_gpu.cu:672-700). */
+int vedic_flash_attention_fwd_lse(const float* Q, const float* K, const float* V, float* out, float* lse, int seq,
+                                  int dh, float scale, int causal, int shunyam, int window, int stride,
+                                  void* stream);
+
 /* The same for nheads (1..64) heads in one launch: Q[h], K[h], V[h], out[h]
- * per head, every head [seq x dh].  New: the reference calls the one-head
+ * per head, every head [seq x dh]; lse may be NULL, or an array of per-head
+ * lse outputs (entries may be NULL).  New: the reference calls the one-head
  * kernel once per head (cuda/ModelGPU.cu:888-968). */
 int vedic_flash_attention_fwd_heads(const float* const* Q, const float* const* K, const float* const* V,
-                                    float* const* out, int nheads, int seq, int dh, float scale, int causal,
-                                    int shunyam, int window, int stride, void* stream);
+                                    float* const* out, float* const* lse, int nheads, int seq, int dh, float scale,
+                                    int causal, int shunyam, int window, int stride, void* stream);
+
+/* Fused attention backward of one head, fp32: from Q, K, V, the forward's
+ * output O and lse (vedic_flash_attention_fwd_lse, same mask arguments) and
+ * the output gradient dO, writes
+ *   dV = P^T dO,  dQ = scale dS K,  dK = scale dS^T Q,
+ *   P = exp(scale Q K^T + mask - lse),  dS = P * (dO V^T - rowsum(dO * O)).
+ * Replaces the per-head backward of cuda/train_gpu.cu:672-740 (score
+ * recompute, causal mask, softmax, attn_dV_kernel, attn_dAttnProbs_kernel,
+ * softmax_bwd_kernel, attn_dQ_kernel, attn_dK_kernel: :422-479) without its
+ * two seq x seq buffers.  That code recomputes the probabilities with the
+ * causal mask only; with shunyam set this function differentiates the
+ * forward as computed (sparse mask included).  dQ, dK, dV are overwritten.
+ * Limits as for the forward; takes a stream-ordered workspace of 8 * seq
+ * bytes (hipMallocAsync on `stream`). */
+int vedic_flash_attention_bwd(const float* Q, const float* K, const float* V, const float* O, const float* dO,
+                              const float* lse, float* dQ, float* dK, float* dV, int seq, int dh, float scale,
+                              int causal, int shunyam, int window, int stride, void* stream);
+
+/* The same for nheads (1..32) heads in one launch (per-head pointer arrays). */
+int vedic_flash_attention_bwd_heads(const float* const* Q, const float* const* K, const float* const* V,
+                                    const float* const* O, const float* const* dO, const float* const* lse,
+                                    float* const* dQ, float* const* dK, float* const* dV, int nheads, int seq,
+                                    int dh, float scale, int causal, int shunyam, int window, int stride,
+                                    void* stream);
 
 /* ---- backend queries --------------------------------------------------- */
 

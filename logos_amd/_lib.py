@@ -102,11 +102,16 @@ SIGNATURES = {
     "vedic_gemm_checked": (c_int, [ctypes.POINTER(GemmDesc), c_float, ctypes.POINTER(VerifyResult)]),
     "vedic_flash_attention_fwd": (
         c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_vp]),
+    "vedic_flash_attention_fwd_lse": (
+        c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_vp]),
     "vedic_flash_attention_fwd_heads": (
         c_int,
-        [ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), c_int, c_int,
-         c_int, c_float, c_int, c_int, c_int, c_int, c_vp],
+        [ctypes.POINTER(c_vp)] * 5 + [c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_vp],
     ),
+    "vedic_flash_attention_bwd": (
+        c_int, [c_vp] * 9 + [c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_vp]),
+    "vedic_flash_attention_bwd_heads": (
+        c_int, [ctypes.POINTER(c_vp)] * 9 + [c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_vp]),
     "vedic_uses_vendor_blas": (c_int, []),
     "vedic_backend_name": (c_char_p, []),
     "vedic_status_string": (c_char_p, [c_int]),

@@ -31,6 +31,7 @@ SOURCES = [
     "vedic_gemm_mfma.hip",
     "vedic_gemm_skinny.hip",
     "vedic_flash_attn.hip",
+    "vedic_flash_attn_bwd.hip",
     "vedic_capi.hip",
 ]
 

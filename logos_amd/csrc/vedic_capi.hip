@@ -898,15 +898,22 @@ extern "C" int vedic_gemm_checked(const vedic_gemm_desc_t* d, float tolerance, v
 #define VEDIC_FA_ITEMS_PER_4CU 11
 #endif
 
-static int flash_impl(const float* const* Q, const float* const* K, const float* const* V, float* const* out,
-                      int nheads, int seq, int dh, float scale, int causal, int shunyam, int window, int stride,
-                      void* stream) {
+// Shape checks shared by the attention entry points.
+static int flash_check(int nheads, int max_heads, int seq, int dh, int shunyam, int window, int stride) {
     if (nheads < 1 || seq < 1 || dh < 1 || dh > 128) return VEDIC_STATUS_BAD_DIM;
-    if (nheads > kMaxHeads) return VEDIC_STATUS_TOO_LARGE;
+    if (nheads > max_heads) return VEDIC_STATUS_TOO_LARGE;
     if (dh != 64 && dh != 128) return VEDIC_STATUS_UNSUPPORTED;
     if ((int64_t)seq * dh >= (int64_t(1) << 29)) return VEDIC_STATUS_TOO_LARGE;
+    if (shunyam && seq > window && stride < 1) return VEDIC_STATUS_BAD_DIM;
+    return VEDIC_STATUS_OK;
+}
+
+static int flash_impl(const float* const* Q, const float* const* K, const float* const* V, float* const* out,
+                      float* const* lse, int nheads, int seq, int dh, float scale, int causal, int shunyam,
+                      int window, int stride, void* stream) {
+    const int chk = flash_check(nheads, kMaxHeads, seq, dh, shunyam, window, stride);
+    if (chk != VEDIC_STATUS_OK) return chk;
     const bool sparse = shunyam && seq > window;
-    if (sparse && stride < 1) return VEDIC_STATUS_BAD_DIM;
     if (!Q || !K || !V || !out) return VEDIC_STATUS_NULL_POINTER;
     FlashArgs a{};
     for (int h = 0; h < nheads; ++h) {
@@ -917,6 +924,7 @@ static int flash_impl(const float* const* Q, const float* const* K, const float*
         a.k[h] = K[h];
         a.v[h] = V[h];
         a.o[h] = out[h];
+        a.lse[h] = lse ? lse[h] : nullptr;
     }
     a.nheads = nheads;
     a.seq = seq;
@@ -967,13 +975,78 @@ extern "C" int vedic_flash_attention_fwd(const float* Q, const float* K, const f
                                          int seq, int dh, float scale, int causal, int shunyam, int window,
                                          int stride, void* stream) {
     if (attn != nullptr) return VEDIC_STATUS_UNSUPPORTED;
-    return flash_impl(&Q, &K, &V, &out, 1, seq, dh, scale, causal, shunyam, window, stride, stream);
+    return flash_impl(&Q, &K, &V, &out, nullptr, 1, seq, dh, scale, causal, shunyam, window, stride, stream);
+}
+
+extern "C" int vedic_flash_attention_fwd_lse(const float* Q, const float* K, const float* V, float* out, float* lse,
+                                             int seq, int dh, float scale, int causal, int shunyam, int window,
+                                             int stride, void* stream) {
+    if (lse == nullptr) return VEDIC_STATUS_NULL_POINTER;
+    return flash_impl(&Q, &K, &V, &out, &lse, 1, seq, dh, scale, causal, shunyam, window, stride, stream);
 }
 
 extern "C" int vedic_flash_attention_fwd_heads(const float* const* Q, const float* const* K, const float* const* V,
-                                               float* const* out, int nheads, int seq, int dh, float scale,
-                                               int causal, int shunyam, int window, int stride, void* stream) {
-    return flash_impl(Q, K, V, out, nheads, seq, dh, scale, causal, shunyam, window, stride, stream);
+                                               float* const* out, float* const* lse, int nheads, int seq, int dh,
+                                               float scale, int causal, int shunyam, int window, int stride,
+                                               void* stream) {
+    return flash_impl(Q, K, V, out, lse, nheads, seq, dh, scale, causal, shunyam, window, stride, stream);
+}
+
+static int flash_bwd_impl(const float* const* Q, const float* const* K, const float* const* V,
+                          const float* const* O, const float* const* dO, const float* const* lse, float* const* dQ,
+                          float* const* dK, float* const* dV, int nheads, int seq, int dh, float scale, int causal,
+                          int shunyam, int window, int stride, void* stream) {
+    const int chk = flash_check(nheads, kFaBwdHeads, seq, dh, shunyam, window, stride);
+    if (chk != VEDIC_STATUS_OK) return chk;
+    if (!Q || !K || !V || !O || !dO || !lse || !dQ || !dK || !dV) return VEDIC_STATUS_NULL_POINTER;
+    FlashBwdArgs a{};
+    for (int h = 0; h < nheads; ++h) {
+        const void* ps[9] = {Q[h], K[h], V[h], O[h], dO[h], lse[h], dQ[h], dK[h], dV[h]};
+        for (const void* p : ps) {
+            if (!p) return VEDIC_STATUS_NULL_POINTER;
+            if (p != lse[h] && !aligned16(p)) return VEDIC_STATUS_UNSUPPORTED;
+        }
+        a.q[h] = Q[h];
+        a.k[h] = K[h];
+        a.v[h] = V[h];
+        a.o[h] = O[h];
+        a.dout[h] = dO[h];
+        a.lse[h] = lse[h];
+        a.dq[h] = dQ[h];
+        a.dk[h] = dK[h];
+        a.dv[h] = dV[h];
+    }
+    a.nheads = nheads;
+    a.seq = seq;
+    a.nqg = (seq + kFaQ - 1) / kFaQ;
+    a.causal = causal ? 1 : 0;
+    a.sparse = (shunyam && seq > window) ? 1 : 0;
+    a.window = window;
+    a.stride = a.sparse ? stride : 1;
+    a.scale = scale;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&a.delta), sizeof(float) * 2 * (size_t)seq * nheads, s);
+    if (e != hipSuccess) return hip_status(e);
+    e = launch_flash_attn_bwd(a, dh, s);
+    const hipError_t f = hipFreeAsync(a.delta, s);
+    return hip_status(e != hipSuccess ? e : f);
+}
+
+extern "C" int vedic_flash_attention_bwd(const float* Q, const float* K, const float* V, const float* O,
+                                         const float* dO, const float* lse, float* dQ, float* dK, float* dV, int seq,
+                                         int dh, float scale, int causal, int shunyam, int window, int stride,
+                                         void* stream) {
+    return flash_bwd_impl(&Q, &K, &V, &O, &dO, &lse, &dQ, &dK, &dV, 1, seq, dh, scale, causal, shunyam, window,
+                          stride, stream);
+}
+
+extern "C" int vedic_flash_attention_bwd_heads(const float* const* Q, const float* const* K, const float* const* V,
+                                               const float* const* O, const float* const* dO,
+                                               const float* const* lse, float* const* dQ, float* const* dK,
+                                               float* const* dV, int nheads, int seq, int dh, float scale, int causal,
+                                               int shunyam, int window, int stride, void* stream) {
+    return flash_bwd_impl(Q, K, V, O, dO, lse, dQ, dK, dV, nheads, seq, dh, scale, causal, shunyam, window, stride,
+                          stream);
 }
 
 extern "C" int vedic_uses_vendor_blas(void) { return 0; }

@@ -33,38 +33,9 @@
 
 #include <algorithm>
 
-#include "vedic_flash_attn.hpp"
-#include "vedic_gemm_f16.hpp"
+#include "vedic_flash_device.hpp"
 
 namespace vedic {
-
-__device__ __forceinline__ float fa_allowed_score(const FlashArgs& a, float s, int key, int query) {
-    bool ok = key < a.seq;
-    if (a.causal && key > query) ok = false;
-    if (a.sparse) {
-        const bool in_window = key >= query - a.window && key <= query;
-        const bool global = key % a.stride == 0;
-        if (!in_window && !global) ok = false;
-    }
-    return ok ? s : kFaMasked;
-}
-
-// Direct loads of one K block and one V block (keys key0 .. key0 + 31) into
-// stage `dst`: instruction i of this wave fills bytes [1 KiB (wave NLD + i),
-// +1 KiB), lane L its 16-byte chunk L.  Rows at or past `rows` (0 for a
-// stage past the work item) load zeros without touching memory.
-template <int DH, int NLD>
-__device__ __forceinline__ void fa_issue(const float* K, const float* V, int key0, int rows, char* dst, int wave,
-                                         const uint32_t (&loff)[NLD], const int (&lrow)[NLD],
-                                         const bool (&lisv)[NLD]) {
-    const int64_t base = rows > 0 ? (int64_t)key0 * DH : 0;
-    const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(K + base);
-    const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(V + base);
-#pragma unroll
-    for (int i = 0; i < NLD; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(lisv[i] ? rv : rk, (lds_void_t*)(dst + (wave * NLD + i) * 1024), 16,
-                                                 lrow[i] < rows ? loff[i] : kOob, 0, 0, 0);
-}
 
 template <int DH>
 constexpr int fa_stage_bytes() {
@@ -228,6 +199,7 @@ __device__ __forceinline__ void fa_item(const FlashArgs& a, int item, char* t0, 
     // o[d][4 gg + r] is O[query][32 d + 8 gg + 4 h + r].
     if (nch == 1) {
         if (query >= a.seq) return;
+        if (a.lse[head] != nullptr && h == 0) a.lse[head][query] = fa_lse(m_run, l_tot);
         const float inv = l_tot > 1e-9f ? 1.0f / l_tot : 0.0f;
         float* orow = a.o[head] + (int64_t)query * DH;
 #pragma unroll
@@ -319,6 +291,7 @@ __global__ void __launch_bounds__(256) flash_merge_kernel(FlashArgs a) {
     }
     const float inv = L > 1e-9f ? 1.0f / L : 0.0f;
     *reinterpret_cast<float4_t*>(a.o[head] + (int64_t)query * DH + 4 * d4) = acc * inv;
+    if (a.lse[head] != nullptr && d4 == 0) a.lse[head][query] = fa_lse(M, L);
 }
 
 int64_t flash_items_per_head(int seq, int chunk, int causal) {

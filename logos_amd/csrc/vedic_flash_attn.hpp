@@ -19,6 +19,7 @@ struct FlashArgs {
     const float* k[kMaxHeads];
     const float* v[kMaxHeads];
     float* o[kMaxHeads];
+    float* lse[kMaxHeads];  // optional per head: ln of the softmax denominator of each query row
     float* part;  // chunk partials: [heads][items][kFaQ * DH + 2 * kFaQ]; null when unsplit
     int* queue;   // work-item counter (persistent grid of queue_grid workgroups); null: one item per workgroup
     int queue_grid;
@@ -45,8 +46,36 @@ __host__ __device__ inline int64_t fa_prefix(const FlashArgs& a, int g) {
     return g + R * q * (q - 1) / 2 + q * r;
 }
 
+// Natural-log log-sum-exp of a row from its base-2 running max m2 and sum l:
+// ln(sum_k e^(scale s_k)) = (m2 + log2 l) ln 2; +inf for a row with no key,
+// so that the backward's probabilities exp(scale s - lse) are 0 there.
+__device__ __forceinline__ float fa_lse(float m2, float l) {
+    return l > 1e-9f ? (m2 + __builtin_amdgcn_logf(l)) * 0.6931471805599453f : __builtin_inff();
+}
+
 int64_t flash_items_per_head(int seq, int chunk, int causal);
 int flash_slot_floats(int dh);
 hipError_t launch_flash_attn(const FlashArgs& a, int dh, hipStream_t s);
+
+// Backward: heads per launch (nine pointer arrays in the kernel arguments).
+constexpr int kFaBwdHeads = 32;
+
+struct FlashBwdArgs {
+    const float* q[kFaBwdHeads];
+    const float* k[kFaBwdHeads];
+    const float* v[kFaBwdHeads];
+    const float* o[kFaBwdHeads];
+    const float* dout[kFaBwdHeads];
+    const float* lse[kFaBwdHeads];
+    float* dq[kFaBwdHeads];
+    float* dk[kFaBwdHeads];
+    float* dv[kFaBwdHeads];
+    float* delta;  // [heads][seq] workspace: rowsum(dO * O), written by the dQ pass
+    int nheads, seq, nqg;
+    int causal, sparse, window, stride;
+    float scale;
+};
+
+hipError_t launch_flash_attn_bwd(const FlashBwdArgs& a, int dh, hipStream_t s);
 
 }  // namespace vedic

@@ -37,7 +37,7 @@ __all__ = [
     "cast_pack_fp16", "add_bias", "gelu_",
     "cast_fp32_to_fp16",
     "cast_fp16_to_fp32", "verify", "gemm_checked", "VerifyResult", "uses_vendor_blas", "backend_name",
-    "flash_attention_fwd", "flash_attention_fwd_heads",
+    "flash_attention_fwd", "flash_attention_fwd_heads", "flash_attention_bwd", "flash_attention_bwd_heads",
 ]
 
 _DT = {torch.float32: DT_F32, torch.float16: DT_F16}
@@ -375,13 +375,16 @@ def _head(t: torch.Tensor, name: str, seq: int | None = None, dh: int | None = N
 
 def flash_attention_fwd(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, out: torch.Tensor | None = None,
                         scale: float | None = None, causal: bool = True, shunyam: bool = False, window: int = 0,
-                        stride: int = 1, attn: torch.Tensor | None = None) -> torch.Tensor:
+                        stride: int = 1, attn: torch.Tensor | None = None,
+                        lse: torch.Tensor | None = None) -> torch.Tensor:
     """out = softmax(scale Q K^T + mask) V for one head, fp32 [seq x dh] (dh 64
     or 128): cuda_flash_attention_fwd (cuda/VedicGEMM.cu:1065-1104).  scale
     defaults to 1/sqrt(dh), the caller's value (cuda/ModelGPU.cu:963).  The
     mask drops keys after the query (causal) and, with shunyam and seq >
     window, keys outside [query - window, query] that are not multiples of
-    stride.  `attn` (the reference's optional probability copy) must be None."""
+    stride.  `attn` (the reference's optional probability copy) must be None.
+    lse (optional float32 [seq] GPU tensor) receives each row's log-sum-exp
+    ln(sum over allowed keys of e^(scale q.k)), for flash_attention_bwd."""
     seq, dh = _head(Q, "Q")
     _head(K, "K", seq, dh)
     _head(V, "V", seq, dh)
@@ -390,18 +393,32 @@ def flash_attention_fwd(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, out: 
     _head(out, "out", seq, dh)
     if scale is None:
         scale = 1.0 / float(dh) ** 0.5
+    flags = (float(scale), int(causal), int(shunyam), int(window), int(stride), _stream())
+    if lse is not None:
+        if attn is not None:
+            raise ValueError("attn must be None")
+        _vec(lse, "lse", seq)
+        _check(_lib.load().vedic_flash_attention_fwd_lse(Q.data_ptr(), K.data_ptr(), V.data_ptr(), out.data_ptr(),
+                                                         lse.data_ptr(), seq, dh, *flags))
+        return out
     ap = None if attn is None else attn.data_ptr()
     _check(_lib.load().vedic_flash_attention_fwd(Q.data_ptr(), K.data_ptr(), V.data_ptr(), out.data_ptr(), ap, seq,
-                                                 dh, float(scale), int(causal), int(shunyam), int(window),
-                                                 int(stride), _stream()))
+                                                 dh, *flags))
     return out
+
+
+def _vec(t: torch.Tensor, name: str, n: int) -> None:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda or t.dtype != torch.float32 or t.numel() != n \
+            or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous float32 GPU tensor of {n} values")
 
 
 def flash_attention_fwd_heads(Qs: list[torch.Tensor], Ks: list[torch.Tensor], Vs: list[torch.Tensor],
                               outs: list[torch.Tensor] | None = None, scale: float | None = None,
                               causal: bool = True, shunyam: bool = False, window: int = 0,
-                              stride: int = 1) -> list[torch.Tensor]:
-    """flash_attention_fwd for several heads (all [seq x dh]) in one launch."""
+                              stride: int = 1, lses: list[torch.Tensor] | None = None) -> list[torch.Tensor]:
+    """flash_attention_fwd for several heads (all [seq x dh]) in one launch;
+    lses: optional per-head log-sum-exp outputs."""
     n = len(Qs)
     if n == 0 or len(Ks) != n or len(Vs) != n:
         raise ValueError("Qs, Ks and Vs must be non-empty lists of the same length")
@@ -418,8 +435,54 @@ def flash_attention_fwd_heads(Qs: list[torch.Tensor], Ks: list[torch.Tensor], Vs
         _head(outs[i], f"out[{i}]", seq, dh)
     if scale is None:
         scale = 1.0 / float(dh) ** 0.5
+    if lses is not None:
+        if len(lses) != n:
+            raise ValueError("lses must have one tensor per head")
+        for i in range(n):
+            _vec(lses[i], f"lse[{i}]", seq)
     arr = lambda ts: (ctypes.c_void_p * n)(*[t.data_ptr() for t in ts])
-    _check(_lib.load().vedic_flash_attention_fwd_heads(arr(Qs), arr(Ks), arr(Vs), arr(outs), n, seq, dh,
+    _check(_lib.load().vedic_flash_attention_fwd_heads(arr(Qs), arr(Ks), arr(Vs), arr(outs),
+                                                       None if lses is None else arr(lses), n, seq, dh,
                                                        float(scale), int(causal), int(shunyam), int(window),
                                                        int(stride), _stream()))
     return outs
+
+
+def flash_attention_bwd(Q, K, V, O, dO, lse, dQ=None, dK=None, dV=None, scale: float | None = None,
+                        causal: bool = True, shunyam: bool = False, window: int = 0, stride: int = 1):
+    """(dQ, dK, dV) of flash_attention_fwd for one head from Q, K, V, its
+    output O, the output gradient dO and the forward's lse; same mask
+    arguments as the forward.  Replaces the backward of cuda/train_gpu.cu:672-740."""
+    return tuple(t[0] for t in flash_attention_bwd_heads([Q], [K], [V], [O], [dO], [lse],
+                                                          None if dQ is None else [dQ], None if dK is None else [dK],
+                                                          None if dV is None else [dV], scale, causal, shunyam,
+                                                          window, stride))
+
+
+def flash_attention_bwd_heads(Qs, Ks, Vs, Os, dOs, lses, dQs=None, dKs=None, dVs=None, scale: float | None = None,
+                              causal: bool = True, shunyam: bool = False, window: int = 0, stride: int = 1):
+    """flash_attention_bwd for 1..32 heads in one launch; returns (dQs, dKs, dVs)."""
+    n = len(Qs)
+    if n == 0 or any(len(x) != n for x in (Ks, Vs, Os, dOs, lses)):
+        raise ValueError("Qs, Ks, Vs, Os, dOs and lses must be non-empty lists of the same length")
+    seq, dh = _head(Qs[0], "Q[0]")
+    for i in range(n):
+        for t, name in ((Qs[i], "Q"), (Ks[i], "K"), (Vs[i], "V"), (Os[i], "O"), (dOs[i], "dO")):
+            _head(t, f"{name}[{i}]", seq, dh)
+        _vec(lses[i], f"lse[{i}]", seq)
+    out = []
+    for given in (dQs, dKs, dVs):
+        ts = [torch.empty_like(q) for q in Qs] if given is None else given
+        if len(ts) != n:
+            raise ValueError("gradient lists must have one tensor per head")
+        for i in range(n):
+            _head(ts[i], f"gradient[{i}]", seq, dh)
+        out.append(ts)
+    if scale is None:
+        scale = 1.0 / float(dh) ** 0.5
+    arr = lambda ts: (ctypes.c_void_p * n)(*[t.data_ptr() for t in ts])
+    _check(_lib.load().vedic_flash_attention_bwd_heads(arr(Qs), arr(Ks), arr(Vs), arr(Os), arr(dOs), arr(lses),
+                                                       arr(out[0]), arr(out[1]), arr(out[2]), n, seq, dh,
+                                                       float(scale), int(causal), int(shunyam), int(window),
+                                                       int(stride), _stream()))
+    return tuple(out)

@@ -49,6 +49,7 @@ def _load():
             "oracle_checksum": [_fp, _fp, _fp, _i, _i, _i, _dp, _dp],
             "oracle_flash_attention": [_fp, _fp, _fp, _fp, _i, _i, ctypes.c_float, _i, _i, _i, _i],
             "oracle_flash_attention_rows": [_fp, _fp, _fp, _fp, _i, _i, ctypes.c_float, _i, _i, _i, _i, _i, _i],
+            "oracle_attention_backward": [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _i, _i, ctypes.c_float],
         }
         for name, args in sig.items():
             fn = getattr(lib, name)
@@ -356,6 +357,22 @@ def inf_rel_err(got, want64) -> float:
     return num / denom
 
 
+def grad_rel_err(got, want64) -> float:
+    """Largest inf-norm error over a tuple of gradients (dQ, dK, dV), each
+    relative to its own inf-norm or, if that is below it, to a tenth of the
+    largest gradient of the tuple (a gradient that is exactly 0 in exact
+    arithmetic, e.g. dQ and dK with a single key, has only rounding noise of
+    the size of the others' rounding to compare against)."""
+    floor = 0.1 * max(float(np.max(np.abs(np.asarray(w, dtype=np.float64)))) for w in want64)
+    err = 0.0
+    for g, w in zip(got, want64):
+        g = np.asarray(g, dtype=np.float64)
+        w = np.asarray(w, dtype=np.float64)
+        den = max(float(np.max(np.abs(w))), floor)
+        err = max(err, float(np.max(np.abs(g - w))) / den if den > 0 else float(np.max(np.abs(g))))
+    return err
+
+
 def fp32_tolerance(K: int) -> float:
     """Max relative error bound for the FP32 path: 1e-5 * sqrt(K)."""
     return 1e-5 * float(np.sqrt(K))
@@ -421,3 +438,83 @@ def flash_attention_rows(Q, K, V, scale, q_begin, q_end, causal=True, shunyam=Fa
     if rc != 0:
         raise ValueError(f"oracle_flash_attention_rows failed ({rc})")
     return out
+
+
+def flash_attention_stats_f64(Q, K, V, scale, causal=True, shunyam=False, window=0, stride=1, block=1024):
+    """float64 (O, lse) of the attention forward over all rows, in row blocks:
+    O = softmax over the allowed keys times V, lse = ln sum_allowed e^(scale q.k)
+    (+inf for a row with no allowed key)."""
+    Q = np.asarray(Q, dtype=np.float64)
+    K = np.asarray(K, dtype=np.float64)
+    V = np.asarray(V, dtype=np.float64)
+    seq = K.shape[0]
+    O = np.zeros((Q.shape[0], V.shape[1]))
+    lse = np.full(Q.shape[0], np.inf)
+    for r0 in range(0, Q.shape[0], block):
+        idx = np.arange(r0, min(Q.shape[0], r0 + block))
+        mask = attention_mask(seq, causal, shunyam, window, stride)[idx] if seq <= 4096 else \
+            _mask_rows(seq, idx, causal, shunyam, window, stride)
+        S = np.where(mask, scale * (Q[idx] @ K.T), -np.inf)
+        m = S.max(axis=1, keepdims=True)
+        ok = np.isfinite(m[:, 0])
+        m = np.where(np.isfinite(m), m, 0.0)
+        E = np.where(mask, np.exp(S - m), 0.0)
+        den = E.sum(axis=1)
+        O[idx] = np.where(den[:, None] > 0, (E @ V) / np.where(den > 0, den, 1.0)[:, None], 0.0)
+        lse[idx] = np.where(ok, m[:, 0] + np.log(np.where(den > 0, den, 1.0)), np.inf)
+    return O, lse
+
+
+def _mask_rows(seq, idx, causal, shunyam, window, stride):
+    q = np.asarray(idx)[:, None]
+    k = np.arange(seq)[None, :]
+    ok = np.ones((len(idx), seq), dtype=bool)
+    if causal:
+        ok &= k <= q
+    if shunyam and seq > window:
+        ok &= ((k >= q - window) & (k <= q)) | (k % stride == 0)
+    return ok
+
+
+def flash_attention_bwd_f64(Q, K, V, dO, scale, causal=True, shunyam=False, window=0, stride=1,
+                            q_rows=None, k_rows=None, stats=None):
+    """float64 gradients of out = softmax(scale Q K^T + mask) V against dO:
+    dV = P^T dO, dS = P * (dO V^T - rowsum(dO * O)), dQ = scale dS K,
+    dK = scale dS^T Q.  q_rows / k_rows restrict dQ / (dK, dV) to those rows
+    (None: all); stats = (O, lse) from flash_attention_stats_f64 (computed if
+    None).  Returns (dQ rows, dK rows, dV rows)."""
+    Q = np.asarray(Q, dtype=np.float64)
+    K = np.asarray(K, dtype=np.float64)
+    V = np.asarray(V, dtype=np.float64)
+    dO = np.asarray(dO, dtype=np.float64)
+    seq = K.shape[0]
+    O, lse = stats if stats is not None else flash_attention_stats_f64(Q, K, V, scale, causal, shunyam, window, stride)
+    D = (dO * O).sum(axis=1)
+    qi = np.arange(seq) if q_rows is None else np.asarray(q_rows)
+    ki = np.arange(seq) if k_rows is None else np.asarray(k_rows)
+    lse_f = np.where(np.isfinite(lse), lse, 0.0)
+    # rows of P for the dQ rows
+    mq = _mask_rows(seq, qi, causal, shunyam, window, stride) & np.isfinite(lse[qi])[:, None]
+    Pq = np.where(mq, np.exp(scale * (Q[qi] @ K.T) - lse_f[qi][:, None]), 0.0)
+    dSq = Pq * (dO[qi] @ V.T - D[qi][:, None])
+    dQ = scale * (dSq @ K)
+    # columns of P for the dK / dV rows
+    mk = _mask_rows(seq, np.arange(seq), causal, shunyam, window, stride)[:, ki] & np.isfinite(lse)[:, None]
+    Pk = np.where(mk, np.exp(scale * (Q @ K[ki].T) - lse_f[:, None]), 0.0)
+    dSk = Pk * (dO @ V[ki].T - D[:, None])
+    dV = Pk.T @ dO
+    dK = scale * (dSk.T @ Q)
+    return dQ, dK, dV
+
+
+def attention_backward_reference(Q, K, V, dO, scale):
+    """The reference's per-head backward (cuda/train_gpu.cu:672-740) restated
+    on the CPU in fp32: scores recomputed with the causal mask only."""
+    Q, K, V, dO = _f32(Q), _f32(K), _f32(V), _f32(dO)
+    seq, dh = Q.shape
+    dQ, dK, dV = (np.empty_like(Q) for _ in range(3))
+    rc = _load().oracle_attention_backward(_p(Q), _p(K), _p(V), _p(dO), _p(dQ), _p(dK), _p(dV), seq, dh,
+                                           float(scale))
+    if rc != 0:
+        raise ValueError(f"oracle_attention_backward failed ({rc})")
+    return dQ, dK, dV

@@ -59,6 +59,17 @@
  *     probability row itself, which exposes the mask and the weights), zero K
  *     (uniform weights over the allowed keys: the mean of their V rows) and
  *     a sparse pattern that leaves each query exactly the keys {0, q}.
+ *
+ *  4. oracle_attention_backward <- cuda/train_gpu.cu:672-740 (the per-head
+ *     backward: scores recomputed with vedic_gemm_kernel, cuda/VedicGEMM.cu:39-66,
+ *     scaled, causal mask of -1e9, boltzmann_softmax_kernel at temperature 1,
+ *     :108-150, then attn_dV, attn_dAttnProbs, softmax_bwd, attn_dQ, attn_dK,
+ *     cuda/train_gpu.cu:422-479).  Every dot product runs in ascending index
+ *     with fmaf, as nvcc compiles those loops; the softmax row sum is taken
+ *     sequentially (the reference reduces it in a thread tree: the same
+ *     terms in another order).  Pinned in tests/test_oracle.py against the
+ *     float64 gradient (oracle.py flash_attention_bwd_f64), itself pinned by
+ *     central finite differences of sum(dO * attention(Q, K, V)).
  */
 #include <math.h>
 #include <pthread.h>
@@ -443,4 +454,74 @@ int oracle_flash_attention_rows(const float* Q, const float* K, const float* V, 
 int oracle_flash_attention(const float* Q, const float* K, const float* V, float* out, int seq, int dh,
                            float scale, int causal, int shunyam, int window, int stride) {
     return oracle_flash_attention_rows(Q, K, V, out, seq, dh, scale, causal, shunyam, window, stride, 0, seq);
+}
+
+/* --------------------------------------------------- attention backward */
+
+/* dQ, dK, dV [seq x dh] of one head, the reference's backward restated
+ * (see the header): S = scale Q K^T + causal mask (-1e9), P = softmax(S)
+ * (row max, expf, sum + 1e-9), dV = P^T dO, dP = dO V^T,
+ * dS = P (dP - rowsum(P dP)) scale, dQ = dS K, dK = dS^T Q. */
+int oracle_attention_backward(const float* Q, const float* K, const float* V, const float* dO, float* dQ, float* dK,
+                              float* dV, int seq, int dh, float scale) {
+    if (seq <= 0 || dh <= 0) return -1;
+    float* P = (float*)malloc(sizeof(float) * (size_t)seq * seq);
+    float* dS = (float*)malloc(sizeof(float) * (size_t)seq * seq);
+    if (!P || !dS) {
+        free(P);
+        free(dS);
+        return -3;
+    }
+    for (int i = 0; i < seq; ++i) {
+        float* row = P + (int64_t)i * seq;
+        float mx = -1e38f;
+        for (int k = 0; k < seq; ++k) {
+            float acc = 0.0f;
+            for (int d = 0; d < dh; ++d) acc = fmaf(Q[(int64_t)i * dh + d], K[(int64_t)k * dh + d], acc);
+            acc *= scale;
+            if (k > i) acc += -1e9f;
+            row[k] = acc;
+            mx = fmaxf(mx, acc);
+        }
+        float sum = 0.0f;
+        for (int k = 0; k < seq; ++k) {
+            row[k] = expf((row[k] - mx) / 1.0f);
+            sum += row[k];
+        }
+        sum += 1e-9f;
+        for (int k = 0; k < seq; ++k) row[k] /= sum;
+    }
+    for (int k = 0; k < seq; ++k)
+        for (int j = 0; j < dh; ++j) {
+            float acc = 0.0f;
+            for (int i = 0; i < seq; ++i) acc = fmaf(P[(int64_t)i * seq + k], dO[(int64_t)i * dh + j], acc);
+            dV[(int64_t)k * dh + j] = acc;
+        }
+    for (int i = 0; i < seq; ++i) {
+        const float* p = P + (int64_t)i * seq;
+        float* ds = dS + (int64_t)i * seq;
+        for (int k = 0; k < seq; ++k) {
+            float acc = 0.0f;
+            for (int j = 0; j < dh; ++j) acc = fmaf(dO[(int64_t)i * dh + j], V[(int64_t)k * dh + j], acc);
+            ds[k] = acc;  /* dP for now */
+        }
+        float dot = 0.0f;
+        for (int k = 0; k < seq; ++k) dot = fmaf(p[k], ds[k], dot);
+        for (int k = 0; k < seq; ++k) ds[k] = p[k] * (ds[k] - dot) * scale;
+    }
+    for (int i = 0; i < seq; ++i)
+        for (int j = 0; j < dh; ++j) {
+            float acc = 0.0f;
+            for (int k = 0; k < seq; ++k) acc = fmaf(dS[(int64_t)i * seq + k], K[(int64_t)k * dh + j], acc);
+            dQ[(int64_t)i * dh + j] = acc;
+        }
+    for (int k = 0; k < seq; ++k)
+        for (int j = 0; j < dh; ++j) {
+            float acc = 0.0f;
+            for (int i = 0; i < seq; ++i) acc = fmaf(dS[(int64_t)i * seq + k], Q[(int64_t)i * dh + j], acc);
+            dK[(int64_t)k * dh + j] = acc;
+        }
+    free(P);
+    free(dS);
+    return 0;
 }

@@ -106,6 +106,14 @@ def test_flash_attention_validation():
     assert f(p, p, p, p, None, 1 << 23, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_TOO_LARGE
     arr = (ctypes.c_void_p * 65)(*([p] * 65))
     g = lib.vedic_flash_attention_fwd_heads
-    assert g(arr, arr, arr, arr, 65, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_TOO_LARGE
-    assert g(arr, arr, arr, arr, 0, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_BAD_DIM
+    assert g(arr, arr, arr, arr, None, 65, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_TOO_LARGE
+    assert g(arr, arr, arr, arr, None, 0, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_BAD_DIM
     assert _lib.status_string(_lib.STATUS_UNSUPPORTED).startswith("case not provided")
+    fl = lib.vedic_flash_attention_fwd_lse
+    assert fl(p, p, p, p, None, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_NULL_POINTER
+    b = lib.vedic_flash_attention_bwd
+    assert b(p, p, p, p, p, p, p, p, p, 16, 32, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED
+    assert b(p, p, p, p, p, None, p, p, p, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_NULL_POINTER
+    assert b(p, p, p, p, p, p, p, p, p + 4, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED
+    bh = lib.vedic_flash_attention_bwd_heads
+    assert bh(*([arr] * 9), 33, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_TOO_LARGE

@@ -156,3 +156,103 @@ def test_rejections():
         v.flash_attention_fwd(y, y, y, attn=torch.zeros((64, 64), device="cuda"))
     with pytest.raises(ValueError):
         v.flash_attention_fwd(y, y[:32], y)
+
+
+# ------------------------------------------------------------------ backward
+
+def fwd_with_lse(v, Q, K, V, scale, mask):
+    lse = torch.empty(Q.shape[0], device="cuda")
+    out = v.flash_attention_fwd(Q, K, V, scale=scale, causal=bool(mask[0]), shunyam=bool(mask[1]), window=mask[2],
+                                stride=mask[3], lse=lse)
+    return out, lse
+
+
+BWD_MASKS = [(1, 0, 0, 1), (0, 0, 0, 1), (1, 1, 8, 4), (0, 1, 5, 7)]
+
+
+@pytest.mark.parametrize("mask", BWD_MASKS)
+@pytest.mark.parametrize("dh", [64, 128])
+@pytest.mark.parametrize("seq", [1, 31, 33, 128, 129, 300])
+def test_backward_one_head(seq, dh, mask):
+    rng = np.random.default_rng(seq * 17 + dh + mask[2] + 3 * mask[0])
+    Q, K, V = qkv(rng, seq, dh)
+    dO = normal(rng, (seq, dh))
+    scale = 1.0 / np.sqrt(dh)
+    print(f"flash bwd seq={seq} dh={dh} mask={mask}", flush=True)
+    v = vedic()
+    tQ, tK, tV, tdO = dev(Q), dev(K), dev(V), dev(dO)
+    out, lse = fwd_with_lse(v, tQ, tK, tV, scale, mask)
+    O64, lse64 = o.flash_attention_stats_f64(Q, K, V, scale, *mask)
+    lse_h = host(lse)
+    fin = np.isfinite(lse64)
+    assert np.array_equal(np.isfinite(lse_h), fin)
+    assert np.max(np.abs(lse_h[fin] - lse64[fin])) <= 1e-5 * max(1.0, float(np.max(np.abs(lse64[fin]))))
+    grads = v.flash_attention_bwd(tQ, tK, tV, out, tdO, lse, scale=scale, causal=bool(mask[0]),
+                                  shunyam=bool(mask[1]), window=mask[2], stride=mask[3])
+    got = tuple(host(g) for g in grads)
+    want = o.flash_attention_bwd_f64(Q, K, V, dO, scale, *mask, stats=(O64, lse64))
+    err = o.grad_rel_err(got, want)
+    assert err <= fp32_tol(max(seq, dh)), f"{err:.3e}"
+    if mask == (1, 0, 0, 1):  # the reference's own backward recomputes with the causal mask only
+        ref = o.attention_backward_reference(Q, K, V, dO, scale)
+        assert o.grad_rel_err(got, ref) <= 2 * fp32_tol(max(seq, dh))
+
+
+@pytest.mark.parametrize("dh", [64, 128])
+def test_backward_heads_batched(dh):
+    rng = np.random.default_rng(500 + dh)
+    seq, H = 257, 3
+    heads = [qkv(rng, seq, dh) + (normal(rng, (seq, dh)),) for _ in range(H)]
+    scale = 1.0 / np.sqrt(dh)
+    v = vedic()
+    Qs, Ks, Vs, dOs = ([dev(h[i]) for h in heads] for i in range(4))
+    lses = [torch.empty(seq, device="cuda") for _ in range(H)]
+    outs = v.flash_attention_fwd_heads(Qs, Ks, Vs, scale=scale, lses=lses)
+    dQs, dKs, dVs = v.flash_attention_bwd_heads(Qs, Ks, Vs, outs, dOs, lses, scale=scale)
+    for i, (Q, K, V, dO) in enumerate(heads):
+        want = o.flash_attention_bwd_f64(Q, K, V, dO, scale)
+        got = (host(dQs[i]), host(dKs[i]), host(dVs[i]))
+        assert o.grad_rel_err(got, want) <= fp32_tol(seq), f"head {i}"
+
+
+def test_backward_deterministic():
+    rng = np.random.default_rng(9)
+    Q, K, V = (dev(x) for x in qkv(rng, 500, 64))
+    dO = dev(normal(rng, (500, 64)))
+    v = vedic()
+    out, lse = fwd_with_lse(v, Q, K, V, 0.125, (1, 0, 0, 1))
+    a = v.flash_attention_bwd(Q, K, V, out, dO, lse, scale=0.125)
+    b = v.flash_attention_bwd(Q, K, V, out, dO, lse, scale=0.125)
+    torch.cuda.synchronize()
+    assert all(torch.equal(x, y) for x, y in zip(a, b))
+
+
+def test_backward_full_size(full_heads):
+    """seq 8192, DH 64, causal: two heads of a 16-head launch, dQ on sampled
+    query rows and dK, dV on sampled key rows against float64."""
+    print("flash bwd full size", flush=True)
+    v = vedic()
+    rng = np.random.default_rng(88)
+    dOs_h = [normal(rng, (8192, 64)) for _ in range(16)]
+    Qs, Ks, Vs = ([dev(h[i]) for h in full_heads] for i in range(3))
+    dOs = [dev(x) for x in dOs_h]
+    lses = [torch.empty(8192, device="cuda") for _ in range(16)]
+    outs = v.flash_attention_fwd_heads(Qs, Ks, Vs, scale=0.125, lses=lses)
+    dQs, dKs, dVs = v.flash_attention_bwd_heads(Qs, Ks, Vs, outs, dOs, lses, scale=0.125)
+    rows = FULL_ROWS
+    for i in (0, 15):
+        Q, K, V = full_heads[i]
+        want = o.flash_attention_bwd_f64(Q, K, V, dOs_h[i], 0.125, q_rows=rows, k_rows=rows)
+        got = (host(dQs[i])[rows], host(dKs[i])[rows], host(dVs[i])[rows])
+        assert o.grad_rel_err(got, want) <= fp32_tol(8192), f"head {i}"
+
+
+def test_backward_rejections():
+    v = vedic()
+    x = torch.zeros((64, 64), device="cuda")
+    lse = torch.zeros(64, device="cuda")
+    with pytest.raises(ValueError):
+        v.flash_attention_bwd(x, x, x, x, x, lse[:32])
+    y = torch.zeros((64, 32), device="cuda")
+    with pytest.raises(ValueError):
+        v.flash_attention_bwd(y, y, y, y, y, lse)

@@ -390,3 +390,53 @@ def test_flash_catches_a_dropped_scale():
     right = o.flash_attention_f64(Q, K, V, 0.125)
     wrong = o.flash_attention(Q, K, V, 1.0)
     assert o.inf_rel_err(wrong, right) > 1e-2
+
+
+@pytest.mark.parametrize("causal,shunyam,window,stride", MASKS[:4])
+def test_attention_bwd_f64_against_finite_differences(causal, shunyam, window, stride):
+    """The float64 gradient of sum(dO * attention(Q, K, V)) against central
+    differences (every input, sampled entries)."""
+    rng = np.random.default_rng(21 + window)
+    seq, dh, sc = 20, 8, 0.3
+    Q, K, V, dO = (rng.standard_normal((seq, dh)) for _ in range(4))
+    grads = o.flash_attention_bwd_f64(Q, K, V, dO, sc, causal, shunyam, window, stride)
+
+    def loss(Q_, K_, V_):
+        out, _ = o.flash_attention_stats_f64(Q_, K_, V_, sc, causal, shunyam, window, stride)
+        return float((dO * out).sum())
+
+    eps = 1e-6
+    for which, (X, G) in enumerate(zip((Q, K, V), grads)):
+        for i, j in [(0, 0), (5, 3), (19, 7), (11, 2), (8, 5)]:
+            args_p, args_m = [Q, K, V], [Q, K, V]
+            args_p[which] = X.copy()
+            args_p[which][i, j] += eps
+            args_m[which] = X.copy()
+            args_m[which][i, j] -= eps
+            fd = (loss(*args_p) - loss(*args_m)) / (2 * eps)
+            assert abs(fd - G[i, j]) <= 1e-7 * max(1.0, abs(fd)), (which, i, j)
+
+
+def test_attention_bwd_f64_catches_a_dropped_delta():
+    """Leaving the rowsum term out of dS (a plausible slip) changes dQ well
+    beyond the bounds used against it."""
+    rng = np.random.default_rng(5)
+    seq, dh, sc = 24, 8, 0.4
+    Q, K, V, dO = (rng.standard_normal((seq, dh)) for _ in range(4))
+    dQ, _, _ = o.flash_attention_bwd_f64(Q, K, V, dO, sc)
+    out, lse = o.flash_attention_stats_f64(Q, K, V, sc)
+    P = np.where(o.attention_mask(seq), np.exp(sc * Q @ K.T - lse[:, None]), 0.0)
+    wrong = sc * ((P * (dO @ V.T)) @ K)
+    assert o.inf_rel_err(wrong, dQ) > 1e-2
+
+
+@pytest.mark.parametrize("seq,dh", [(1, 64), (33, 64), (70, 128)])
+def test_reference_backward_restatement_against_f64(seq, dh):
+    """The reference's per-head backward (causal recompute) against the float64
+    gradient of the causal forward."""
+    rng = np.random.default_rng(seq + dh)
+    Q, K, V, dO = (rng.standard_normal((seq, dh), dtype=np.float32) for _ in range(4))
+    sc = 1.0 / np.sqrt(dh)
+    got = o.attention_backward_reference(Q, K, V, dO, sc)
+    want = o.flash_attention_bwd_f64(Q, K, V, dO, sc, 1)
+    assert o.grad_rel_err(got, want) <= o.fp32_tolerance(max(seq, dh))
