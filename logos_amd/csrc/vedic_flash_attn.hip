@@ -280,9 +280,12 @@ __global__ void __launch_bounds__(256) flash_merge_kernel(FlashArgs a) {
     constexpr int SLOT = kFaQ * DH + 2 * kFaQ;
     const float* base = a.part + ((int64_t)head * a.items + fa_prefix(a, g)) * SLOT;
     float M = kFaMasked;
+    // loads of different chunks are independent: unrolled so they are in flight together
+#pragma unroll 8
     for (int c = 0; c < nch; ++c) M = fmaxf(M, base[(int64_t)c * SLOT + kFaQ * DH + qi]);
     float L = 0.0f;
     float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
     for (int c = 0; c < nch; ++c) {
         const float* sl = base + (int64_t)c * SLOT;
         const float w = __builtin_amdgcn_exp2f(sl[kFaQ * DH + qi] - M);
