@@ -56,6 +56,8 @@ def sampled_check(got_rows, layout, A, B, rows, tol, bias=None, gelu=False, labe
         ref = o.gemm_nt(As, B)
     else:
         ref = o.gemm_tn(As, B)
+    if bias is not None and layout != o.NN:
+        ref = ref + np.asarray(bias, np.float32)
     if gelu:
         ref = o.gelu(ref)
     err2 = o.inf_rel_err(got_rows, ref)

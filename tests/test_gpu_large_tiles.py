@@ -1,0 +1,85 @@
+"""The 256 x 256 fp16 tile (plain, bias and bias + GELU epilogues) on shapes
+large enough for the library to pick that tile, edges included.
+
+Every output is compared over the whole matrix with the same product through
+the epilogue that also writes the pre-activation (another instantiation of
+the kernel, same accumulation order), which must agree exactly, and on a
+seeded row sample (first and last rows included) with the fp64 oracle and the
+restated reference CPU path.  The shapes cover interior tiles only, tiles that
+cross the end of M, N and K, K below one stage, an odd number of stages, and
+workgroups that walk interior and edge tiles in turn.
+"""
+import zlib
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import oracle as o  # noqa: E402
+from tests._gpu_helpers import FP16_TOL, dev, dev_f16, host, normal  # noqa: E402
+from tests.test_gpu_configs import rows_of, sampled_check  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+OPS = {"NN": o.NN, "NT": o.NT, "TN": o.TN}
+# (M, N, K): edges in M, N and K; interior tiles with an odd stage count;
+# K below one 64-deep stage; edge and interior tiles with whole stages
+SHAPES = [(7000, 3464, 1000), (7936, 3840, 960), (7000, 3464, 40), (7000, 3464, 1024)]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    yield
+    torch.cuda.empty_cache()
+
+
+def _operands(rng, layout, M, N, K):
+    A = normal(rng, (K, M) if layout == o.TN else (M, K))
+    B = normal(rng, (N, K) if layout == o.NT else (K, N), std=0.25)
+    return A, B
+
+
+@pytest.mark.parametrize("epi", ["plain", "bias", "bias_gelu"])
+@pytest.mark.parametrize("opname", list(OPS))
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_large_tile_epilogues_match(shape, opname, epi):
+    from logos_amd import vedic
+
+    layout = OPS[opname]
+    M, N, K = shape
+    print(f"large-tile {opname} {epi} {shape}", flush=True)
+    rng = np.random.default_rng(zlib.crc32(f"{shape}-{opname}-{epi}".encode()))
+    A, B = _operands(rng, layout, M, N, K)
+    a, Ar = dev_f16(A)
+    b, Br = dev_f16(B)
+    bias = normal(rng, (N,), std=0.1) if epi != "plain" else None
+    kw = {}
+    if bias is not None:
+        kw = dict(bias=dev(bias), epilogue=vedic.EPI_BIAS_GELU if epi == "bias_gelu" else vedic.EPI_BIAS)
+    got = vedic.gemm(layout, a, b, **kw)
+    # the same product through the epilogue that also writes the pre-activation
+    pre = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    ref = vedic.gemm(layout, a, b, preact=pre, **kw)
+    g, r = host(got), host(ref)
+    assert np.array_equal(g, r), f"{np.count_nonzero(g != r)} elements differ from the pre-activation epilogue"
+    rows = rows_of(M, 11)
+    sampled_check(g[rows], layout, Ar, Br, rows, FP16_TOL, bias=bias, gelu=epi == "bias_gelu",
+                  label=f"{opname} {epi} {shape}")
+
+
+def test_large_tile_leaves_outside_rows_alone():
+    """C as rows 1..M of a larger buffer: the rows around it keep their values."""
+    from logos_amd import vedic
+
+    rng = np.random.default_rng(5)
+    M, N, K = 7000, 3464, 200
+    A, B = normal(rng, (M, K)), normal(rng, (K, N))
+    a, _ = dev_f16(A)
+    b, _ = dev_f16(B)
+    buf = torch.full((M + 2, N), 7.0, dtype=torch.float32, device="cuda")
+    vedic.gemm(o.NN, a, b, C=buf[1:M + 1])
+    h = host(buf)
+    assert np.all(h[0] == 7.0) and np.all(h[M + 1] == 7.0)
