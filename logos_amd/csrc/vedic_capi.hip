@@ -177,8 +177,10 @@ static int choose_ksplit(int M, int N, int K, int cus, bool f16) {
     }
     const int min_slice = f16 ? 1024 : 128;
     // fp32 products run on 256 x 64 tiles when N <= 64 and on 64 x 64 tiles
-    // when 128 x 128 ones would cover at most half the CUs (f32_small_tiles)
-    const int64_t tiles = (!f16 && N <= 64)                ? (int64_t)((M + 255) / 256)
+    // when 128 x 128 ones would cover at most half the CUs (f32_small_tiles);
+    // fp16 ones with N <= 64 on 64 x 32 tiles (128 x 32 for TN)
+    const int64_t tiles = (f16 && N <= 64)                 ? (int64_t)((M + 63) / 64) * ((N + 31) / 32)
+                          : (!f16 && N <= 64)              ? (int64_t)((M + 255) / 256)
                           : (!f16 && f32_small_tiles(M, N, cus)) ? (int64_t)((M + 63) / 64) * ((N + 63) / 64)
                                                                   : (int64_t)((M + 127) / 128) * ((N + 127) / 128);
     if (tiles * 2 > cus || K < 2 * min_slice) return 1;

@@ -49,10 +49,14 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
-// KC chunk swizzle for rows of CPR 16-byte chunks (CPR = BK / 8).
+// KC chunk swizzle for rows of CPR 16-byte chunks (CPR = BK / 8).  Rows of
+// 16 chunks (256 bytes, BK = 128) span the 64 banks exactly, so the chunk is
+// XORed with row mod 16: a 16-lane b128 group (16 consecutive rows) then
+// touches 16 distinct bank groups.
 template <int CPR>
 __device__ __forceinline__ int swz_kc(int r) {
-    if constexpr (CPR == 8) return (r & 7) ^ ((r >> 3) & 3);
+    if constexpr (CPR == 16) return r & 15;
+    else if constexpr (CPR == 8) return (r & 7) ^ ((r >> 3) & 3);
     else return ((r >> 1) ^ (r >> 3)) & 3;
 }
 // MC slot swizzle.  Rows of 16 or more slots (BM / BN >= 128): slots XOR
@@ -94,7 +98,10 @@ struct Side {
         const int q = (wave * NLD + i) * 64 + lane;
         row = q / CPR;
         const int p = q % CPR;
-        c = KC ? (p ^ swz_kc<CPR>(row)) : (p ^ swz_mc<R>(row));
+        if constexpr (KC)
+            c = p ^ swz_kc<CPR>(row);
+        else
+            c = p ^ swz_mc<R>(row);
     }
     __device__ __forceinline__ void init(int wave, int lane, int64_t ld, int mn0, int MN) {
 #pragma unroll
@@ -406,6 +413,26 @@ struct CfgMid {  // 256 x 128, eight waves of 64 x 64
     static constexpr int PER_CU = 1;
 };
 
+// Narrow products (N <= 64, e.g. one attention head's 8192 x 64 projection):
+// 32-column tiles, so a 64-column product has no empty half-tiles and a tall
+// one has enough tiles to fill the GPU.  NN and NT use 64 x 32 with two waves
+// of 32 x 32; TN uses 128 x 32 with four, since its A operand keeps the MC
+// layout, which takes 32 or at least 128 rows.
+#ifndef VEDIC_F16_NARROW_BK
+#define VEDIC_F16_NARROW_BK 128
+#endif
+#ifndef VEDIC_F16_NARROW_ST
+#define VEDIC_F16_NARROW_ST 4
+#endif
+struct CfgNarrow {
+    static constexpr int BM = 64, BN = 32, BK = VEDIC_F16_NARROW_BK, ST = VEDIC_F16_NARROW_ST, WGM = 2, WGN = 1;
+    static constexpr int PER_CU = 1;
+};
+struct CfgNarrowT {
+    static constexpr int BM = 128, BN = 32, BK = VEDIC_F16_NARROW_BK, ST = 3, WGM = 4, WGN = 1;
+    static constexpr int PER_CU = 1;
+};
+
 int device_cu_count();
 
 // Tile configuration for an M x N product on `cus` CUs: the one with the
@@ -467,6 +494,12 @@ static hipError_t launch_f16_kind(const GemmArgs& a, hipStream_t s) {
 // contiguous extent of each operand a multiple of 8 (checked by the caller).
 template <int OP>
 hipError_t launch_gemm_f16_direct_op(const GemmArgs& a, hipStream_t s) {
+    if (a.ksplit <= 1 && a.N <= 64) {
+        if constexpr (OP == 2)
+            return launch_f16_kind<OP, CfgNarrowT>(a, s);
+        else
+            return launch_f16_kind<OP, CfgNarrow>(a, s);
+    }
     switch (a.ksplit > 1 ? 2 : f16_tile_config(a.M, a.N, device_cu_count())) {
         case 0: return launch_f16_kind<OP, CfgLarge>(a, s);
         case 1: return launch_f16_kind<OP, CfgMid>(a, s);

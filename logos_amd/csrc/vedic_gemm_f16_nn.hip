@@ -29,6 +29,14 @@ template __global__ void gemm_f16_kernel<0, CfgMid::BM, CfgMid::BN, CfgMid::BK, 
 template __global__ void gemm_f16_kernel<0, CfgMid::BM, CfgMid::BN, CfgMid::BK, CfgMid::ST, CfgMid::WGM, CfgMid::WGN, EK_GENERIC>(GemmArgs);
 template __global__ void gemm_f16_kernel<0, CfgMid::BM, CfgMid::BN, CfgMid::BK, CfgMid::ST, CfgMid::WGM, CfgMid::WGN, EK_GELU_BWD>(GemmArgs);
 template __global__ void gemm_f16_kernel<0, CfgMid::BM, CfgMid::BN, CfgMid::BK, CfgMid::ST, CfgMid::WGM, CfgMid::WGN, EK_LINEAR_CS>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_PLAIN>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_BIAS>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_BIAS_GELU>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_BIAS_GELU_PRE>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_ACCUM>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_GENERIC>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_GELU_BWD>(GemmArgs);
+template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_LINEAR_CS>(GemmArgs);
 
 hipError_t launch_gemm_f16_direct_nn(const GemmArgs& a, hipStream_t s) {
     return launch_gemm_f16_direct_op<0>(a, s);

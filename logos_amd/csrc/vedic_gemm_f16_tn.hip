@@ -29,6 +29,14 @@ template __global__ void gemm_f16_kernel<2, CfgMid::BM, CfgMid::BN, CfgMid::BK, 
 template __global__ void gemm_f16_kernel<2, CfgMid::BM, CfgMid::BN, CfgMid::BK, CfgMid::ST, CfgMid::WGM, CfgMid::WGN, EK_GENERIC>(GemmArgs);
 template __global__ void gemm_f16_kernel<2, CfgMid::BM, CfgMid::BN, CfgMid::BK, CfgMid::ST, CfgMid::WGM, CfgMid::WGN, EK_GELU_BWD>(GemmArgs);
 template __global__ void gemm_f16_kernel<2, CfgMid::BM, CfgMid::BN, CfgMid::BK, CfgMid::ST, CfgMid::WGM, CfgMid::WGN, EK_LINEAR_CS>(GemmArgs);
+template __global__ void gemm_f16_kernel<2, CfgNarrowT::BM, CfgNarrowT::BN, CfgNarrowT::BK, CfgNarrowT::ST, CfgNarrowT::WGM, CfgNarrowT::WGN, EK_PLAIN>(GemmArgs);
+template __global__ void gemm_f16_kernel<2, CfgNarrowT::BM, CfgNarrowT::BN, CfgNarrowT::BK, CfgNarrowT::ST, CfgNarrowT::WGM, CfgNarrowT::WGN, EK_BIAS>(GemmArgs);
+template __global__ void gemm_f16_kernel<2, CfgNarrowT::BM, CfgNarrowT::BN, CfgNarrowT::BK, CfgNarrowT::ST, CfgNarrowT::WGM, CfgNarrowT::WGN, EK_BIAS_GELU>(GemmArgs);
+template __global__ void gemm_f16_kernel<2, CfgNarrowT::BM, CfgNarrowT::BN, CfgNarrowT::BK, CfgNarrowT::ST, CfgNarrowT::WGM, CfgNarrowT::WGN, EK_BIAS_GELU_PRE>(GemmArgs);
+template __global__ void gemm_f16_kernel<2, CfgNarrowT::BM, CfgNarrowT::BN, CfgNarrowT::BK, CfgNarrowT::ST, CfgNarrowT::WGM, CfgNarrowT::WGN, EK_ACCUM>(GemmArgs);
+template __global__ void gemm_f16_kernel<2, CfgNarrowT::BM, CfgNarrowT::BN, CfgNarrowT::BK, CfgNarrowT::ST, CfgNarrowT::WGM, CfgNarrowT::WGN, EK_GENERIC>(GemmArgs);
+template __global__ void gemm_f16_kernel<2, CfgNarrowT::BM, CfgNarrowT::BN, CfgNarrowT::BK, CfgNarrowT::ST, CfgNarrowT::WGM, CfgNarrowT::WGN, EK_GELU_BWD>(GemmArgs);
+template __global__ void gemm_f16_kernel<2, CfgNarrowT::BM, CfgNarrowT::BN, CfgNarrowT::BK, CfgNarrowT::ST, CfgNarrowT::WGM, CfgNarrowT::WGN, EK_LINEAR_CS>(GemmArgs);
 
 hipError_t launch_gemm_f16_direct_tn(const GemmArgs& a, hipStream_t s) {
     return launch_gemm_f16_direct_op<2>(a, s);
