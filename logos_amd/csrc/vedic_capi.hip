@@ -194,13 +194,47 @@ static int choose_ksplit(int M, int N, int K, int cus, bool f16) {
     return s >= 2 ? s : 1;
 }
 
-// Runs the product as `ks` slices into a stream-ordered workspace, then the
-// reduction with the caller's epilogue.  Slices are whole contraction steps
-// of the kernel (64 fp16 or 32 fp32 values).
-static hipError_t launch_split(bool f16, int op, bool vec, const GemmArgs& a, int ks, hipStream_t s) {
+// Contraction slice length for `ks` slices: whole steps of the kernel (64
+// fp16 or 32 fp32 values); `ks` becomes the number of slices that gives.
+static int split_kslice(int K, int& ks, bool f16) {
     const int step = f16 ? 64 : 32;
-    const int kslice = (((a.K + ks - 1) / ks) + step - 1) / step * step;
-    ks = (a.K + kslice - 1) / kslice;
+    const int kslice = (((K + ks - 1) / ks) + step - 1) / step * step;
+    ks = (K + kslice - 1) / kslice;
+    return kslice;
+}
+
+__global__ void zero_rows_kernel(float* __restrict__ C, int64_t ldc, int M, int N) {
+    const int64_t total = (int64_t)M * N;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x)
+        C[(i / N) * ldc + i % N] = 0.0f;
+}
+
+// A plain fp32 product in two contraction slices: C is zeroed, then both
+// slices add their raw partials into it with fp32 atomic adds.  The sum is
+// the same whichever slice lands first (0 + a + b = a + b = b + a in IEEE
+// arithmetic), so the result is deterministic, and neither a workspace nor a
+// reduction pass is needed.
+static hipError_t launch_split2_atomic(int op, const GemmArgs& a, int kslice, hipStream_t s) {
+    int64_t blocks = ((int64_t)a.M * a.N + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s, static_cast<float*>(a.C), a.ldc,
+                       a.M, a.N);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    GemmArgs p = a;
+    p.epi_kind = EK_ATOMIC;
+    p.ksplit = 2;
+    p.kslice = kslice;
+    p.c_split_stride = 0;
+    return op == VEDIC_OP_NN   ? launch_gemm_f32_direct_nn(p, s)
+           : op == VEDIC_OP_NT ? launch_gemm_f32_direct_nt(p, s)
+                               : launch_gemm_f32_direct_tn(p, s);
+}
+
+// Runs the product as `ks` slices into a stream-ordered workspace, then the
+// reduction with the caller's epilogue.
+static hipError_t launch_split(bool f16, int op, bool vec, const GemmArgs& a, int ks, hipStream_t s) {
+    const int kslice = split_kslice(a.K, ks, f16);
     const int64_t total = (int64_t)a.M * a.N;
     float* ws = nullptr;
     hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), sizeof(float) * (size_t)total * ks, s);
@@ -342,7 +376,12 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
         // decode-time shapes: bound by streaming B once from HBM
         e = f16 ? launch_gemm_f16_skinny(a, s) : launch_gemm_f32_skinny(a, s);
     } else if (ks > 1) {
-        e = launch_split(f16, d->op, vec, a, ks, s);
+        int ks2 = ks;
+        const int kslice = split_kslice(d->K, ks2, f16);
+        if (!f16 && direct && ks2 == 2 && a.epi_kind == EK_PLAIN)
+            e = launch_split2_atomic(d->op, a, kslice, s);
+        else
+            e = launch_split(f16, d->op, vec, a, ks, s);
     } else if (f16 && direct) {
         e = d->op == VEDIC_OP_NN   ? launch_gemm_f16_direct_nn(a, s)
             : d->op == VEDIC_OP_NT ? launch_gemm_f16_direct_nt(a, s)

@@ -401,6 +401,30 @@ def test_split_k_fp32(opname, shape):
     assert np.array_equal(host(vedic.gemm(layout, a, b)), got)
 
 
+@pytest.mark.parametrize("opname", list(OPS))
+def test_split_k_fp32_two_slices_atomic(opname):
+    """Plain fp32 products split into two slices add both into a zeroed C with
+    atomic adds (config 1's 512 x 1024 x 1024 is one): C may hold anything
+    beforehand, a row pitch wider than N leaves the gap untouched, and eight
+    runs agree bit for bit (two addends onto zero commute exactly)."""
+    vedic = V()
+    layout = OPS[opname]
+    M, N, K = 512, 1024, 1024
+    rng = np.random.default_rng(zlib.crc32(f"split2-{opname}".encode()))
+    A, B = _operands(rng, layout, M, N, K)
+    a, b = dev(A), dev(B)
+    buf = torch.full((M, N + 8), float("nan"), dtype=torch.float32, device="cuda")
+    C = buf[:, :N]
+    vedic.gemm(layout, a, b, C)
+    first = host(C).copy()
+    check(first, layout, A, B, tol=fp32_tol(K), label=f"two-slice fp32 {opname}")
+    assert np.all(np.isnan(host(buf[:, N:]))), "the row gap was written"
+    for _ in range(7):
+        C.fill_(12345.0)
+        vedic.gemm(layout, a, b, C)
+        assert np.array_equal(host(C), first)
+
+
 def test_split_k_fp32_epilogues():
     vedic = V()
     rng = np.random.default_rng(31)
