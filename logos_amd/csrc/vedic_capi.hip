@@ -204,9 +204,10 @@ static int split_kslice(int K, int& ks, bool f16) {
 }
 
 __global__ void zero_rows_kernel(float* __restrict__ C, int64_t ldc, int M, int N) {
-    const int64_t total = (int64_t)M * N;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x)
-        C[(i / N) * ldc + i % N] = 0.0f;
+    for (int r = blockIdx.x; r < M; r += gridDim.x) {
+        float* row = C + (int64_t)r * ldc;
+        for (int c = threadIdx.x; c < N; c += blockDim.x) row[c] = 0.0f;
+    }
 }
 
 // A plain fp32 product in two contraction slices: C is zeroed, then both
@@ -215,8 +216,7 @@ __global__ void zero_rows_kernel(float* __restrict__ C, int64_t ldc, int M, int 
 // arithmetic), so the result is deterministic, and neither a workspace nor a
 // reduction pass is needed.
 static hipError_t launch_split2_atomic(int op, const GemmArgs& a, int kslice, hipStream_t s) {
-    int64_t blocks = ((int64_t)a.M * a.N + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
+    const int blocks = a.M < 4096 ? a.M : 4096;  // one row per workgroup and step
     hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s, static_cast<float*>(a.C), a.ldc,
                        a.M, a.N);
     hipError_t e = hipGetLastError();
@@ -691,6 +691,45 @@ __global__ void dsum_cols_partial_kernel(const T* __restrict__ X, int64_t ld, in
     part[(int64_t)blockIdx.y * cols + c] = s;
 }
 
+// The same with 16-byte loads (rows and X 16-byte aligned, cols a multiple
+// of E = 16 / sizeof(T)): thread (x, y) sums columns E (64 blockIdx.x + x)
+// .. + E - 1 over rows y, y + 4, ... of the chunk; the four row groups are
+// then added in ascending y.
+template <typename T>
+__global__ void __launch_bounds__(256) dsum_cols_partial_vec_kernel(const T* __restrict__ X, int64_t ld, int rows,
+                                                                    int cols, double* __restrict__ part) {
+    constexpr int E = 16 / sizeof(T);
+    __shared__ double sh[3][64][E];
+    const int x = threadIdx.x & 63, y = threadIdx.x >> 6;
+    const int v = blockIdx.x * 64 + x;
+    const bool on = v * E < cols;
+    const int r0 = blockIdx.y * kDsumChunk, r1 = min(rows, r0 + kDsumChunk);
+    double s[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) s[e] = 0.0;
+    if (on) {
+#pragma unroll 4
+        for (int r = r0 + y; r < r1; r += 4) {
+            const float4_t q = *reinterpret_cast<const float4_t*>(X + (int64_t)r * ld + (int64_t)v * E);
+            const T* xv = reinterpret_cast<const T*>(&q);
+#pragma unroll
+            for (int e = 0; e < E; ++e) s[e] += (double)xv[e];
+        }
+    }
+    if (y > 0) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) sh[y - 1][x][e] = s[e];
+    }
+    __syncthreads();
+    if (y == 0 && on) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const double t = ((s[e] + sh[0][x][e]) + sh[1][x][e]) + sh[2][x][e];
+            part[(int64_t)blockIdx.y * cols + (int64_t)v * E + e] = t;
+        }
+    }
+}
+
 // 32 columns per workgroup, 8 groups of 32 threads each adding a contiguous
 // run of chunks in ascending order, then the 8 group sums in ascending order.
 __global__ void __launch_bounds__(256) dsum_cols_reduce_kernel(const double* __restrict__ part, int nchunks,
@@ -701,8 +740,10 @@ __global__ void __launch_bounds__(256) dsum_cols_reduce_kernel(const double* __r
     const int q = (nchunks + 7) / 8;
     const int q0 = min(nchunks, g * q), q1 = min(nchunks, q0 + q);
     double s = 0.0;
-    if (col < cols)
+    if (col < cols) {
+#pragma unroll 8
         for (int k = q0; k < q1; ++k) s += part[(int64_t)k * cols + col];
+    }
     sh[g][c] = s;
     __syncthreads();
     if (g == 0 && col < cols) {
@@ -713,25 +754,28 @@ __global__ void __launch_bounds__(256) dsum_cols_reduce_kernel(const double* __r
 }
 
 // res[0] = sum_j cs[j], res[1] = sum_k sa[k] sb[k], res[2] = sum_j bias[j]
-// (bias may be null), each by one workgroup with a fixed stride-256 order and
-// a fixed tree.
-__global__ void __launch_bounds__(256) checksum_finalize_kernel(const float* __restrict__ cs, int N,
-                                                                const double* __restrict__ sa,
-                                                                const double* __restrict__ sb, int K,
-                                                                const float* __restrict__ bias,
-                                                                double* __restrict__ res) {
-    __shared__ double red[3][256];
+// (bias may be null), by one workgroup with a fixed stride-1024 order and a
+// fixed tree.
+constexpr int kFinThreads = 1024;
+__global__ void __launch_bounds__(kFinThreads) checksum_finalize_kernel(const float* __restrict__ cs, int N,
+                                                                        const double* __restrict__ sa,
+                                                                        const double* __restrict__ sb, int K,
+                                                                        const float* __restrict__ bias,
+                                                                        double* __restrict__ res) {
+    __shared__ double red[3][kFinThreads];
     double s0 = 0.0, s1 = 0.0, s2 = 0.0;
-    for (int j = threadIdx.x; j < N; j += 256) {
+#pragma unroll 8
+    for (int j = threadIdx.x; j < N; j += kFinThreads) {
         s0 += (double)cs[j];
         if (bias) s2 += (double)bias[j];
     }
-    for (int k = threadIdx.x; k < K; k += 256) s1 += sa[k] * sb[k];
+#pragma unroll 4
+    for (int k = threadIdx.x; k < K; k += kFinThreads) s1 += sa[k] * sb[k];
     red[0][threadIdx.x] = s0;
     red[1][threadIdx.x] = s1;
     red[2][threadIdx.x] = s2;
     __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
+    for (int w = kFinThreads / 2; w > 0; w >>= 1) {
         if ((int)threadIdx.x < w)
             for (int t = 0; t < 3; ++t) red[t][threadIdx.x] += red[t][threadIdx.x + w];
         __syncthreads();
@@ -740,11 +784,26 @@ __global__ void __launch_bounds__(256) checksum_finalize_kernel(const float* __r
 }
 
 template <typename T>
-__global__ void dsum_rows_kernel(const T* __restrict__ X, int64_t ld, int cols, double* __restrict__ out) {
+__global__ void dsum_rows_kernel(const T* __restrict__ X, int64_t ld, int cols, double* __restrict__ out, int vec) {
     __shared__ double red[kEwThreads];
-    const int64_t base = (int64_t)blockIdx.x * ld;
+    constexpr int E = 16 / sizeof(T);
+    const T* row = X + (int64_t)blockIdx.x * ld;
     double s = 0.0;
-    for (int c = threadIdx.x; c < cols; c += kEwThreads) s += (double)X[base + c];
+    int c0 = 0;
+    if (vec) {  // 16-byte loads; the row start is 16-byte aligned
+        const int nv = cols / E;
+#pragma unroll 4
+        for (int v = threadIdx.x; v < nv; v += kEwThreads) {
+            const float4_t q = *reinterpret_cast<const float4_t*>(row + (int64_t)v * E);
+            const T* x = reinterpret_cast<const T*>(&q);
+            double t = 0.0;
+#pragma unroll
+            for (int e = 0; e < E; ++e) t += (double)x[e];
+            s += t;
+        }
+        c0 = nv * E;
+    }
+    for (int c = c0 + threadIdx.x; c < cols; c += kEwThreads) s += (double)row[c];
     red[threadIdx.x] = s;
     __syncthreads();
     for (int w = kEwThreads / 2; w > 0; w >>= 1) {
@@ -762,14 +821,21 @@ static size_t dsum_scratch(int rows, int cols, bool along_rows) {
 template <typename T>
 static void launch_dsum(const T* X, int64_t ld, int rows, int cols, bool along_rows, double* out, double* scratch,
                         hipStream_t s) {
+    constexpr int E = 16 / sizeof(T);
+    const bool vec = aligned16(X) && ld % E == 0;  // every row starts 16-byte aligned
     if (along_rows) {
         const int nq = (rows + kDsumChunk - 1) / kDsumChunk;
-        hipLaunchKernelGGL(dsum_cols_partial_kernel<T>, dim3((unsigned)((cols + 255) / 256), (unsigned)nq),
-                           dim3(256), 0, s, X, ld, rows, cols, scratch);
+        if (vec && cols % E == 0)
+            hipLaunchKernelGGL(dsum_cols_partial_vec_kernel<T>, dim3((unsigned)((cols / E + 63) / 64), (unsigned)nq),
+                               dim3(256), 0, s, X, ld, rows, cols, scratch);
+        else
+            hipLaunchKernelGGL(dsum_cols_partial_kernel<T>, dim3((unsigned)((cols + 255) / 256), (unsigned)nq),
+                               dim3(256), 0, s, X, ld, rows, cols, scratch);
         hipLaunchKernelGGL(dsum_cols_reduce_kernel, dim3((unsigned)((cols + 31) / 32)), dim3(256), 0, s, scratch,
                            nq, cols, out);
     } else {
-        hipLaunchKernelGGL(dsum_rows_kernel<T>, dim3((unsigned)rows), dim3(kEwThreads), 0, s, X, ld, cols, out);
+        hipLaunchKernelGGL(dsum_rows_kernel<T>, dim3((unsigned)rows), dim3(kEwThreads), 0, s, X, ld, cols, out,
+                           vec ? 1 : 0);
     }
 }
 
@@ -907,7 +973,7 @@ extern "C" int vedic_gemm_checked(const vedic_gemm_desc_t* d, float tolerance, v
             launch_dsum(static_cast<const float*>(d->B), d->ldb, br, bc, b_rows, d_sb, d_scr_b, s);
         }
         double* d_res = d_scr_b + scr_b;  // 3 doubles
-        hipLaunchKernelGGL(checksum_finalize_kernel, dim3(1), dim3(256), 0, s, d_cs, N, d_sa, d_sb, K,
+        hipLaunchKernelGGL(checksum_finalize_kernel, dim3(1), dim3(kFinThreads), 0, s, d_cs, N, d_sa, d_sb, K,
                            want_bias ? d->bias : nullptr, d_res);
         e = hipGetLastError();
         double host[3] = {0.0, 0.0, 0.0};
