@@ -52,12 +52,14 @@ typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 // KC chunk swizzle for rows of CPR 16-byte chunks (CPR = BK / 8).  Rows of
 // 16 chunks (256 bytes, BK = 128) span the 64 banks exactly, so the chunk is
 // XORed with row mod 16: a 16-lane b128 group (16 consecutive rows) then
-// touches 16 distinct bank groups.
+// touches 16 distinct bank groups.  Rows of 4 chunks (64 bytes, BK = 32):
+// four consecutive rows fill one 256-byte bank window, and XOR with
+// (row / 4) mod 4 separates the four rows that share a window position.
 template <int CPR>
 __device__ __forceinline__ int swz_kc(int r) {
     if constexpr (CPR == 16) return r & 15;
     else if constexpr (CPR == 8) return (r & 7) ^ ((r >> 3) & 3);
-    else return ((r >> 1) ^ (r >> 3)) & 3;
+    else return (r >> 2) & 3;
 }
 // MC slot swizzle.  Rows of 16 or more slots (BM / BN >= 128): slots XOR
 // 4 (k mod 4).  Rows of 4 slots (32 columns, 64 bytes) need none: the four
