@@ -437,6 +437,10 @@ struct CfgNarrowT {
 
 int device_cu_count();
 
+#ifndef VEDIC_F16_COLUMN_SPLIT
+#define VEDIC_F16_COLUMN_SPLIT 1
+#endif
+
 // Tile configuration for an M x N product on `cus` CUs: the one with the
 // least estimated time, rounds of resident tiles x the work one CU does per
 // round / the configuration's relative efficiency (in percent, measured).
@@ -494,6 +498,53 @@ static hipError_t launch_f16_kind(const GemmArgs& a, hipStream_t s) {
 
 // Requires: A, B 16-byte aligned; lda, ldb multiples of 8 and < 2^22; the
 // contiguous extent of each operand a multiple of 8 (checked by the caller).
+// Column split against tile quantization: when the 256 x 256 tiles of the
+// first n1 columns fill whole rounds and the remaining columns fit one round
+// of 256 x 128 tiles, two launches (n1 columns large, the rest mid) beat any
+// single configuration whose last round is partly empty (8192 x 3072: one
+// round of each, against three rounds of 256 x 128 tiles).  Returns n1, or 0
+// for no split.  Same cost model as f16_tile_config.
+inline int f16_column_split(int M, int N, int cus) {
+    const int tm = (M + 255) / 256;
+    if (tm <= 0 || cus % tm != 0) return 0;
+    const int cols_round = cus / tm * 256;  // columns one round of 256 x 256 tiles covers
+    const int n1 = N / cols_round * cols_round;
+    if (n1 == 0 || n1 == N) return 0;
+    const int64_t mid_tiles = (int64_t)((M + 255) / 256) * ((N - n1 + 127) / 128);
+    if (mid_tiles > cus) return 0;
+    const double t_split = (double)(n1 / cols_round) * 256 * 256 + 256.0 * 128 * 100.0 / VEDIC_F16_MID_EFF;
+    // the best single configuration's estimate
+    struct C { int bm, bn, per_cu, eff; };
+    const C cfgs[3] = {{256, 256, 1, 100}, {256, 128, 1, VEDIC_F16_MID_EFF}, {128, 128, VEDIC_F16_SMALL_PER_CU, VEDIC_F16_SMALL_EFF}};
+    double best = 0.0;
+    for (int i = 0; i < 3; ++i) {
+        const int64_t tiles = (int64_t)((M + cfgs[i].bm - 1) / cfgs[i].bm) * ((N + cfgs[i].bn - 1) / cfgs[i].bn);
+        const int64_t slots = (int64_t)cus * cfgs[i].per_cu;
+        const int64_t rounds = (tiles + slots - 1) / slots;
+        const int64_t per_cu = tiles < slots ? (tiles + cus - 1) / cus : cfgs[i].per_cu;
+        const double t = (double)rounds * per_cu * cfgs[i].bm * cfgs[i].bn * 100.0 / cfgs[i].eff;
+        if (i == 0 || t < best) best = t;
+    }
+    return t_split < best ? n1 : 0;
+}
+
+// The same product restricted to columns [c0, c0 + n): operand B, C, the
+// bias, the pre-activation and the scattered heads shifted to column c0.
+template <int OP>
+inline GemmArgs f16_columns(const GemmArgs& a, int c0, int n) {
+    GemmArgs p = a;
+    const _Float16* B = static_cast<const _Float16*>(a.B);
+    p.B = OP == 1 ? B + (int64_t)c0 * a.ldb : B + c0;
+    const int es = (a.epi_kind == EK_GENERIC && (a.epi & EPI_F16OUT)) ? 2 : 4;
+    p.C = static_cast<char*>(a.C) + (int64_t)c0 * es;
+    if (a.bias) p.bias = a.bias + c0;
+    if (a.preact) p.preact = a.preact + c0;
+    if (a.head_cols > 0)
+        for (int h = 0; h < kMaxHeads; ++h) p.heads[h] = h + c0 / a.head_cols < kMaxHeads ? a.heads[h + c0 / a.head_cols] : nullptr;
+    p.N = n;
+    return p;
+}
+
 template <int OP>
 hipError_t launch_gemm_f16_direct_op(const GemmArgs& a, hipStream_t s) {
     if (a.ksplit <= 1 && a.N <= 64) {
@@ -501,6 +552,14 @@ hipError_t launch_gemm_f16_direct_op(const GemmArgs& a, hipStream_t s) {
             return launch_f16_kind<OP, CfgNarrowT>(a, s);
         else
             return launch_f16_kind<OP, CfgNarrow>(a, s);
+    }
+    if (a.ksplit <= 1 && a.cs_part == nullptr && VEDIC_F16_COLUMN_SPLIT) {
+        const int n1 = f16_column_split(a.M, a.N, device_cu_count());
+        if (n1 > 0 && (a.head_cols <= 0 || n1 % a.head_cols == 0)) {
+            const hipError_t e = launch_f16_kind<OP, CfgLarge>(f16_columns<OP>(a, 0, n1), s);
+            if (e != hipSuccess) return e;
+            return launch_f16_kind<OP, CfgMid>(f16_columns<OP>(a, n1, a.N - n1), s);
+        }
     }
     switch (a.ksplit > 1 ? 2 : f16_tile_config(a.M, a.N, device_cu_count())) {
         case 0: return launch_f16_kind<OP, CfgLarge>(a, s);

@@ -1,5 +1,6 @@
 """The 256 x 256 fp16 tile (plain, bias and bias + GELU epilogues) on shapes
-large enough for the library to pick that tile, edges included.
+large enough for the library to pick that tile, edges included, and the
+column split that runs part of a product on 256 x 128 tiles.
 
 Every output is compared over the whole matrix with the same product through
 the epilogue that also writes the pre-activation (another instantiation of
@@ -24,8 +25,11 @@ pytestmark = pytest.mark.gpu
 
 OPS = {"NN": o.NN, "NT": o.NT, "TN": o.TN}
 # (M, N, K): edges in M, N and K; interior tiles with an odd stage count;
-# K below one 64-deep stage; edge and interior tiles with whole stages
-SHAPES = [(7000, 3464, 1000), (7936, 3840, 960), (7000, 3464, 40), (7000, 3464, 1024)]
+# K below one 64-deep stage; edge and interior tiles with whole stages; and
+# two products the library splits by columns (2048 columns of 256 x 256
+# tiles, the rest on 256 x 128 tiles), the second with an edge in N
+SHAPES = [(7000, 3464, 1000), (7936, 3840, 960), (7000, 3464, 40), (7000, 3464, 1024), (8192, 3072, 1024),
+          (8192, 3000, 200)]
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -83,3 +87,22 @@ def test_large_tile_leaves_outside_rows_alone():
     vedic.gemm(o.NN, a, b, C=buf[1:M + 1])
     h = host(buf)
     assert np.all(h[0] == 7.0) and np.all(h[M + 1] == 7.0)
+
+
+@pytest.mark.parametrize("opname", list(OPS))
+def test_column_split_fp16_output(opname):
+    """fp16 C through the column split: the second part's C starts 2048
+    two-byte elements in."""
+    from logos_amd import vedic
+
+    layout = OPS[opname]
+    M, N, K = 8192, 3072, 256
+    rng = np.random.default_rng(zlib.crc32(f"split16-{opname}".encode()))
+    A, B = _operands(rng, layout, M, N, K)
+    a, Ar = dev_f16(A)
+    b, Br = dev_f16(B)
+    got = host(vedic.gemm(layout, a, b, out_dtype=torch.float16))
+    rows = rows_of(M, 13)
+    want, _ = o.gemm_f64(layout, np.ascontiguousarray(Ar[:, rows]) if layout == o.TN else Ar[rows], Br)
+    err = o.inf_rel_err(got[rows], want)
+    assert err <= FP16_TOL, f"{opname} fp16 out: {err:.3e}"
