@@ -71,13 +71,23 @@ __device__ __forceinline__ float ld_f16(__amdgpu_buffer_rsrc_t rs, uint32_t voff
     return (float)__builtin_bit_cast(_Float16, b);
 }
 
+// Whether epilogue kind KIND adds the bias (the generic and column-sum kinds
+// when the flags ask for it).
+template <int KIND>
+__device__ __forceinline__ bool epi_wants_bias(const GemmArgs& a) {
+    return (KIND == EK_BIAS || KIND == EK_BIAS_GELU || KIND == EK_BIAS_GELU_PRE) ||
+           ((KIND == EK_GENERIC || KIND == EK_LINEAR_CS) && (a.epi & EPI_BIAS));
+}
+
 // Writes a (32*MI) x (32*NI) wave tile whose top-left output is (row0, col0)
 // of the matrix at Cp (a.C, or a split-K slab of the workspace).
 // CHECK: the tile may extend past M or N.  Offsets are 32-bit: the caller
 // guarantees (32*MI) * ld * 4 < 2^31 for ldc and ldp.
+// bias_pre: the NI bias values of this lane's columns, already loaded by the
+// caller (columns past N as 0), or null to load them here.
 template <int KIND, bool CHECK, int MI, int NI>
 __device__ __forceinline__ void epilogue(const GemmArgs& a, void* Cp, const float16_t (&acc)[MI][NI], int row0,
-                                         int col0, int lane) {
+                                         int col0, int lane, const float* bias_pre = nullptr) {
     const int l32 = lane & 31, h = lane >> 5;
     const bool f16out = (KIND == EK_GENERIC) && (a.epi & EPI_F16OUT);
     const int es = f16out ? 2 : 4;
@@ -93,8 +103,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, void* Cp, const floa
     const bool colsum = (KIND == EK_GELU_BWD || KIND == EK_GENERIC || KIND == EK_LINEAR_CS) && a.cs_part != nullptr;
     const uint32_t ldc_b = (uint32_t)(a.ldc * es);
     const uint32_t ldp_b = (uint32_t)(a.ldp * 4);
-    const bool want_bias = (KIND == EK_BIAS || KIND == EK_BIAS_GELU || KIND == EK_BIAS_GELU_PRE) ||
-                           ((KIND == EK_GENERIC || KIND == EK_LINEAR_CS) && (a.epi & EPI_BIAS));
+    const bool want_bias = epi_wants_bias<KIND>(a);
     const int row_lim = a.M - row0 - 4 * h;  // rows 4h + u of the tile exist iff u < row_lim
     // Kinds that read memory per element (the old C, the pre-activation) load
     // a whole 32 x 32 block's values before they are needed: the next block's
@@ -109,7 +118,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, void* Cp, const floa
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
         const int col = col0 + 32 * j + l32;
-        bias_j[j] = (want_bias && (!CHECK || col < a.N)) ? a.bias[col] : 0.0f;
+        bias_j[j] = !want_bias ? 0.0f : bias_pre ? bias_pre[j] : (!CHECK || col < a.N) ? a.bias[col] : 0.0f;
     }
     // Scattered C (plain and bias kinds only; the host allows it for no
     // other): block column c0 lies in head c0 / head_cols, whose matrix
