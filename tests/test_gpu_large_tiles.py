@@ -106,3 +106,32 @@ def test_column_split_fp16_output(opname):
     want, _ = o.gemm_f64(layout, np.ascontiguousarray(Ar[:, rows]) if layout == o.TN else Ar[rows], Br)
     err = o.inf_rel_err(got[rows], want)
     assert err <= FP16_TOL, f"{opname} fp16 out: {err:.3e}"
+
+
+@pytest.mark.parametrize("opname", list(OPS))
+def test_large_tile_padded_leading_dimensions(opname):
+    """A, B and C as views into wider buffers (row pitch > the used extent) on
+    the 256 x 256 tile: the same bits as the contiguous product, and the
+    padding columns of C untouched."""
+    from logos_amd import vedic
+
+    layout = OPS[opname]
+    M, N, K = 4096, 4096, 512
+    rng = np.random.default_rng(zlib.crc32(f"padded-{opname}".encode()))
+    A, B = _operands(rng, layout, M, N, K)
+    a, Ar = dev_f16(A)
+    b, Br = dev_f16(B)
+    bias = dev(normal(rng, (N,), std=0.1))
+    want = host(vedic.gemm(layout, a, b, bias=bias, epilogue=vedic.EPI_BIAS_GELU))
+    pa = torch.zeros((a.shape[0], a.shape[1] + 40), dtype=torch.float16, device="cuda")
+    pb = torch.zeros((b.shape[0], b.shape[1] + 72), dtype=torch.float16, device="cuda")
+    pa[:, :a.shape[1]] = a
+    pb[:, :b.shape[1]] = b
+    pc = torch.full((M, N + 24), 3.0, dtype=torch.float32, device="cuda")
+    vedic.gemm(layout, pa[:, :a.shape[1]], pb[:, :b.shape[1]], pc[:, :N], bias=bias, epilogue=vedic.EPI_BIAS_GELU)
+    got = host(pc)
+    assert np.array_equal(got[:, :N], want), "padded operands changed the result"
+    assert np.all(got[:, N:] == 3.0), "the row padding of C was written"
+    rows = rows_of(M, 17)
+    sampled_check(want[rows], layout, Ar, Br, rows, FP16_TOL, bias=host(bias), gelu=True,
+                  label=f"padded {opname}")
