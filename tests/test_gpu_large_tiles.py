@@ -108,16 +108,18 @@ def test_column_split_fp16_output(opname):
     assert err <= FP16_TOL, f"{opname} fp16 out: {err:.3e}"
 
 
+@pytest.mark.parametrize("shape", [(4096, 4096, 512), (8192, 3072, 256)], ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("opname", list(OPS))
-def test_large_tile_padded_leading_dimensions(opname):
+def test_large_tile_padded_leading_dimensions(opname, shape):
     """A, B and C as views into wider buffers (row pitch > the used extent) on
-    the 256 x 256 tile: the same bits as the contiguous product, and the
-    padding columns of C untouched."""
+    the 256 x 256 tile and through the column split (whose second part starts
+    B 2048 columns -- for NT 2048 rows of pitch ldb -- in): the same bits as
+    the contiguous product, and the padding columns of C untouched."""
     from logos_amd import vedic
 
     layout = OPS[opname]
-    M, N, K = 4096, 4096, 512
-    rng = np.random.default_rng(zlib.crc32(f"padded-{opname}".encode()))
+    M, N, K = shape
+    rng = np.random.default_rng(zlib.crc32(f"padded-{opname}-{shape}".encode()))
     A, B = _operands(rng, layout, M, N, K)
     a, Ar = dev_f16(A)
     b, Br = dev_f16(B)
