@@ -202,12 +202,22 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f32_kernel(GemmArgs args) 
 #pragma unroll
     for (int s = 0; s < ST - 1; ++s) VEDIC_ISSUE32(s, As[s], Bs[s]);
 
+    // The bias is loaded as a tile starts and waited for before the next
+    // tile's first stages are issued (as in the fp16 kernel): the epilogue
+    // then never waits behind those stage loads in the in-order counter.
+    const bool pre_bias = epi_wants_bias<KIND>(args);  // (split-K slices run the plain kind)
+    float bias_pre[NI];
     while (true) {
         float16_t acc[MI][NI];
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int j = 0; j < NI; ++j) acc[i][j] = float16_t{};
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const int col = n0 + wn * WN + 32 * j + lane % 32;
+            bias_pre[j] = pre_bias && col < args.N ? args.bias[col] : 0.0f;
+        }
 
         // Uniform pipeline: every stage step waits for the same number of
         // loads and issues stage kt + ST - 1, which past the work item's
@@ -235,6 +245,8 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f32_kernel(GemmArgs args) 
                                        : args.C;
         w += G;
         const bool more = w < nwork;
+#pragma unroll
+        for (int j = 0; j < NI; ++j) asm volatile("" : "+v"(bias_pre[j]));  // the bias has landed
         if (more) {
             __syncthreads();  // every wave is done reading the stage buffers
             it = work_of<BM, BN, BK>(args, w, ntiles);
@@ -247,9 +259,9 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f32_kernel(GemmArgs args) 
         }
         const bool full = (row0 + WM <= args.M) && (col0 + WN <= args.N);
         if (KIND != EK_GENERIC && full)
-            epilogue<KIND, false, MI, NI>(args, cp, acc, row0, col0, lane);
+            epilogue<KIND, false, MI, NI>(args, cp, acc, row0, col0, lane, pre_bias ? bias_pre : nullptr);
         else
-            epilogue<KIND, true, MI, NI>(args, cp, acc, row0, col0, lane);
+            epilogue<KIND, true, MI, NI>(args, cp, acc, row0, col0, lane, pre_bias ? bias_pre : nullptr);
         if (!more) break;
     }
     wait_vmcnt<0>();  // the trailing zero loads still write LDS
