@@ -672,86 +672,10 @@ __global__ void arraysum_kernel(const float* __restrict__ x, int64_t n, double* 
 
 // Sums in double over one dimension of a strided matrix of T (float or
 // binary16), for the checked GEMM: along_rows = true gives, for each column c,
-// sum_r X[r][c]; false gives, for each row r, sum_c X[r][c].  One thread per
-// output; rows are read as contiguous segments across threads when summing
-// columns, and with a fixed stride-64 tree when summing rows.
-// Column sums in two fixed-order levels: part[q][c] over the rows of chunk q
-// (kDsumChunk rows), then the chunks in ascending q.
+// sum_r X[r][c]; false gives, for each row r, sum_c X[r][c]
+// (dsum_pair_pass1_kernel and dsum_pair_pass2_kernel below).  Column sums
+// come in two fixed-order levels over chunks of kDsumChunk rows.
 constexpr int kDsumChunk = 64;
-
-template <typename T>
-__global__ void dsum_cols_partial_kernel(const T* __restrict__ X, int64_t ld, int rows, int cols,
-                                         double* __restrict__ part) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= cols) return;
-    const int r0 = blockIdx.y * kDsumChunk, r1 = min(rows, r0 + kDsumChunk);
-    double s = 0.0;
-#pragma unroll 4
-    for (int r = r0; r < r1; ++r) s += (double)X[(int64_t)r * ld + c];
-    part[(int64_t)blockIdx.y * cols + c] = s;
-}
-
-// The same with 16-byte loads (rows and X 16-byte aligned, cols a multiple
-// of E = 16 / sizeof(T)): thread (x, y) sums columns E (64 blockIdx.x + x)
-// .. + E - 1 over rows y, y + 4, ... of the chunk; the four row groups are
-// then added in ascending y.
-template <typename T>
-__global__ void __launch_bounds__(256) dsum_cols_partial_vec_kernel(const T* __restrict__ X, int64_t ld, int rows,
-                                                                    int cols, double* __restrict__ part) {
-    constexpr int E = 16 / sizeof(T);
-    __shared__ double sh[3][64][E];
-    const int x = threadIdx.x & 63, y = threadIdx.x >> 6;
-    const int v = blockIdx.x * 64 + x;
-    const bool on = v * E < cols;
-    const int r0 = blockIdx.y * kDsumChunk, r1 = min(rows, r0 + kDsumChunk);
-    double s[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) s[e] = 0.0;
-    if (on) {
-#pragma unroll 4
-        for (int r = r0 + y; r < r1; r += 4) {
-            const float4_t q = *reinterpret_cast<const float4_t*>(X + (int64_t)r * ld + (int64_t)v * E);
-            const T* xv = reinterpret_cast<const T*>(&q);
-#pragma unroll
-            for (int e = 0; e < E; ++e) s[e] += (double)xv[e];
-        }
-    }
-    if (y > 0) {
-#pragma unroll
-        for (int e = 0; e < E; ++e) sh[y - 1][x][e] = s[e];
-    }
-    __syncthreads();
-    if (y == 0 && on) {
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const double t = ((s[e] + sh[0][x][e]) + sh[1][x][e]) + sh[2][x][e];
-            part[(int64_t)blockIdx.y * cols + (int64_t)v * E + e] = t;
-        }
-    }
-}
-
-// 32 columns per workgroup, 8 groups of 32 threads each adding a contiguous
-// run of chunks in ascending order, then the 8 group sums in ascending order.
-__global__ void __launch_bounds__(256) dsum_cols_reduce_kernel(const double* __restrict__ part, int nchunks,
-                                                               int cols, double* __restrict__ out) {
-    __shared__ double sh[8][32];
-    const int c = threadIdx.x & 31, g = threadIdx.x >> 5;
-    const int col = blockIdx.x * 32 + c;
-    const int q = (nchunks + 7) / 8;
-    const int q0 = min(nchunks, g * q), q1 = min(nchunks, q0 + q);
-    double s = 0.0;
-    if (col < cols) {
-#pragma unroll 8
-        for (int k = q0; k < q1; ++k) s += part[(int64_t)k * cols + col];
-    }
-    sh[g][c] = s;
-    __syncthreads();
-    if (g == 0 && col < cols) {
-        double t = sh[0][c];
-        for (int k = 1; k < 8; ++k) t += sh[k][c];
-        out[col] = t;
-    }
-}
 
 // res[0] = sum_j cs[j], res[1] = sum_k sa[k] sb[k], res[2] = sum_j bias[j]
 // (bias may be null), by one workgroup with a fixed stride-1024 order and a
@@ -783,60 +707,192 @@ __global__ void __launch_bounds__(kFinThreads) checksum_finalize_kernel(const fl
     if (threadIdx.x < 3) res[threadIdx.x] = red[threadIdx.x][0];
 }
 
-template <typename T>
-__global__ void dsum_rows_kernel(const T* __restrict__ X, int64_t ld, int cols, double* __restrict__ out, int vec) {
-    __shared__ double red[kEwThreads];
-    constexpr int E = 16 / sizeof(T);
-    const T* row = X + (int64_t)blockIdx.x * ld;
-    double s = 0.0;
-    int c0 = 0;
-    if (vec) {  // 16-byte loads; the row start is 16-byte aligned
-        const int nv = cols / E;
-#pragma unroll 4
-        for (int v = threadIdx.x; v < nv; v += kEwThreads) {
-            const float4_t q = *reinterpret_cast<const float4_t*>(row + (int64_t)v * E);
-            const T* x = reinterpret_cast<const T*>(&q);
-            double t = 0.0;
-#pragma unroll
-            for (int e = 0; e < E; ++e) t += (double)x[e];
-            s += t;
-        }
-        c0 = nv * E;
-    }
-    for (int c = c0 + threadIdx.x; c < cols; c += kEwThreads) s += (double)row[c];
-    red[threadIdx.x] = s;
-    __syncthreads();
-    for (int w = kEwThreads / 2; w > 0; w >>= 1) {
-        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) out[blockIdx.x] = red[0];
-}
-
-// Doubles of scratch launch_dsum needs for a column sum of `rows` x `cols`.
+// Doubles of scratch the column partials need for a column sum of `rows` x `cols`.
 static size_t dsum_scratch(int rows, int cols, bool along_rows) {
     return along_rows ? (size_t)((rows + kDsumChunk - 1) / kDsumChunk) * cols : 0;
 }
 
+// The sums of both operands of the checked GEMM in two launches: a first
+// pass whose blocks [0, n0) run operand 0's work and the rest operand 1's,
+// then one pass adding the column partials of whichever operands have them.
+// Row sums: one row per block, 16-byte loads where rows are aligned, a fixed
+// stride-256 order and a fixed tree.  Column sums: part[q][c] over the rows
+// of chunk q (kDsumChunk rows; with 16-byte loads thread (x, y) sums columns
+// E (64 bx + x) .. + E - 1 over rows y, y + 4, ... and the four row groups
+// are added in ascending y), then the chunks in ascending q (8 groups of 32
+// threads each adding a contiguous run of chunks, then the 8 group sums in
+// ascending order).
+struct DsumJob {
+    const void* X;
+    int64_t ld;
+    int rows, cols;
+    int along_rows, vec;
+    double* out;
+    double* scratch;
+    int gx, nblocks;   // first pass: blocks along the columns (column partials), total blocks
+    int nchunks, nred;  // second pass: row chunks per column, blocks (0: no second pass)
+};
+
 template <typename T>
-static void launch_dsum(const T* X, int64_t ld, int rows, int cols, bool along_rows, double* out, double* scratch,
-                        hipStream_t s) {
+__device__ __forceinline__ void dsum_job_pass1(const DsumJob& j, int b) {
     constexpr int E = 16 / sizeof(T);
+    const T* X = static_cast<const T*>(j.X);
+    if (!j.along_rows) {  // row sums
+        __shared__ double red[kEwThreads];
+        const T* row = X + (int64_t)b * j.ld;
+        double s = 0.0;
+        int c0 = 0;
+        if (j.vec) {
+            const int nv = j.cols / E;
+#pragma unroll 4
+            for (int v = threadIdx.x; v < nv; v += kEwThreads) {
+                const float4_t q = *reinterpret_cast<const float4_t*>(row + (int64_t)v * E);
+                const T* x = reinterpret_cast<const T*>(&q);
+                double t = 0.0;
+#pragma unroll
+                for (int e = 0; e < E; ++e) t += (double)x[e];
+                s += t;
+            }
+            c0 = nv * E;
+        }
+        for (int c = c0 + threadIdx.x; c < j.cols; c += kEwThreads) s += (double)row[c];
+        red[threadIdx.x] = s;
+        __syncthreads();
+        for (int w = kEwThreads / 2; w > 0; w >>= 1) {
+            if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) j.out[b] = red[0];
+        return;
+    }
+    const int bx = b % j.gx, by = b / j.gx;
+    const int r0 = by * kDsumChunk, r1 = min(j.rows, r0 + kDsumChunk);
+    if (!j.vec) {  // column partials, one column per thread
+        const int c = bx * 256 + threadIdx.x;
+        if (c >= j.cols) return;
+        double s = 0.0;
+#pragma unroll 4
+        for (int r = r0; r < r1; ++r) s += (double)X[(int64_t)r * j.ld + c];
+        j.scratch[(int64_t)by * j.cols + c] = s;
+        return;
+    }
+    // column partials, E columns per thread
+    __shared__ double sh[3][64][E];
+    const int x = threadIdx.x & 63, y = threadIdx.x >> 6;
+    const int v = bx * 64 + x;
+    const bool on = v * E < j.cols;
+    double s[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) s[e] = 0.0;
+    if (on) {
+#pragma unroll 4
+        for (int r = r0 + y; r < r1; r += 4) {
+            const float4_t q = *reinterpret_cast<const float4_t*>(X + (int64_t)r * j.ld + (int64_t)v * E);
+            const T* xv = reinterpret_cast<const T*>(&q);
+#pragma unroll
+            for (int e = 0; e < E; ++e) s[e] += (double)xv[e];
+        }
+    }
+    if (y > 0) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) sh[y - 1][x][e] = s[e];
+    }
+    __syncthreads();
+    if (y == 0 && on) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const double t = ((s[e] + sh[0][x][e]) + sh[1][x][e]) + sh[2][x][e];
+            j.scratch[(int64_t)by * j.cols + (int64_t)v * E + e] = t;
+        }
+    }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) dsum_pair_pass1_kernel(DsumJob j0, DsumJob j1) {
+    const int b = blockIdx.x;
+    if (b < j0.nblocks)
+        dsum_job_pass1<T>(j0, b);
+    else
+        dsum_job_pass1<T>(j1, b - j0.nblocks);
+}
+
+// The chunks of the column partials, for the blocks of both jobs.
+__global__ void __launch_bounds__(256) dsum_pair_pass2_kernel(DsumJob j0, DsumJob j1) {
+    __shared__ double sh[8][32];
+    const bool first = (int)blockIdx.x < j0.nred;
+    const DsumJob& j = first ? j0 : j1;
+    const int blk = first ? blockIdx.x : blockIdx.x - j0.nred;
+    const int c = threadIdx.x & 31, g = threadIdx.x >> 5;
+    const int col = blk * 32 + c;
+    const int q = (j.nchunks + 7) / 8;
+    const int q0 = min(j.nchunks, g * q), q1 = min(j.nchunks, q0 + q);
+    double s = 0.0;
+    if (col < j.cols) {
+#pragma unroll 8
+        for (int k = q0; k < q1; ++k) s += j.scratch[(int64_t)k * j.cols + col];
+    }
+    sh[g][c] = s;
+    __syncthreads();
+    if (g == 0 && col < j.cols) {
+        double t = sh[0][c];
+        for (int k = 1; k < 8; ++k) t += sh[k][c];
+        j.out[col] = t;
+    }
+}
+
+template <typename T>
+static DsumJob dsum_job(const T* X, int64_t ld, int rows, int cols, bool along_rows, double* out, double* scratch) {
+    constexpr int E = 16 / sizeof(T);
+    DsumJob j{};
+    j.X = X;
+    j.ld = ld;
+    j.rows = rows;
+    j.cols = cols;
+    j.along_rows = along_rows ? 1 : 0;
+    j.out = out;
+    j.scratch = scratch;
     const bool vec = aligned16(X) && ld % E == 0;  // every row starts 16-byte aligned
     if (along_rows) {
-        const int nq = (rows + kDsumChunk - 1) / kDsumChunk;
-        if (vec && cols % E == 0)
-            hipLaunchKernelGGL(dsum_cols_partial_vec_kernel<T>, dim3((unsigned)((cols / E + 63) / 64), (unsigned)nq),
-                               dim3(256), 0, s, X, ld, rows, cols, scratch);
-        else
-            hipLaunchKernelGGL(dsum_cols_partial_kernel<T>, dim3((unsigned)((cols + 255) / 256), (unsigned)nq),
-                               dim3(256), 0, s, X, ld, rows, cols, scratch);
-        hipLaunchKernelGGL(dsum_cols_reduce_kernel, dim3((unsigned)((cols + 31) / 32)), dim3(256), 0, s, scratch,
-                           nq, cols, out);
+        j.vec = vec && cols % E == 0;
+        j.nchunks = (rows + kDsumChunk - 1) / kDsumChunk;
+        j.gx = j.vec ? (cols / E + 63) / 64 : (cols + 255) / 256;
+        j.nblocks = j.gx * j.nchunks;
+        j.nred = (cols + 31) / 32;
     } else {
-        hipLaunchKernelGGL(dsum_rows_kernel<T>, dim3((unsigned)rows), dim3(kEwThreads), 0, s, X, ld, cols, out,
-                           vec ? 1 : 0);
+        j.vec = vec ? 1 : 0;
+        j.gx = 1;
+        j.nblocks = rows;
+        j.nchunks = 0;
+        j.nred = 0;
     }
+    return j;
+}
+
+template <typename T>
+static void launch_dsum_pair(const DsumJob& j0, const DsumJob& j1, hipStream_t s) {
+    hipLaunchKernelGGL(dsum_pair_pass1_kernel<T>, dim3((unsigned)(j0.nblocks + j1.nblocks)), dim3(256), 0, s, j0,
+                       j1);
+    if (j0.nred + j1.nred > 0)
+        hipLaunchKernelGGL(dsum_pair_pass2_kernel, dim3((unsigned)(j0.nred + j1.nred)), dim3(256), 0, s, j0, j1);
+}
+
+// A pinned, device-visible slot per host thread for the few doubles a
+// synchronous check returns: the last kernel writes them straight into host
+// memory, so no device-to-host copy (a staging kernel and a handshake) is
+// needed.  Allocated on the thread's first call and kept for the process.
+static double* result_slot(double** dev, hipError_t& e) {
+    static thread_local double* slot = nullptr;
+    e = hipSuccess;
+    if (!slot) {
+        void* p = nullptr;
+        e = hipHostMalloc(&p, 64, hipHostMallocPortable | hipHostMallocMapped);
+        if (e != hipSuccess) return nullptr;
+        slot = static_cast<double*>(p);
+    }
+    void* d = nullptr;
+    e = hipHostGetDevicePointer(&d, slot, 0);
+    *dev = static_cast<double*>(d);
+    return e == hipSuccess ? slot : nullptr;
 }
 
 }  // namespace
@@ -947,9 +1003,9 @@ extern "C" int vedic_gemm_checked(const vedic_gemm_desc_t* d, float tolerance, v
     const int ar = a_rows ? M : K, ac = a_rows ? K : M;
     const int br = b_rows ? N : K, bc = b_rows ? K : N;
     // workspace: colsum(C) [N] fp32 (padded to 8 bytes) | sa [K] | sb [K] |
-    // scratch of the column sums | 3 result doubles
+    // scratch of the column sums
     const size_t fbytes = (sizeof(float) * (size_t)N + 7) / 8 * 8;
-    const size_t bytes = fbytes + sizeof(double) * ((size_t)K * 2 + 3);
+    const size_t bytes = fbytes + sizeof(double) * (size_t)K * 2;
     const size_t scr_a = dsum_scratch(ar, ac, a_rows), scr_b = dsum_scratch(br, bc, b_rows);
     char* ws = nullptr;
     hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), bytes + sizeof(double) * (scr_a + scr_b), s);
@@ -966,20 +1022,26 @@ extern "C" int vedic_gemm_checked(const vedic_gemm_desc_t* d, float tolerance, v
     if (st == VEDIC_STATUS_OK) {
         // sa[k] = sum_m op(A)[m][k]; sb[k] = sum_n op(B)[k][n]
         if (d->in_dtype == VEDIC_DT_F16) {
-            launch_dsum(static_cast<const _Float16*>(d->A), d->lda, ar, ac, a_rows, d_sa, d_scr_a, s);
-            launch_dsum(static_cast<const _Float16*>(d->B), d->ldb, br, bc, b_rows, d_sb, d_scr_b, s);
+            const auto* A = static_cast<const _Float16*>(d->A);
+            const auto* B = static_cast<const _Float16*>(d->B);
+            launch_dsum_pair<_Float16>(dsum_job(A, d->lda, ar, ac, a_rows, d_sa, d_scr_a),
+                                       dsum_job(B, d->ldb, br, bc, b_rows, d_sb, d_scr_b), s);
         } else {
-            launch_dsum(static_cast<const float*>(d->A), d->lda, ar, ac, a_rows, d_sa, d_scr_a, s);
-            launch_dsum(static_cast<const float*>(d->B), d->ldb, br, bc, b_rows, d_sb, d_scr_b, s);
+            const auto* A = static_cast<const float*>(d->A);
+            const auto* B = static_cast<const float*>(d->B);
+            launch_dsum_pair<float>(dsum_job(A, d->lda, ar, ac, a_rows, d_sa, d_scr_a),
+                                    dsum_job(B, d->ldb, br, bc, b_rows, d_sb, d_scr_b), s);
         }
-        double* d_res = d_scr_b + scr_b;  // 3 doubles
-        hipLaunchKernelGGL(checksum_finalize_kernel, dim3(1), dim3(kFinThreads), 0, s, d_cs, N, d_sa, d_sb, K,
-                           want_bias ? d->bias : nullptr, d_res);
-        e = hipGetLastError();
-        double host[3] = {0.0, 0.0, 0.0};
-        if (e == hipSuccess) e = hipMemcpyAsync(host, d_res, sizeof(host), hipMemcpyDeviceToHost, s);
+        double* res_dev = nullptr;
+        const double* const res = result_slot(&res_dev, e);  // 3 doubles, written by the finalize kernel
+        if (e == hipSuccess) {
+            hipLaunchKernelGGL(checksum_finalize_kernel, dim3(1), dim3(kFinThreads), 0, s, d_cs, N, d_sa, d_sb, K,
+                               want_bias ? d->bias : nullptr, res_dev);
+            e = hipGetLastError();
+        }
         if (e == hipSuccess) e = hipStreamSynchronize(s);
         if (e == hipSuccess) {
+            const double host[3] = {res[0], res[1], res[2]};
             const double pred = (double)d->alpha * host[1] + (double)M * host[2];
             out->checksum_C = (float)host[0];
             out->checksum_vedic = (float)pred;
