@@ -244,7 +244,9 @@ int vedic_verify(const float* A, const float* B, const float* C, int M, int K, i
  * so C is not read again, against colsum(op(A)) . rowsum(op(B)) (times alpha,
  * plus M * sum(bias) with VEDIC_EPI_BIAS) from one pass over A and B, in
  * double.  Any op and input dtype; fp32 C; epilogue NONE or BIAS; beta = 0;
- * desc->colsum must be NULL.  Synchronous, like vedic_verify.  New: the
+ * desc->colsum must be NULL.  Synchronous, like vedic_verify.  The result
+ * doubles land in a 64-byte pinned host slot allocated on a host thread's
+ * first call and kept for the process (one per thread).  New: the
  * reference verifies with a separate pass over C at checkpoints
  * (cuda/train_gpu.cu:1695-1719). */
 int vedic_gemm_checked(const vedic_gemm_desc_t* desc, float tolerance, vedic_verify_result_t* out);
