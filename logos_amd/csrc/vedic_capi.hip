@@ -109,11 +109,11 @@ __global__ void colsum_partial_kernel(const float* __restrict__ X, int64_t ldx, 
 // 32 threads: group g adds blocks [g q, (g + 1) q) in ascending order
 // (q = ceil(nblocks / 8); each step reads 128 contiguous bytes), and the 8
 // group sums are added in ascending g.
-__global__ void __launch_bounds__(256) colsum_reduce_kernel(const float* __restrict__ part, int nblocks, int N,
-                                                            float* __restrict__ out, float beta) {
+__device__ __forceinline__ void colsum_reduce_block(const float* __restrict__ part, int nblocks, int N,
+                                                    float* __restrict__ out, float beta, int blk) {
     __shared__ float sh[8][32];
     const int c = threadIdx.x & 31, g = threadIdx.x >> 5;
-    const int j = blockIdx.x * 32 + c;
+    const int j = blk * 32 + c;
     const int q = (nblocks + 7) / 8;
     const int b0 = min(nblocks, g * q), b1 = min(nblocks, b0 + q);
     float acc = 0.0f;
@@ -129,6 +129,11 @@ __global__ void __launch_bounds__(256) colsum_reduce_kernel(const float* __restr
         for (int k = 1; k < 8; ++k) t += sh[k][c];
         out[j] = beta == 0.0f ? t : beta * out[j] + t;
     }
+}
+
+__global__ void __launch_bounds__(256) colsum_reduce_kernel(const float* __restrict__ part, int nblocks, int N,
+                                                            float* __restrict__ out, float beta) {
+    colsum_reduce_block(part, nblocks, N, out, beta, blockIdx.x);
 }
 
 static hipError_t launch_colsum_reduce(const float* part, int nblocks, int N, float* out, float beta,
@@ -273,7 +278,16 @@ static hipError_t launch_split(bool f16, int op, bool vec, const GemmArgs& a, in
 
 // The GEMM; with nheads > 0 the columns of C are scattered to heads[0..nheads)
 // (each [M x head_cols], row-major) instead of written to d->C.
-static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads, int head_cols) {
+// Column partials handed to the caller instead of reduced here (the checked
+// GEMM reduces them in its own pass); part stays null when the product
+// produced no partials, and the caller then owns nothing.
+struct ColsumHandoff {
+    float* part;
+    int blocks;
+};
+
+static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads, int head_cols,
+                     ColsumHandoff* handoff = nullptr) {
     if (!d) return VEDIC_STATUS_NULL_POINTER;
     if (d->M <= 0 || d->N <= 0 || d->K <= 0) return VEDIC_STATUS_BAD_DIM;
     const bool scatter = nheads > 0;
@@ -392,6 +406,11 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
         e = launch_f32_tiled(d->op, vec, a, s);
     }
 
+    if (handoff && cs_part && e == hipSuccess) {  // the caller reduces and frees the partials
+        handoff->part = cs_part;
+        handoff->blocks = cs_blocks;
+        return VEDIC_STATUS_OK;
+    }
     if (d->colsum && e == hipSuccess) {
         if (cs_part)
             e = launch_colsum_reduce(cs_part, cs_blocks, d->N, d->colsum, d->colsum_beta, s);
@@ -816,8 +835,14 @@ __global__ void __launch_bounds__(256) dsum_pair_pass1_kernel(DsumJob j0, DsumJo
         dsum_job_pass1<T>(j1, b - j0.nblocks);
 }
 
-// The chunks of the column partials, for the blocks of both jobs.
-__global__ void __launch_bounds__(256) dsum_pair_pass2_kernel(DsumJob j0, DsumJob j1) {
+// The chunks of the column partials, for the blocks of both jobs; blocks past
+// those reduce the GEMM's column partials of C (cs_part, cs_blocks) into cs.
+__global__ void __launch_bounds__(256) dsum_pair_pass2_kernel(DsumJob j0, DsumJob j1, const float* cs_part,
+                                                              int cs_blocks, int N, float* cs) {
+    if ((int)blockIdx.x >= j0.nred + j1.nred) {
+        colsum_reduce_block(cs_part, cs_blocks, N, cs, 0.0f, blockIdx.x - j0.nred - j1.nred);
+        return;
+    }
     __shared__ double sh[8][32];
     const bool first = (int)blockIdx.x < j0.nred;
     const DsumJob& j = first ? j0 : j1;
@@ -868,12 +893,17 @@ static DsumJob dsum_job(const T* X, int64_t ld, int rows, int cols, bool along_r
     return j;
 }
 
+// ho.part: the GEMM's column partials of C, reduced into cs in the second
+// pass (null: cs already holds the column sums).
 template <typename T>
-static void launch_dsum_pair(const DsumJob& j0, const DsumJob& j1, hipStream_t s) {
+static void launch_dsum_pair(const DsumJob& j0, const DsumJob& j1, const ColsumHandoff& ho, int N, float* cs,
+                             hipStream_t s) {
     hipLaunchKernelGGL(dsum_pair_pass1_kernel<T>, dim3((unsigned)(j0.nblocks + j1.nblocks)), dim3(256), 0, s, j0,
                        j1);
-    if (j0.nred + j1.nred > 0)
-        hipLaunchKernelGGL(dsum_pair_pass2_kernel, dim3((unsigned)(j0.nred + j1.nred)), dim3(256), 0, s, j0, j1);
+    const int ncs = ho.part ? (N + 31) / 32 : 0;
+    if (j0.nred + j1.nred + ncs > 0)
+        hipLaunchKernelGGL(dsum_pair_pass2_kernel, dim3((unsigned)(j0.nred + j1.nred + ncs)), dim3(256), 0, s, j0,
+                           j1, ho.part, ho.blocks, N, cs);
 }
 
 // A pinned, device-visible slot per host thread for the few doubles a
@@ -1018,19 +1048,20 @@ extern "C" int vedic_gemm_checked(const vedic_gemm_desc_t* d, float tolerance, v
     vedic_gemm_desc_t g = *d;
     g.colsum = d_cs;
     g.colsum_beta = 0.0f;
-    int st = vedic_gemm(&g);
+    ColsumHandoff ho{nullptr, 0};
+    int st = gemm_impl(&g, nullptr, 0, 0, &ho);
     if (st == VEDIC_STATUS_OK) {
         // sa[k] = sum_m op(A)[m][k]; sb[k] = sum_n op(B)[k][n]
         if (d->in_dtype == VEDIC_DT_F16) {
             const auto* A = static_cast<const _Float16*>(d->A);
             const auto* B = static_cast<const _Float16*>(d->B);
             launch_dsum_pair<_Float16>(dsum_job(A, d->lda, ar, ac, a_rows, d_sa, d_scr_a),
-                                       dsum_job(B, d->ldb, br, bc, b_rows, d_sb, d_scr_b), s);
+                                       dsum_job(B, d->ldb, br, bc, b_rows, d_sb, d_scr_b), ho, N, d_cs, s);
         } else {
             const auto* A = static_cast<const float*>(d->A);
             const auto* B = static_cast<const float*>(d->B);
             launch_dsum_pair<float>(dsum_job(A, d->lda, ar, ac, a_rows, d_sa, d_scr_a),
-                                    dsum_job(B, d->ldb, br, bc, b_rows, d_sb, d_scr_b), s);
+                                    dsum_job(B, d->ldb, br, bc, b_rows, d_sb, d_scr_b), ho, N, d_cs, s);
         }
         double* res_dev = nullptr;
         const double* const res = result_slot(&res_dev, e);  // 3 doubles, written by the finalize kernel
@@ -1050,6 +1081,10 @@ extern "C" int vedic_gemm_checked(const vedic_gemm_desc_t* d, float tolerance, v
             out->pass = out->relative_error < tolerance;
         }
         st = hip_status(e);
+    }
+    if (ho.part) {
+        const hipError_t f = hipFreeAsync(ho.part, s);
+        if (st == VEDIC_STATUS_OK && f != hipSuccess) st = hip_status(f);
     }
     const hipError_t f = hipFreeAsync(ws, s);
     if (st == VEDIC_STATUS_OK && f != hipSuccess) st = hip_status(f);
