@@ -203,13 +203,17 @@ def test_bias_grad(shape, beta):
 
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 @pytest.mark.parametrize("opname,layout", [("NN", 0), ("NT", 1), ("TN", 2)])
-def test_gemm_checked_sums(dtype, opname, layout):
+@pytest.mark.parametrize("shape", [(300, 264, 520), (97, 45, 133), (256, 256, 4096)])
+def test_gemm_checked_sums(dtype, opname, layout, shape):
     """The checked GEMM: C identical to the plain call; checksum_C the sum of
     the returned C (fp32 column sums, added in double); checksum_vedic the
-    prediction colsum(op(A)) . rowsum(op(B)) + M sum(bias), in double."""
+    prediction colsum(op(A)) . rowsum(op(B)) + M sum(bias), in double.
+    Shapes: aligned tiles (C's column partials from the GEMM's epilogue),
+    odd extents (unaligned rows: the element-wise kernels and scalar operand
+    sums), and few tiles over a long K (split K)."""
     vedic = V()
-    M, N, K = 300, 264, 520
-    rng = np.random.default_rng(zlib.crc32(f"checked-{dtype}-{opname}".encode()))
+    M, N, K = shape
+    rng = np.random.default_rng(zlib.crc32(f"checked-{dtype}-{opname}-{shape}".encode()))
     a_shape = (K, M) if layout == 2 else (M, K)
     b_shape = (N, K) if layout == 1 else (K, N)
     A = normal(rng, a_shape, absval=True)
