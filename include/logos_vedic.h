@@ -311,6 +311,19 @@ int vedic_flash_attention_bwd_heads(const float* const* Q, const float* const* K
                                     int dh, float scale, int causal, int shunyam, int window, int stride,
                                     void* stream);
 
+/* ---- test hooks --------------------------------------------------------- */
+
+/* Off by default.  When on, every GEMM with column sums allocates its
+ * per-32-row-block partial-sum workspace with a guard band of 8 block rows
+ * past its end, filled with a marker; after the GEMM the call checks the band
+ * (synchronously) and adds the number of overwritten words to a
+ * process-wide counter.  New: no counterpart in the reference; for the
+ * regression tests of the workspace bound on partial last tiles. */
+void vedic_debug_set_workspace_guard(int on);
+
+/* Overwritten guard words seen since the process started. */
+long vedic_debug_workspace_guard_hits(void);
+
 /* ---- backend queries --------------------------------------------------- */
 
 /* Always 0: no vendor BLAS is linked.

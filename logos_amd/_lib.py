@@ -112,6 +112,8 @@ SIGNATURES = {
         c_int, [c_vp] * 9 + [c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_vp]),
     "vedic_flash_attention_bwd_heads": (
         c_int, [ctypes.POINTER(c_vp)] * 9 + [c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_vp]),
+    "vedic_debug_set_workspace_guard": (None, [c_int]),
+    "vedic_debug_workspace_guard_hits": (ctypes.c_long, []),
     "vedic_uses_vendor_blas": (c_int, []),
     "vedic_backend_name": (c_char_p, []),
     "vedic_status_string": (c_char_p, [c_int]),

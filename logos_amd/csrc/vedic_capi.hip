@@ -276,6 +276,29 @@ static hipError_t launch_split(bool f16, int op, bool vec, const GemmArgs& a, in
 
 // ------------------------------------------------------------------ GEMM
 
+// Test hook (off by default): the column-partial workspace is allocated with
+// kGuardRows block rows past its end, filled with kGuardWord; after the GEMM
+// a check kernel counts guard words that changed, and the call waits for it.
+// A write past the ceil(M / 32) block rows the workspace is sized for shows
+// up as a count instead of silently landing in a neighbouring allocation.
+static std::atomic<int> g_ws_guard{0};
+static std::atomic<long> g_ws_guard_hits{0};
+static constexpr int kGuardRows = 8;  // a 256-row tile has 8 blocks of 32 rows
+static constexpr uint32_t kGuardWord = 0x7FC0DEADu;
+
+// g[0, n) = kGuardWord, g[n] (the hit counter) = 0
+__global__ void guard_fill_kernel(uint32_t* __restrict__ g, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i <= n; i += (int64_t)gridDim.x * blockDim.x)
+        g[i] = i < n ? kGuardWord : 0u;
+}
+
+__global__ void guard_check_kernel(const uint32_t* __restrict__ g, int64_t n, unsigned* __restrict__ hits) {
+    unsigned c = 0;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        c += g[i] != kGuardWord;
+    if (c) atomicAdd(hits, c);
+}
+
 // The GEMM; with nheads > 0 the columns of C are scattered to heads[0..nheads)
 // (each [M x head_cols], row-major) instead of written to d->C.
 // Column partials handed to the caller instead of reduced here (the checked
@@ -380,10 +403,23 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
     // finished C instead.
     float* cs_part = nullptr;
     const int cs_blocks = (d->M + 31) / 32;
+    const bool guard = g_ws_guard.load(std::memory_order_relaxed) != 0;
+    const int64_t guard_n = (int64_t)kGuardRows * d->N;  // guard words past the partials
     if (d->colsum && ks == 1) {
-        e = hipMallocAsync(reinterpret_cast<void**>(&cs_part), sizeof(float) * (size_t)cs_blocks * d->N, s);
+        // with the guard: partials | guard rows | one hit counter
+        const size_t bytes = sizeof(float) * (size_t)cs_blocks * d->N + (guard ? 4 * (size_t)guard_n + 4 : 0);
+        e = hipMallocAsync(reinterpret_cast<void**>(&cs_part), bytes, s);
         if (e != hipSuccess) return hip_status(e);
         a.cs_part = cs_part;
+        if (guard) {
+            uint32_t* g = reinterpret_cast<uint32_t*>(cs_part + (size_t)cs_blocks * d->N);
+            hipLaunchKernelGGL(guard_fill_kernel, dim3(64), dim3(256), 0, s, g, guard_n);
+            e = hipGetLastError();
+            if (e != hipSuccess) {
+                (void)hipFreeAsync(cs_part, s);
+                return hip_status(e);
+            }
+        }
     }
 
     if (skinny) {
@@ -406,6 +442,15 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
         e = launch_f32_tiled(d->op, vec, a, s);
     }
 
+    if (guard && cs_part && e == hipSuccess) {
+        uint32_t* g = reinterpret_cast<uint32_t*>(cs_part + (size_t)cs_blocks * d->N);
+        unsigned hits = 0;
+        hipLaunchKernelGGL(guard_check_kernel, dim3(64), dim3(256), 0, s, g, guard_n, g + guard_n);
+        e = hipGetLastError();
+        if (e == hipSuccess) e = hipMemcpyAsync(&hits, g + guard_n, 4, hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e == hipSuccess) g_ws_guard_hits.fetch_add(hits);
+    }
     if (handoff && cs_part && e == hipSuccess) {  // the caller reduces and frees the partials
         handoff->part = cs_part;
         handoff->blocks = cs_blocks;
@@ -425,6 +470,10 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
 }
 
 extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) { return gemm_impl(d, nullptr, 0, 0); }
+
+extern "C" void vedic_debug_set_workspace_guard(int on) { g_ws_guard.store(on ? 1 : 0); }
+
+extern "C" long vedic_debug_workspace_guard_hits(void) { return g_ws_guard_hits.load(); }
 
 extern "C" int vedic_gemm_scatter(const vedic_gemm_desc_t* d, float* const* heads, int nheads, int head_cols) {
     if (nheads <= 0) return VEDIC_STATUS_BAD_DIM;
@@ -896,33 +945,47 @@ static DsumJob dsum_job(const T* X, int64_t ld, int rows, int cols, bool along_r
 // ho.part: the GEMM's column partials of C, reduced into cs in the second
 // pass (null: cs already holds the column sums).
 template <typename T>
-static void launch_dsum_pair(const DsumJob& j0, const DsumJob& j1, const ColsumHandoff& ho, int N, float* cs,
-                             hipStream_t s) {
+static hipError_t launch_dsum_pair(const DsumJob& j0, const DsumJob& j1, const ColsumHandoff& ho, int N, float* cs,
+                                   hipStream_t s) {
     hipLaunchKernelGGL(dsum_pair_pass1_kernel<T>, dim3((unsigned)(j0.nblocks + j1.nblocks)), dim3(256), 0, s, j0,
                        j1);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
     const int ncs = ho.part ? (N + 31) / 32 : 0;
-    if (j0.nred + j1.nred + ncs > 0)
+    if (j0.nred + j1.nred + ncs > 0) {
         hipLaunchKernelGGL(dsum_pair_pass2_kernel, dim3((unsigned)(j0.nred + j1.nred + ncs)), dim3(256), 0, s, j0,
                            j1, ho.part, ho.blocks, N, cs);
+        e = hipGetLastError();
+    }
+    return e;
 }
 
 // A pinned, device-visible slot per host thread for the few doubles a
 // synchronous check returns: the last kernel writes them straight into host
 // memory, so no device-to-host copy (a staging kernel and a handshake) is
 // needed.  Allocated on the thread's first call and kept for the process.
+// The holder frees the slot when its thread ends (thread pools and worker
+// threads do not accumulate pinned mappings).
+struct PinnedSlot {
+    double* p = nullptr;
+    ~PinnedSlot() {
+        if (p) (void)hipHostFree(p);
+    }
+};
+
 static double* result_slot(double** dev, hipError_t& e) {
-    static thread_local double* slot = nullptr;
+    static thread_local PinnedSlot slot;
     e = hipSuccess;
-    if (!slot) {
+    if (!slot.p) {
         void* p = nullptr;
         e = hipHostMalloc(&p, 64, hipHostMallocPortable | hipHostMallocMapped);
         if (e != hipSuccess) return nullptr;
-        slot = static_cast<double*>(p);
+        slot.p = static_cast<double*>(p);
     }
     void* d = nullptr;
-    e = hipHostGetDevicePointer(&d, slot, 0);
+    e = hipHostGetDevicePointer(&d, slot.p, 0);
     *dev = static_cast<double*>(d);
-    return e == hipSuccess ? slot : nullptr;
+    return e == hipSuccess ? slot.p : nullptr;
 }
 
 }  // namespace
@@ -1055,16 +1118,17 @@ extern "C" int vedic_gemm_checked(const vedic_gemm_desc_t* d, float tolerance, v
         if (d->in_dtype == VEDIC_DT_F16) {
             const auto* A = static_cast<const _Float16*>(d->A);
             const auto* B = static_cast<const _Float16*>(d->B);
-            launch_dsum_pair<_Float16>(dsum_job(A, d->lda, ar, ac, a_rows, d_sa, d_scr_a),
-                                       dsum_job(B, d->ldb, br, bc, b_rows, d_sb, d_scr_b), ho, N, d_cs, s);
+            e = launch_dsum_pair<_Float16>(dsum_job(A, d->lda, ar, ac, a_rows, d_sa, d_scr_a),
+                                           dsum_job(B, d->ldb, br, bc, b_rows, d_sb, d_scr_b), ho, N, d_cs, s);
         } else {
             const auto* A = static_cast<const float*>(d->A);
             const auto* B = static_cast<const float*>(d->B);
-            launch_dsum_pair<float>(dsum_job(A, d->lda, ar, ac, a_rows, d_sa, d_scr_a),
-                                    dsum_job(B, d->ldb, br, bc, b_rows, d_sb, d_scr_b), ho, N, d_cs, s);
+            e = launch_dsum_pair<float>(dsum_job(A, d->lda, ar, ac, a_rows, d_sa, d_scr_a),
+                                        dsum_job(B, d->ldb, br, bc, b_rows, d_sb, d_scr_b), ho, N, d_cs, s);
         }
         double* res_dev = nullptr;
-        const double* const res = result_slot(&res_dev, e);  // 3 doubles, written by the finalize kernel
+        const double* res = nullptr;  // 3 doubles, written by the finalize kernel
+        if (e == hipSuccess) res = result_slot(&res_dev, e);
         if (e == hipSuccess) {
             hipLaunchKernelGGL(checksum_finalize_kernel, dim3(1), dim3(kFinThreads), 0, s, d_cs, N, d_sa, d_sb, K,
                                want_bias ? d->bias : nullptr, res_dev);

@@ -221,7 +221,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, void* Cp, const floa
         }
         if (colsum) {
             csum += __shfl_xor(csum, 32);
-            if (h == 0 && col_ok) a.cs_part[(int64_t)((row0 >> 5) + i) * a.N + col] = csum;
+            // cs_part holds ceil(M / 32) block rows: a block that starts at
+            // or past M (the lower blocks of a last, partial tile) has none
+            if (h == 0 && col_ok && row0 + 32 * i < a.M) a.cs_part[(int64_t)((row0 >> 5) + i) * a.N + col] = csum;
         }
         if constexpr (READS) {
 #pragma unroll
