@@ -45,14 +45,23 @@ HBM_PEAK_GBS = 8000.0                   # MI355X HBM3E, GB/s (published)
 
 # One GEMM: (M, K, N, op, dtype, epilogue, beta).  op as stored:
 #   NN A[MxK] B[KxN]; NT A[MxK] B[NxK]; TN A[KxM] B[KxN].
-def _g(M, K, N, op="NN", dtype="fp16", epi="none", beta=0.0, checked=False, heads=0, alpha=1.0):
-    return dict(M=M, K=K, N=N, op=op, dtype=dtype, epi=epi, beta=beta, checked=checked, heads=heads, alpha=alpha)
+#   dtype "amp": A fp32, converted to binary16 inside the GEMM (the AMP path from
+#   an fp32 activation); cast_a: an fp32 A cast into a binary16 buffer by a
+#   separate launch before the fp16 GEMM, every step (the reference's amp_gemm).
+def _g(M, K, N, op="NN", dtype="fp16", epi="none", beta=0.0, checked=False, heads=0, alpha=1.0, cast_a=False):
+    return dict(M=M, K=K, N=N, op=op, dtype=dtype, epi=epi, beta=beta, checked=checked, heads=heads, alpha=alpha,
+                cast_a=cast_a)
 
 
 # BASELINE.json configs; each workload is a list of GEMMs run back to back per step.
 WORKLOADS = {
     "fp32_nn_512x1024x1024": dict(cfg=1, gemms=[_g(512, 1024, 1024, dtype="fp32")]),
     "ffn_up_fp16_bias_gelu": dict(cfg=2, gemms=[_g(8192, 1024, 4096, epi="bias_gelu")]),
+    # the FFN-up from the fp32 activation: converted inside the GEMM, against the
+    # reference's per-call cast into a binary16 buffer followed by the fp16 GEMM
+    # (cuda/ModelGPU.cu:840-856)
+    "ffn_up_amp_fp32_act": dict(cfg=2, gemms=[_g(8192, 1024, 4096, dtype="amp", epi="bias_gelu")]),
+    "ffn_up_cast_then_fp16": dict(cfg=2, gemms=[_g(8192, 1024, 4096, epi="bias_gelu", cast_a=True)]),
     "ffn_down_dx_nt_fp16": dict(cfg=3, gemms=[_g(8192, 1024, 4096, op="NT")]),
     "ffn_down_dw_tn_fp16": dict(cfg=3, gemms=[_g(4096, 8192, 1024, op="TN", beta=1.0)]),
     # FFN backward through the activation, fused: dH = (dY . W2^T) * gelu'(H)
@@ -110,8 +119,11 @@ COPY_WORKLOAD = "copy_256mib"  # calibration for the FETCH_SIZE / WRITE_SIZE cou
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    # The GPU's shader clock ramps over the first ~10 ms of sustained work
+    # (a 20-step warmup of the headline measured 86 us per step, 200 or more
+    # 75-77 us): the default warmup runs the kernel for ~40 ms first.
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--workload", default="ffn_up_fp16_bias_gelu", choices=sorted(WORKLOADS) + [COPY_WORKLOAD])
     ap.add_argument("--all", action="store_true", help="every workload, one JSON line each")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -145,7 +157,7 @@ def summarize_traffic(args):
     fetch_dir, write_dir, cfetch_dir, cwrite_dir = args.summarize_traffic
     w = WORKLOADS[args.workload]
     kern = ("flash_attn_kernel" if "attn" in w
-            else "gemm_f16_kernel" if w["gemms"][0]["dtype"] == "fp16" else "gemm_f32_kernel")
+            else "gemm_f32_kernel" if w["gemms"][0]["dtype"] == "fp32" else "gemm_f16_kernel")
     fetch, nf = _pmc_kib(fetch_dir, "FETCH_SIZE", kern)
     write, nw = _pmc_kib(write_dir, "WRITE_SIZE", kern)
     # torch's copy_ of 256 MiB (the runtime's copyBuffer blit) reads and writes exactly 256 MiB
@@ -267,7 +279,7 @@ def cpu_baseline(w: dict, seconds: float, seed: int = 7):
         A = rng.standard_normal((rows, K), dtype=np.float32)
         B = (rng.standard_normal((K, N), dtype=np.float32) * np.float32(0.02))
         bias = (rng.standard_normal(N, dtype=np.float32) * np.float32(0.01))
-        if g["dtype"] == "fp16":
+        if g["dtype"] in ("fp16", "amp"):
             A, B = o.f16_round(A), o.f16_round(B)
         Hs = (rng.standard_normal((rows, N), dtype=np.float32) * np.float32(2.0)) if g["epi"] == "gelu_bwd" else None
         if op == "NT":
@@ -340,8 +352,15 @@ def make_step(w: dict, dev, torch):
         A = torch.randn(a_shape, generator=gen, device=dev)
         B = torch.randn(b_shape, generator=gen, device=dev) * 0.02
         bias = torch.randn((N,), generator=gen, device=dev) * 0.01
+        A32 = None
         if g["dtype"] == "fp16":
+            if g["cast_a"]:
+                A32 = A
             A, B = A.half(), B.half()
+        elif g["dtype"] == "amp":
+            B = B.half()
+        g["_cast"] = (A32, A) if A32 is not None else None
+        keep.append(A32)
         C = torch.randn((M, N), generator=gen, device=dev) * 1e-3 if g["beta"] else torch.empty((M, N), device=dev)
         keep += [A, B, bias, C]
         epi = {"none": _lib.EPI_NONE, "bias": _lib.EPI_BIAS, "bias_gelu": _lib.EPI_BIAS_GELU,
@@ -352,14 +371,18 @@ def make_step(w: dict, dev, torch):
         keep += [H, db]
         d = _lib.GemmDesc(
             op={"NN": _lib.OP_NN, "NT": _lib.OP_NT, "TN": _lib.OP_TN}[op],
-            in_dtype=_lib.DT_F16 if g["dtype"] == "fp16" else _lib.DT_F32, out_dtype=_lib.DT_F32,
+            in_dtype={"fp16": _lib.DT_F16, "fp32": _lib.DT_F32, "amp": _lib.DT_F32_F16}[g["dtype"]],
+            out_dtype=_lib.DT_F32,
             M=M, N=N, K=K, A=A.data_ptr(), lda=A.shape[1], B=B.data_ptr(), ldb=B.shape[1],
             C=C.data_ptr(), ldc=N, alpha=g["alpha"], beta=g["beta"],
             bias=bias.data_ptr() if g["epi"] in ("bias", "bias_gelu") else None, epilogue=epi,
             preact=H.data_ptr() if gbwd else None, ld_preact=N if gbwd else 0, stream=stream.cuda_stream,
             colsum=db.data_ptr() if gbwd else None, colsum_beta=1.0)
         es = 2 if g["dtype"] == "fp16" else 4
-        hbm = (M * K + K * N) * es + M * N * 4 * (2 if g["beta"] else 1) + (N * 4 if g["epi"] != "none" else 0)
+        es_b = 4 if g["dtype"] == "fp32" else 2
+        hbm = M * K * es + K * N * es_b + M * N * 4 * (2 if g["beta"] else 1) + (N * 4 if g["epi"] != "none" else 0)
+        if g["cast_a"]:
+            hbm += M * K * 6  # the cast pass: fp32 read, binary16 written
         if gbwd:
             hbm += M * N * 4 + N * 4  # H read, db read and written
         if g["checked"]:
@@ -377,9 +400,17 @@ def make_step(w: dict, dev, torch):
     gemm = lib.vedic_gemm
     vres = _lib.VerifyResult()
 
+    cast = lib.vedic_cast_f32_to_f16
+    sp = stream.cuda_stream
+
     def step():
         for p, g in ptrs:
             checked = g["checked"]
+            if g["_cast"] is not None:
+                src, dst = g["_cast"]
+                rc = cast(src.data_ptr(), dst.data_ptr(), src.numel(), sp)
+                if rc:
+                    raise RuntimeError(f"vedic_cast_f32_to_f16 failed: {_lib.status_string(rc)}")
             if g["heads"]:
                 rc = lib.vedic_gemm_scatter(p, g["_heads"], g["heads"], g["N"] // g["heads"])
             else:
@@ -514,6 +545,7 @@ def run_workload(name, args, torch, dev, with_cpu):
     flops = sum(f for _, f, _ in items)
     hbm = sum(b for _, _, b in items)
     dtype = w["gemms"][0]["dtype"]
+    peak_key = "fp32" if dtype == "fp32" else "fp16"  # the AMP path multiplies binary16 values
     tflops = flops / (ms * 1e-3) / 1e12
     if w.get("hbm"):
         gbs = hbm / (ms * 1e-3) / 1e9
@@ -521,8 +553,8 @@ def run_workload(name, args, torch, dev, with_cpu):
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(name),
                 "algorithmic_bytes_per_launch": hbm}
     else:
-        roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK[dtype], "unit": "TFLOP/s",
-                "frac": round(tflops / PEAK[dtype], 4), "traffic": traffic_from_profiles(name),
+        roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK[peak_key], "unit": "TFLOP/s",
+                "frac": round(tflops / PEAK[peak_key], 4), "traffic": traffic_from_profiles(name),
                 "algorithmic_flops_per_launch": flops, "algorithmic_bytes_per_launch": hbm}
     roof["kernel_avg_us"] = round(ms * 1e3 / len(items), 3)
     cpu = cpu_baseline(w, args.cpu_seconds) if with_cpu else None
@@ -546,7 +578,7 @@ def run_workload(name, args, torch, dev, with_cpu):
         "data": "synthetic (seeded torch.randn: activations N(0,1), weights N(0,0.02), bias N(0,0.01); "
                 "fp16 operands rounded by torch's half() cast)",
         "config": config,
-        "pct_of_peak": round(100.0 * tflops / PEAK[dtype], 2),
+        "pct_of_peak": round(100.0 * tflops / PEAK[peak_key], 2),
         "roofline": roof,
         "cpu_baseline": cpu,
         "wall_s": round(wall, 4),

@@ -77,12 +77,18 @@ typedef enum {
 } vedic_epilogue_t;
 
 typedef enum {
-    VEDIC_DT_F32 = 0, /* IEEE binary32 */
-    VEDIC_DT_F16 = 1  /* IEEE binary16 */
+    VEDIC_DT_F32 = 0,     /* IEEE binary32 */
+    VEDIC_DT_F16 = 1,     /* IEEE binary16 */
+    VEDIC_DT_F32_F16 = 2  /* in_dtype only, op NN only: A binary32, B binary16;
+                             A is clamped to +-65504 and rounded to binary16
+                             (round to nearest even, as vedic_cast_f32_to_f16)
+                             inside the GEMM -- the AMP product of an fp32
+                             activation with a binary16 shadow weight */
 } vedic_dtype_t;
 
-/* Full descriptor of one GEMM.  A and B share in_dtype; C is out_dtype
- * (F16 output only with F16 inputs); bias and preact are always fp32.
+/* Full descriptor of one GEMM.  A and B share in_dtype (but see
+ * VEDIC_DT_F32_F16); C is out_dtype (F16 output only with F16 or F32_F16
+ * inputs); bias and preact are always fp32.
  * Zero-initialise it (`= {0}`) so that fields a caller does not use are off. */
 typedef struct {
     int op;        /* vedic_op_t */
@@ -148,6 +154,33 @@ int vedic_gemm_bias_gelu_f16(const void* X, const void* W, const float* bias, fl
  * include/FeedForward.hpp:112-114). */
 int vedic_gemm_bias_gelu_f32(const float* X, const float* W, const float* bias, float* H,
                              float* preact, int M, int K, int N, void* stream);
+
+/* AMP products from an fp32 activation, the reference's amp_gemm /
+ * amp_gemm_bias lambdas (cuda/ModelGPU.cu:819-859):
+ *     C[MxN] = binary16(A)[MxK] . W16[KxN]            (+ bias[j])
+ * with binary16(A) the clamp-and-round of cast_fp32_to_fp16_kernel
+ * (cuda/MixedPrecision.cuh:149-161), applied inside the GEMM as A is staged
+ * (no cast pass and no per-call buffer, where the reference allocates and
+ * casts the activation on every call, cuda/ModelGPU.cu:825-827); fp32
+ * accumulation and output.  When W16 is NULL the call is the fp32 product
+ * with W32, as the reference falls back to cuda_vedic_gemm(_bias) for a
+ * parameter without a shadow.  A and C contiguous.  For N > 1024, or an A
+ * whose base is not 16-byte aligned or whose K is not a multiple of 8, the
+ * call casts A into a stream-ordered M x K binary16 workspace (hipMallocAsync
+ * on `stream`) and runs the fp16 GEMM on it: each output tile converts its
+ * own rows of A, ceil(N / 128) conversions per element, which loses to one
+ * cast pass for wide products.  Results are the same bits either way. */
+int vedic_amp_gemm(const float* A, int M, int K, const void* W16, const float* W32, int N, float* C,
+                   void* stream);
+int vedic_amp_gemm_bias(const float* A, int M, int K, const void* W16, const float* W32, int N,
+                        const float* bias, float* C, void* stream);
+
+/* The fused FFN-up from the fp32 activation: H = gelu_tanh(binary16(X) . W16
+ * + bias), preact (nullable) receives the pre-activation.  Replaces
+ * amp_gemm_bias + D2D copy + cuda_gelu (cuda/ModelGPU.cu:1023-1028) with one
+ * launch; W16 NULL gives the fp32 form with W32 (vedic_gemm_bias_gelu_f32). */
+int vedic_amp_gemm_bias_gelu(const float* X, int M, int K, const void* W16, const float* W32, int N,
+                             const float* bias, float* H, float* preact, void* stream);
 
 /* NT backward: dX[MxN] = dY[MxK] . W^T + beta * dX, W stored [NxK].
  * Replaces lmhead_grad_dx / ffn_da / ffn_dx / attn_dConcat / attn_dHeadOut

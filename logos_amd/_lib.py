@@ -30,7 +30,7 @@ STATUS_UNSUPPORTED = 9
 
 OP_NN, OP_NT, OP_TN = 0, 1, 2
 EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU, EPI_GELU_BWD = 0, 1, 2, 3, 4
-DT_F32, DT_F16 = 0, 1
+DT_F32, DT_F16, DT_F32_F16 = 0, 1, 2
 
 
 class GemmDesc(ctypes.Structure):
@@ -81,6 +81,9 @@ SIGNATURES = {
     "vedic_gemm_f16_f16out": (c_int, [c_vp, c_int, c_int, c_vp, c_int, c_vp, c_float, c_float, c_vp]),
     "vedic_gemm_bias_gelu_f16": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     "vedic_gemm_bias_gelu_f32": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
+    "vedic_amp_gemm": (c_int, [c_vp, c_int, c_int, c_vp, c_vp, c_int, c_vp, c_vp]),
+    "vedic_amp_gemm_bias": (c_int, [c_vp, c_int, c_int, c_vp, c_vp, c_int, c_vp, c_vp, c_vp]),
+    "vedic_amp_gemm_bias_gelu": (c_int, [c_vp, c_int, c_int, c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp]),
     "vedic_gemm_nt_f32": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_float, c_vp]),
     "vedic_gemm_nt_f16": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_float, c_vp]),
     "vedic_gemm_tn_f32": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_float, c_vp]),

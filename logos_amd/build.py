@@ -25,6 +25,7 @@ SOURCES = [
     "vedic_gemm_f16_nn.hip",
     "vedic_gemm_f16_nt.hip",
     "vedic_gemm_f16_tn.hip",
+    "vedic_gemm_f16_amp.hip",
     "vedic_gemm_f32_nn.hip",
     "vedic_gemm_f32_nt.hip",
     "vedic_gemm_f32_tn.hip",

@@ -18,6 +18,7 @@ hipError_t launch_gemm_f32(int op, bool vec, const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_nn(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_nt(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_tn(const GemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_f16_direct_amp(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_skinny(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f32_skinny(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f32_direct_nn(const GemmArgs& a, hipStream_t s);
@@ -236,6 +237,26 @@ static hipError_t launch_split2_atomic(int op, const GemmArgs& a, int kslice, hi
                                : launch_gemm_f32_direct_tn(p, s);
 }
 
+// The 16-byte-load fp16 kernels; op kOpAmp is NN with an fp32 A converted to
+// binary16 on its way into the kernel.
+constexpr int kOpAmp = 3;
+// Each tile converts its own rows of A, so the in-kernel conversion repeats
+// ceil(N / tile width) times per element.  Measured at M = 8192, K = 1024
+// with bias + GELU: in-kernel 33.7 us against cast + fp16 GEMM 34.2 us at
+// N = 1024, 63.0 against 49.3 at N = 2048, 122.6 against 86.4 at N = 4096;
+// past this N one cast pass into a workspace and the fp16 GEMM run instead.
+#ifndef VEDIC_AMP_IN_KERNEL_MAX_N
+#define VEDIC_AMP_IN_KERNEL_MAX_N 1024
+#endif
+constexpr int kAmpInKernelMaxN = VEDIC_AMP_IN_KERNEL_MAX_N;
+
+static hipError_t launch_f16_direct(int op, const GemmArgs& a, hipStream_t s) {
+    return op == VEDIC_OP_NN   ? launch_gemm_f16_direct_nn(a, s)
+           : op == VEDIC_OP_NT ? launch_gemm_f16_direct_nt(a, s)
+           : op == VEDIC_OP_TN ? launch_gemm_f16_direct_tn(a, s)
+                               : launch_gemm_f16_direct_amp(a, s);
+}
+
 // Runs the product as `ks` slices into a stream-ordered workspace, then the
 // reduction with the caller's epilogue.
 static hipError_t launch_split(bool f16, int op, bool vec, const GemmArgs& a, int ks, hipStream_t s) {
@@ -259,9 +280,7 @@ static hipError_t launch_split(bool f16, int op, bool vec, const GemmArgs& a, in
     p.kslice = kslice;
     p.c_split_stride = total;
     if (f16)
-        e = op == VEDIC_OP_NN   ? launch_gemm_f16_direct_nn(p, s)
-            : op == VEDIC_OP_NT ? launch_gemm_f16_direct_nt(p, s)
-                                : launch_gemm_f16_direct_tn(p, s);
+        e = launch_f16_direct(op, p, s);
     else
         e = launch_f32_tiled(op, vec, p, s);
     if (e == hipSuccess) {
@@ -309,6 +328,9 @@ struct ColsumHandoff {
     int blocks;
 };
 
+static int amp_via_cast(const vedic_gemm_desc_t* d, float* const* heads, int nheads, int head_cols,
+                        ColsumHandoff* handoff);
+
 static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads, int head_cols,
                      ColsumHandoff* handoff = nullptr) {
     if (!d) return VEDIC_STATUS_NULL_POINTER;
@@ -327,9 +349,12 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
             return VEDIC_STATUS_BAD_EPILOGUE;
     }
     if (d->op < VEDIC_OP_NN || d->op > VEDIC_OP_TN) return VEDIC_STATUS_BAD_LAYOUT;
-    if (d->in_dtype != VEDIC_DT_F32 && d->in_dtype != VEDIC_DT_F16) return VEDIC_STATUS_BAD_DTYPE;
+    if (d->in_dtype != VEDIC_DT_F32 && d->in_dtype != VEDIC_DT_F16 && d->in_dtype != VEDIC_DT_F32_F16)
+        return VEDIC_STATUS_BAD_DTYPE;
+    const bool amp = d->in_dtype == VEDIC_DT_F32_F16;  // fp32 A, binary16 B, A converted in the kernel
+    if (amp && d->op != VEDIC_OP_NN) return VEDIC_STATUS_BAD_DTYPE;
     if (d->out_dtype != VEDIC_DT_F32 &&
-        !(d->out_dtype == VEDIC_DT_F16 && d->in_dtype == VEDIC_DT_F16))
+        !(d->out_dtype == VEDIC_DT_F16 && (d->in_dtype == VEDIC_DT_F16 || amp)))
         return VEDIC_STATUS_BAD_DTYPE;
     if (!d->A || !d->B || (!d->C && !scatter)) return VEDIC_STATUS_NULL_POINTER;
     if (d->epilogue < VEDIC_EPI_NONE || d->epilogue > VEDIC_EPI_GELU_BWD) return VEDIC_STATUS_BAD_EPILOGUE;
@@ -379,8 +404,11 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
 
     // 16-byte vector loads need aligned bases, leading dimensions that keep
     // every row aligned, and contiguous extents that end on a chunk boundary.
-    const int ve = d->in_dtype == VEDIC_DT_F16 ? 8 : 4;
-    const bool vec = aligned16(d->A) && aligned16(d->B) && d->lda % ve == 0 && d->ldb % ve == 0 &&
+    // An fp32 A of the AMP path is read in chunks of eight values (one
+    // binary16 chunk of the staging layout).
+    const int ve = d->in_dtype == VEDIC_DT_F32 ? 4 : 8;
+    const int vea = d->in_dtype == VEDIC_DT_F16 ? 8 : 4;
+    const bool vec = aligned16(d->A) && aligned16(d->B) && d->lda % vea == 0 && d->ldb % ve == 0 &&
                      a_row % ve == 0 && b_row % ve == 0;
 
     a.epi_kind = epi_kind_of(a.epi, a.alpha, a.beta);
@@ -389,11 +417,14 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
     // row: a few hundred rows of any operand or output must stay below 2 GiB.
     if (a.ldc >= kMaxLd || (d->preact && d->ld_preact >= kMaxLd)) return VEDIC_STATUS_TOO_LARGE;
 
-    const bool f16 = d->in_dtype == VEDIC_DT_F16;
-    const bool direct = vec && d->lda < kMaxLd && d->ldb < kMaxLd;
+    const bool f16 = d->in_dtype != VEDIC_DT_F32;
+    // (an fp32 A's tile rows are twice as long in bytes)
+    const bool direct = vec && d->lda < (amp ? kMaxLd / 2 : kMaxLd) && d->ldb < kMaxLd;
+    if (amp && (!direct || d->N > kAmpInKernelMaxN)) return amp_via_cast(d, heads, nheads, head_cols, handoff);
     // scattered C needs the kernels with a plain or bias epilogue kind
     if (scatter && !direct) return VEDIC_STATUS_BAD_LD;
-    const bool skinny = direct && d->op == VEDIC_OP_NN && d->M <= 32;
+    const bool skinny = direct && !amp && d->op == VEDIC_OP_NN && d->M <= 32;
+    const int kop = amp ? kOpAmp : d->op;  // the fp16 kernels' op
     const int ks = skinny || scatter || (f16 && !direct) ? 1 : choose_ksplit(d->M, d->N, d->K, device_cu_count(), f16);
 
     hipStream_t s = static_cast<hipStream_t>(d->stream);
@@ -431,11 +462,9 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
         if (!f16 && direct && ks2 == 2 && a.epi_kind == EK_PLAIN)
             e = launch_split2_atomic(d->op, a, kslice, s);
         else
-            e = launch_split(f16, d->op, vec, a, ks, s);
+            e = launch_split(f16, kop, vec, a, ks, s);
     } else if (f16 && direct) {
-        e = d->op == VEDIC_OP_NN   ? launch_gemm_f16_direct_nn(a, s)
-            : d->op == VEDIC_OP_NT ? launch_gemm_f16_direct_nt(a, s)
-                                   : launch_gemm_f16_direct_tn(a, s);
+        e = launch_f16_direct(kop, a, s);
     } else if (f16) {
         e = launch_gemm_f16_generic(d->op, a, s);
     } else {
@@ -467,6 +496,39 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
         if (e == hipSuccess) e = f;
     }
     return hip_status(e);
+}
+
+// dst[r][c] = binary16(clamp(src[r][c])) for an M x K fp32 matrix with
+// leading dimension lds into a contiguous M x K one.
+__global__ void cast_rows_f16_kernel(const float* __restrict__ src, int64_t lds, _Float16* __restrict__ dst, int M,
+                                     int K) {
+    for (int r = blockIdx.x; r < M; r += gridDim.x)
+        for (int c = threadIdx.x; c < K; c += blockDim.x) dst[(int64_t)r * K + c] = to_half_clamped(src[r * lds + c]);
+}
+
+// The AMP product for an fp32 A the in-kernel conversion cannot read
+// (unaligned base or leading dimension, K not a multiple of 8, very long
+// rows): A is cast into a stream-ordered binary16 workspace first, as the
+// reference casts into a per-call buffer (cuda/ModelGPU.cu:825-827).
+static int amp_via_cast(const vedic_gemm_desc_t* d, float* const* heads, int nheads, int head_cols,
+                        ColsumHandoff* handoff) {
+    hipStream_t s = static_cast<hipStream_t>(d->stream);
+    _Float16* a16 = nullptr;
+    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&a16), sizeof(_Float16) * (size_t)d->M * d->K, s);
+    if (e != hipSuccess) return hip_status(e);
+    hipLaunchKernelGGL(cast_rows_f16_kernel, dim3((unsigned)(d->M < 4096 ? d->M : 4096)), dim3(256), 0, s,
+                       static_cast<const float*>(d->A), d->lda, a16, d->M, d->K);
+    e = hipGetLastError();
+    int st = hip_status(e);
+    if (e == hipSuccess) {
+        vedic_gemm_desc_t g = *d;
+        g.in_dtype = VEDIC_DT_F16;
+        g.A = a16;
+        g.lda = d->K;
+        st = gemm_impl(&g, heads, nheads, head_cols, handoff);
+    }
+    const hipError_t f = hipFreeAsync(a16, s);
+    return st != VEDIC_STATUS_OK ? st : hip_status(f);
 }
 
 extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) { return gemm_impl(d, nullptr, 0, 0); }
@@ -548,6 +610,33 @@ extern "C" int vedic_gemm_bias_gelu_f32(const float* X, const float* W, const fl
     d.epilogue = VEDIC_EPI_BIAS_GELU;
     d.preact = preact;
     d.ld_preact = N;
+    return vedic_gemm(&d);
+}
+
+extern "C" int vedic_amp_gemm_bias_gelu(const float* X, int M, int K, const void* W16, const float* W32, int N,
+                                        const float* bias, float* H, float* preact, void* stream) {
+    if (!W16) return vedic_gemm_bias_gelu_f32(X, W32, bias, H, preact, M, K, N, stream);
+    vedic_gemm_desc_t d = make_desc(VEDIC_OP_NN, VEDIC_DT_F32_F16, M, N, K, X, K, W16, N, H, 1.f, 0.f, stream);
+    d.bias = bias;
+    d.epilogue = VEDIC_EPI_BIAS_GELU;
+    d.preact = preact;
+    d.ld_preact = preact ? N : 0;
+    return vedic_gemm(&d);
+}
+
+extern "C" int vedic_amp_gemm_bias(const float* A, int M, int K, const void* W16, const float* W32, int N,
+                                   const float* bias, float* C, void* stream) {
+    if (!W16) return vedic_gemm_bias_f32(A, W32, bias, C, M, K, N, stream);
+    vedic_gemm_desc_t d = make_desc(VEDIC_OP_NN, VEDIC_DT_F32_F16, M, N, K, A, K, W16, N, C, 1.f, 0.f, stream);
+    d.bias = bias;
+    d.epilogue = VEDIC_EPI_BIAS;
+    return vedic_gemm(&d);
+}
+
+extern "C" int vedic_amp_gemm(const float* A, int M, int K, const void* W16, const float* W32, int N, float* C,
+                              void* stream) {
+    if (!W16) return vedic_gemm_f32(A, W32, C, M, K, N, stream);
+    vedic_gemm_desc_t d = make_desc(VEDIC_OP_NN, VEDIC_DT_F32_F16, M, N, K, A, K, W16, N, C, 1.f, 0.f, stream);
     return vedic_gemm(&d);
 }
 
@@ -635,9 +724,6 @@ __global__ void gelu_kernel(float* __restrict__ x, int64_t n) {
         x[i] = gelu_tanh(x[i]);
 }
 
-__device__ __forceinline__ _Float16 to_half_clamped(float v) {
-    return (_Float16)fmaxf(fminf(v, 65504.0f), -65504.0f);
-}
 
 // Eight elements per thread per step when the buffers are 16-byte aligned.
 __global__ void cast_f32_f16_kernel(const float* __restrict__ src, _Float16* __restrict__ dst,
@@ -1082,6 +1168,7 @@ extern "C" int vedic_verify(const float* A, const float* B, const float* C, int 
 // prediction colsum(op(A)) . rowsum(op(B)) from one pass over A and B.
 extern "C" int vedic_gemm_checked(const vedic_gemm_desc_t* d, float tolerance, vedic_verify_result_t* out) {
     if (!d || !out) return VEDIC_STATUS_NULL_POINTER;
+    if (d->in_dtype == VEDIC_DT_F32_F16) return VEDIC_STATUS_BAD_DTYPE;  // operand sums of one dtype
     // the identity holds for alpha * A.B (+ bias): no beta, GELU or fp16 C
     if (d->colsum || d->beta != 0.0f || d->out_dtype != VEDIC_DT_F32 ||
         (d->epilogue != VEDIC_EPI_NONE && d->epilogue != VEDIC_EPI_BIAS) || d->preact)

@@ -60,6 +60,13 @@ __device__ __forceinline__ float gelu_tanh_grad(float x) {
     return __builtin_fmaf(2.0f * c * t, __builtin_fmaf(k3, x2, 1.0f), sg);
 }
 
+// binary16(clamp(v, -65504, 65504)), round to nearest even: the AMP cast of
+// cast_fp32_to_fp16_kernel (cuda/MixedPrecision.cuh:149-161).  fminf/fmaxf
+// return the non-NaN operand, so NaN becomes 65504 as there.
+__device__ __forceinline__ _Float16 to_half_clamped(float v) {
+    return (_Float16)fmaxf(fminf(v, 65504.0f), -65504.0f);
+}
+
 // Epilogue flag bits (internal).
 enum : int {
     EPI_BIAS = 1,

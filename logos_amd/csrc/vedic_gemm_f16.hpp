@@ -40,6 +40,8 @@
 // for all of its outstanding loads, not just the stage it needs).
 #pragma once
 
+#include <type_traits>
+
 #include "vedic_common.hpp"
 #include "vedic_epilogue.hpp"
 
@@ -126,6 +128,86 @@ struct Side {
                                                      kend[i] <= krem ? off[i] : kOob, 0, 0, 0);
     }
 };
+
+// An fp32 A operand stored [M x K] (k contiguous) for the AMP path: each
+// 16-byte binary16 chunk of the KC layout is loaded as its eight fp32 values
+// (two 16-byte register loads), clamped and rounded to binary16
+// (to_half_clamped, the cast kernel's conversion) and written to its swizzled
+// LDS position with one ds_write_b128.  Lanes take consecutive chunks of a
+// row, so a wave's loads cover whole 256-byte row segments.  load() issues a
+// stage's register loads; commit() converts and writes them once they have
+// landed.  Rows past M and chunks past K load as zeros (kOob).
+template <int R, int BK, int NW>
+struct SideA32 {
+    static constexpr int CPR = BK / 8;                 // 16-byte binary16 chunks per LDS row
+    static constexpr int NCH = R * CPR / (NW * 64);    // chunks per thread and stage
+    static constexpr int NLD = 2 * NCH;                // register loads per wave and stage
+    static constexpr int BYTES = R * BK * 2;           // the LDS stage (binary16)
+    static_assert(R * CPR % (NW * 64) == 0, "stage chunks do not divide among the threads");
+    uint32_t off[NCH];  // byte offset of the chunk's first fp32 value from the tile base; kOob outside
+    int kend[NCH];
+    float4_t v[NCH][2];
+
+    __device__ __forceinline__ static void geom(int wave, int lane, int i, int& row, int& p) {
+        const int q = (wave * NCH + i) * 64 + lane;
+        row = q / CPR;
+        p = q % CPR;
+    }
+    __device__ __forceinline__ void init(int wave, int lane, int64_t ld, int mn0, int MN) {
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            int row, p;
+            geom(wave, lane, i, row, p);
+            off[i] = mn0 + row < MN ? (uint32_t)((int64_t)row * ld * 4 + p * 32) : kOob;
+            kend[i] = 8 * p + 8;
+        }
+    }
+    // `tile` points at element (mn0, k0); krem = K - k0.
+    __device__ __forceinline__ void load(const float* tile, int krem) {
+        const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(tile);
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const uint32_t o = kend[i] <= krem ? off[i] : kOob;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                v[i][h] = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                           rs, (int)(o == kOob ? kOob : o + 16 * h), 0, 0));
+        }
+    }
+    // Round to nearest even first (packed, two values per instruction), then
+    // clamp the binary16 pair to +-65504 (packed min/max, IEEE minNum /
+    // maxNum): the same bits as clamping in fp32 first.  Finite values at or
+    // above 65520 round to infinity and clamp back to 65504; values below it
+    // round to at most 65504; infinities clamp; a NaN converts to a NaN, which
+    // minNum replaces by 65504, as fminf does in the fp32 clamp.
+    __device__ __forceinline__ void commit(char* lds, int wave, int lane) const {
+        typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+        typedef float float2_t __attribute__((ext_vector_type(2)));
+        const half2_t hi = {(_Float16)65504.0f, (_Float16)65504.0f};
+        const half2_t lo = {(_Float16)-65504.0f, (_Float16)-65504.0f};
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            int row, p;
+            geom(wave, lane, i, row, p);
+            half8_t hv;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const float2_t f = {v[i][e >> 2][e & 3], v[i][e >> 2][(e & 3) + 1]};
+                half2_t h = __builtin_convertvector(f, half2_t);
+                h = __builtin_elementwise_max(__builtin_elementwise_min(h, hi), lo);
+                hv[e] = h[0];
+                hv[e + 1] = h[1];
+            }
+            *reinterpret_cast<half8_t*>(lds + row * (CPR * 16) + ((p ^ swz_kc<CPR>(row)) << 4)) = hv;
+        }
+    }
+};
+
+// lgkmcnt(0), vmcnt and expcnt left at their maxima (gfx9 encoding): the
+// LDS writes of a commit have landed before the stage barrier.
+__device__ __forceinline__ void wait_lgkmcnt0() {
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+}
 
 // MFMA operand fragment: 8 halves, k = 16 kk + 8 (lane / 32) .. + 7, of
 // row/column rc0 + lane % 32.
@@ -252,20 +334,45 @@ __device__ __forceinline__ WorkItem work_of(const GemmArgs& a, int w, int ntiles
 
 #define VEDIC_A_TILE(k) \
     (A_KC ? A + (int64_t)m0 * args.lda + ((k) < K ? (k) : 0) : A + (int64_t)((k) < K ? (k) : 0) * args.lda + m0)
+#define VEDIC_A32_TILE(k) (A32f + (int64_t)m0 * args.lda + ((k) < K ? (k) : 0))
 #define VEDIC_B_TILE(k) \
     (B_KC ? B + (int64_t)n0 * args.ldb + ((k) < K ? (k) : 0) : B + (int64_t)((k) < K ? (k) : 0) * args.ldb + n0)
+// The loads of stage kt: A into (la) (an fp32 A into registers, committed
+// to (la) later), B into (lb).
 #define VEDIC_ISSUE(kt, la, lb)                                                          \
     do {                                                                                 \
         const int k_ = it.kb + (kt) * BK;                                                \
-        sa.load(VEDIC_A_TILE(k_), (la), wave, lane, it.ke - k_);                         \
+        if constexpr (A32)                                                               \
+            sa.load(VEDIC_A32_TILE(k_), it.ke - k_);                                     \
+        else                                                                             \
+            sa.load(VEDIC_A_TILE(k_), (la), wave, lane, it.ke - k_);                     \
         sb.load(VEDIC_B_TILE(k_), (lb), wave, lane, it.ke - k_);                         \
     } while (0)
+// The first ST - 1 stages of a work item; with an fp32 A each stage's A is
+// committed as soon as it has landed (its B may still be in flight).
+#define VEDIC_PROLOGUE_STAGE(s_)                                                         \
+    do {                                                                                 \
+        VEDIC_ISSUE(s_, As[s_], Bs[s_]);                                                 \
+        if constexpr (A32) {                                                             \
+            wait_vmcnt<SB::NLD>();                                                       \
+            sa.commit(As[s_], wave, lane);                                               \
+        }                                                                                \
+    } while (0)
+#define VEDIC_PROLOGUE()                                                                 \
+    do {                                                                                 \
+        VEDIC_PROLOGUE_STAGE(0);                                                         \
+        if constexpr (ST > 2) VEDIC_PROLOGUE_STAGE(1);                                   \
+        if constexpr (ST > 3) VEDIC_PROLOGUE_STAGE(2);                                   \
+    } while (0)
 
+// OP: 0 NN, 1 NT, 2 TN, 3 NN with an fp32 A converted to binary16 on its way
+// into LDS (the AMP path from fp32 activations).
 template <int OP, int BM, int BN, int BK, int ST, int WGM, int WGN, int KIND>
 __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) {
     constexpr int NW = WGM * WGN, WM = BM / WGM, WN = BN / WGN, MI = WM / 32, NI = WN / 32;
+    constexpr bool A32 = OP == 3;
     constexpr bool A_KC = OP != 2, B_KC = OP == 1;
-    using SA = Side<A_KC, BM, BK, NW>;
+    using SA = std::conditional_t<A32, SideA32<BM, BK, NW>, Side<A_KC, BM, BK, NW>>;
     using SB = Side<B_KC, BN, BK, NW>;
     constexpr int L = SA::NLD + SB::NLD;  // load instructions per wave per stage
     static_assert(ST >= 2 && ST <= 4, "2 to 4 LDS stages");
@@ -291,6 +398,7 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
     const int lane = threadIdx.x & 63;
     const int wm = wave / WGN, wn = wave % WGN;
     const _Float16* __restrict__ A = static_cast<const _Float16*>(args.A);
+    const float* __restrict__ A32f = static_cast<const float*>(args.A);
     const _Float16* __restrict__ B = static_cast<const _Float16*>(args.B);
     const int K = args.K;
     const int G = gridDim.x;
@@ -307,8 +415,7 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
     SB sb;
     sa.init(wave, lane, args.lda, m0, args.M);
     sb.init(wave, lane, args.ldb, n0, args.N);
-#pragma unroll
-    for (int s = 0; s < ST - 1; ++s) VEDIC_ISSUE(s, As[s], Bs[s]);
+    VEDIC_PROLOGUE();
 
     // The bias of this wave's columns is loaded as a tile starts and waited
     // for before the next tile's first stages are issued: a bias load issued
@@ -341,10 +448,25 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
 #pragma unroll
             for (int s = 0; s < ST; ++s) {
                 const int kt = k0 + s;
-                wait_vmcnt<(ST - 2) * L>();  // stage kt has landed; ST - 2 later stages in flight
+                if constexpr (A32) {
+                    // A of stage kt was committed at the end of the previous
+                    // step (everything issued before it has landed); B of
+                    // stage kt is the newest batch when ST = 2
+                    wait_vmcnt<(ST - 2) * SB::NLD>();
+                    wait_lgkmcnt0();
+                } else {
+                    wait_vmcnt<(ST - 2) * L>();  // stage kt has landed; ST - 2 later stages in flight
+                }
                 stage_barrier();
                 const int sl = (s + ST - 1) % ST;
-                if constexpr (kInterleave) {
+                if constexpr (A32) {
+                    // register loads, then the MFMAs, then the conversion into
+                    // stage kt - 1's buffer, free since the barrier above
+                    VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
+                    if (kt < nk) mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI>(As[s], Bs[s], wm * WM, wn * WN, lane, acc);
+                    wait_vmcnt<SB::NLD>();
+                    sa.commit(As[sl], wave, lane);
+                } else if constexpr (kInterleave) {
                     // the loads and the MFMAs in one block, one load after each of the first L MFMAs
                     if (kt < nk) {
                         VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
@@ -367,15 +489,17 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
         const bool more = w < nwork;
 #pragma unroll
         for (int j = 0; j < NI; ++j) asm volatile("" : "+v"(bias_pre[j]));  // the bias has landed
-        if (more) {
+        // The next work item's first stages go out before this epilogue
+        // (with an fp32 A after it: its staging registers would be live
+        // across the epilogue).
+        if (!A32 && more) {
             __syncthreads();  // every wave is done reading the stage buffers
             it = work_of<BM, BN, BK>(args, w, ntiles);
             m0 = it.m0;
             n0 = it.n0;
             sa.init(wave, lane, args.lda, m0, args.M);
             sb.init(wave, lane, args.ldb, n0, args.N);
-#pragma unroll
-            for (int s = 0; s < ST - 1; ++s) VEDIC_ISSUE(s, As[s], Bs[s]);
+            VEDIC_PROLOGUE();
         }
         const bool full = (row0 + WM <= args.M) && (col0 + WN <= args.N);
         if (KIND != EK_GENERIC && full)
@@ -383,11 +507,23 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
         else
             epilogue<KIND, true, MI, NI>(args, cp, acc, row0, col0, lane, pre_bias ? bias_pre : nullptr);
         if (!more) break;
+        if constexpr (A32) {
+            __syncthreads();
+            it = work_of<BM, BN, BK>(args, w, ntiles);
+            m0 = it.m0;
+            n0 = it.n0;
+            sa.init(wave, lane, args.lda, m0, args.M);
+            sb.init(wave, lane, args.ldb, n0, args.N);
+            VEDIC_PROLOGUE();
+        }
     }
     wait_vmcnt<0>();  // the trailing zero loads still write LDS
 }
 
 #undef VEDIC_ISSUE
+#undef VEDIC_PROLOGUE
+#undef VEDIC_PROLOGUE_STAGE
+#undef VEDIC_A32_TILE
 #undef VEDIC_A_TILE
 #undef VEDIC_B_TILE
 
@@ -567,18 +703,27 @@ hipError_t launch_gemm_f16_direct_op(const GemmArgs& a, hipStream_t s) {
         else
             return launch_f16_kind<OP, CfgNarrow>(a, s);
     }
-    if (a.ksplit <= 1 && a.cs_part == nullptr && VEDIC_F16_COLUMN_SPLIT) {
-        const int n1 = f16_column_split(a.M, a.N, device_cu_count());
-        if (n1 > 0 && (a.head_cols <= 0 || n1 % a.head_cols == 0)) {
-            const hipError_t e = launch_f16_kind<OP, CfgLarge>(f16_columns<OP>(a, 0, n1), s);
-            if (e != hipSuccess) return e;
-            return launch_f16_kind<OP, CfgMid>(f16_columns<OP>(a, n1, a.N - n1), s);
+    if constexpr (OP == 3) {
+        // fp32 A: no 256 x 256 tiles (its staging registers do not fit beside
+        // their accumulators); 256 x 128 where the cost model picks 256 x 256
+        // or 256 x 128, else 128 x 128
+        if (a.ksplit <= 1 && f16_tile_config(a.M, a.N, device_cu_count()) <= 1)
+            return launch_f16_kind<OP, CfgMid>(a, s);
+        return launch_f16_kind<OP, CfgSmall>(a, s);
+    } else {
+        if (a.ksplit <= 1 && a.cs_part == nullptr && VEDIC_F16_COLUMN_SPLIT) {
+            const int n1 = f16_column_split(a.M, a.N, device_cu_count());
+            if (n1 > 0 && (a.head_cols <= 0 || n1 % a.head_cols == 0)) {
+                const hipError_t e = launch_f16_kind<OP, CfgLarge>(f16_columns<OP>(a, 0, n1), s);
+                if (e != hipSuccess) return e;
+                return launch_f16_kind<OP, CfgMid>(f16_columns<OP>(a, n1, a.N - n1), s);
+            }
         }
-    }
-    switch (a.ksplit > 1 ? 2 : f16_tile_config(a.M, a.N, device_cu_count())) {
-        case 0: return launch_f16_kind<OP, CfgLarge>(a, s);
-        case 1: return launch_f16_kind<OP, CfgMid>(a, s);
-        default: return launch_f16_kind<OP, CfgSmall>(a, s);
+        switch (a.ksplit > 1 ? 2 : f16_tile_config(a.M, a.N, device_cu_count())) {
+            case 0: return launch_f16_kind<OP, CfgLarge>(a, s);
+            case 1: return launch_f16_kind<OP, CfgMid>(a, s);
+            default: return launch_f16_kind<OP, CfgSmall>(a, s);
+        }
     }
 }
 

@@ -33,7 +33,7 @@ from ._lib import (DT_F16, DT_F32, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU, EPI_GELU_B
 __all__ = [
     "OP_NN", "OP_NT", "OP_TN", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU", "EPI_GELU", "EPI_GELU_BWD",
     "gemm", "vedic_gemm", "vedic_gemm_bias", "gemm_fp16_fp32out", "gemm_fp16_fp16out",
-    "gemm_bias_gelu", "gemm_nt", "gemm_tn", "gemm_nt_gelu_bwd", "bias_grad", "gemm_scatter",
+    "gemm_bias_gelu", "amp_gemm", "gemm_nt", "gemm_tn", "gemm_nt_gelu_bwd", "bias_grad", "gemm_scatter",
     "cast_pack_fp16", "add_bias", "gelu_",
     "cast_fp32_to_fp16",
     "cast_fp16_to_fp32", "verify", "gemm_checked", "VerifyResult", "uses_vendor_blas", "backend_name",
@@ -86,8 +86,12 @@ def gemm(op: int, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor | None = Non
     epilogue=EPI_GELU_BWD multiplies by gelu_tanh'(preact) (preact is then an
     input).  colsum (N float32 values) receives colsum_beta * colsum + the
     column sums of the final C."""
-    if A.dtype != B.dtype or A.dtype not in _DT:
-        raise ValueError(f"A and B must share dtype float16 or float32 (got {A.dtype}, {B.dtype})")
+    amp = A.dtype == torch.float32 and B.dtype == torch.float16  # A converted to binary16 in the GEMM
+    if (A.dtype != B.dtype or A.dtype not in _DT) and not amp:
+        raise ValueError(f"A and B must share dtype float16 or float32, or be float32 A with float16 B "
+                         f"(got {A.dtype}, {B.dtype})")
+    if amp and op != OP_NN:
+        raise ValueError("a float32 A with a float16 B is an NN product")
     ar, ac, lda = _mat(A, "A")
     br, bc, ldb = _mat(B, "B")
     if op == OP_NN:
@@ -122,7 +126,7 @@ def gemm(op: int, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor | None = Non
         if colsum.dtype != torch.float32 or colsum.numel() != N or not colsum.is_cuda or not colsum.is_contiguous():
             raise ValueError(f"colsum must be {N} contiguous float32 values on the GPU")
     d = _lib.GemmDesc(
-        op=op, in_dtype=_DT[A.dtype], out_dtype=_DT[C.dtype], M=M, N=N, K=K,
+        op=op, in_dtype=_lib.DT_F32_F16 if amp else _DT[A.dtype], out_dtype=_DT[C.dtype], M=M, N=N, K=K,
         A=A.data_ptr(), lda=lda, B=B.data_ptr(), ldb=ldb, C=C.data_ptr(), ldc=ldc,
         alpha=alpha, beta=beta, bias=bias.data_ptr() if bias is not None else None,
         epilogue=epilogue, preact=preact.data_ptr() if preact is not None else None,
@@ -168,6 +172,29 @@ def gemm_bias_gelu(X: torch.Tensor, W: torch.Tensor, bias: torch.Tensor,
                    out: torch.Tensor | None = None, preact: torch.Tensor | None = None) -> torch.Tensor:
     """H = gelu_tanh(X . W + bias), fp32 output; preact receives X . W + bias."""
     return gemm(OP_NN, X, W, out, bias=bias, epilogue=EPI_BIAS_GELU, preact=preact)
+
+
+def amp_gemm(A: torch.Tensor, W16: torch.Tensor | None, W32: torch.Tensor | None = None,
+             out: torch.Tensor | None = None, bias: torch.Tensor | None = None, gelu: bool = False,
+             preact: torch.Tensor | None = None) -> torch.Tensor:
+    """The reference's amp_gemm / amp_gemm_bias (cuda/ModelGPU.cu:819-859) from a
+    float32 activation A: C = binary16(A) . W16 (+ bias, then GELU if asked),
+    with A clamped and rounded to binary16 inside the GEMM (no cast pass); fp32
+    accumulation and output.  W16 None: the fp32 product with W32, the
+    reference's fallback for a parameter without a binary16 shadow."""
+    if A.dtype != torch.float32:
+        raise ValueError("amp_gemm takes a float32 activation")
+    W = W16 if W16 is not None else W32
+    if W is None:
+        raise ValueError("amp_gemm needs W16 or W32")
+    if W16 is not None and W16.dtype != torch.float16:
+        raise ValueError("W16 must be float16")
+    if W16 is None and W32.dtype != torch.float32:
+        raise ValueError("W32 must be float32")
+    if gelu and bias is None:
+        raise ValueError("the fused GELU form takes a bias")
+    epi = EPI_BIAS_GELU if gelu else EPI_BIAS if bias is not None else EPI_NONE
+    return gemm(OP_NN, A, W, out, bias=bias, epilogue=epi, preact=preact)
 
 
 def gemm_nt(dY: torch.Tensor, W: torch.Tensor, out: torch.Tensor | None = None,

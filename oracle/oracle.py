@@ -373,6 +373,45 @@ def grad_rel_err(got, want64) -> float:
     return err
 
 
+U32 = 2.0 ** -24  # unit roundoff of binary32
+U16 = 2.0 ** -11  # unit roundoff of binary16
+
+
+def componentwise_ratio(got, want64, absdot, rounded=None, unit=U32) -> float:
+    """max over elements of (|got - want| - 2 unit |rounded|) / absdot: the
+    error of a dot product relative to its sum of |a_k b_k| (absdot), after
+    allowing two output roundings of size `unit` per element on the terms in
+    `rounded` (|want| by default; the caller adds |bias|, |beta C_old|).  A
+    K-term fp32 sum has ratio <= gamma_K = K u / (1 - K u) whatever the order
+    (recursive summation bound); random-sign data stays near sqrt(K) u.
+    Elements with absdot = 0 must be within the allowance exactly."""
+    got = np.asarray(got, dtype=np.float64)
+    want64 = np.asarray(want64, dtype=np.float64)
+    absdot = np.asarray(absdot, dtype=np.float64)
+    r = np.abs(want64) if rounded is None else np.asarray(rounded, dtype=np.float64)
+    excess = np.abs(got - want64) - 2.0 * unit * r
+    if not np.all(np.isfinite(excess)):
+        return float("inf")
+    pos = absdot > 0
+    if np.any(excess[~pos] > 0):
+        return float("inf")
+    if not np.any(pos):
+        return 0.0
+    return max(0.0, float(np.max(excess[pos] / absdot[pos])))
+
+
+def gemm_f64_blas(layout, A, B):
+    """(out, absdot) of op(A) op(B) in float64 through numpy's matmul (for
+    full-size outputs, where the element-wise oracle is slow)."""
+    A64 = np.asarray(A, dtype=np.float64)
+    B64 = np.asarray(B, dtype=np.float64)
+    if layout == TN:
+        A64 = A64.T
+    if layout == NT:
+        B64 = B64.T
+    return A64 @ B64, np.abs(A64) @ np.abs(B64)
+
+
 def fp32_tolerance(K: int) -> float:
     """Max relative error bound for the FP32 path: 1e-5 * sqrt(K)."""
     return 1e-5 * float(np.sqrt(K))

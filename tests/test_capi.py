@@ -54,7 +54,9 @@ def _desc(**kw):
     (dict(N=-1), _lib.STATUS_BAD_DIM),
     (dict(K=0), _lib.STATUS_BAD_DIM),
     (dict(op=3), _lib.STATUS_BAD_LAYOUT),
-    (dict(in_dtype=2), _lib.STATUS_BAD_DTYPE),
+    (dict(in_dtype=3), _lib.STATUS_BAD_DTYPE),
+    (dict(in_dtype=2, op=1), _lib.STATUS_BAD_DTYPE),  # fp32 A with binary16 B: NN only
+    (dict(in_dtype=2, op=2), _lib.STATUS_BAD_DTYPE),
     (dict(out_dtype=1), _lib.STATUS_BAD_DTYPE),  # fp16 out needs fp16 in
     (dict(A=None), _lib.STATUS_NULL_POINTER),
     (dict(C=None), _lib.STATUS_NULL_POINTER),

@@ -14,7 +14,8 @@ import pytest
 torch = pytest.importorskip("torch")
 
 from oracle import oracle as o  # noqa: E402
-from tests._gpu_helpers import FP16_TOL, dev, dev_f16, fp32_tol, host, normal  # noqa: E402
+from tests._gpu_helpers import (FP16_TOL, GELU_SLOPE, assert_componentwise, dev, dev_f16, fp32_tol,  # noqa: E402
+                                host, normal)
 
 pytestmark = pytest.mark.gpu
 
@@ -47,9 +48,17 @@ def sampled_check(got_rows, layout, A, B, rows, tol, bias=None, gelu=False, labe
         As = np.ascontiguousarray(A[:, rows])
     else:
         As = np.ascontiguousarray(A[rows])
-    want, _ = o.gemm_f64(layout, As, B, bias=bias, gelu=gelu)
+    t, absdot = o.gemm_f64(layout, As, B, bias=bias)
+    want = o.gelu_f64(t) if gelu else t
     err = o.inf_rel_err(got_rows, want)
     assert err <= tol, f"{label}: {err:.3e} > {tol:.3e} (fp64 oracle)"
+    K = A.shape[0] if layout == o.TN else A.shape[1]
+    extra = np.abs(np.asarray(bias, np.float64)) if bias is not None else 0.0
+    if gelu:
+        assert_componentwise(got_rows, want, absdot, K, slope=GELU_SLOPE,
+                             rounded=GELU_SLOPE * (np.abs(t) + extra) + 4.0 * np.abs(want), label=label)
+    else:
+        assert_componentwise(got_rows, want, absdot, K, rounded=np.abs(want) + extra, label=label)
     if layout == o.NN:
         ref = o.vedic_gemm_bias(As, B, bias) if bias is not None else o.vedic_gemm(As, B)
     elif layout == o.NT:
@@ -113,6 +122,30 @@ def test_config2_ffn_up_bias_gelu():
     sampled_check(host(pre[torch.from_numpy(rows).cuda()]), o.NN, Xr, Wr, rows, FP16_TOL, bias=b,
                   label="FFN-up preact")
     checksum_ok(Xr, Wr, host(pre), bias=b)
+
+
+def test_config2_full_output():
+    """Config 2 over every output element: the pre-activation against numpy's
+    fp64 matmul under the componentwise bounds, and H = gelu(pre) against the
+    fp64 closed form of the same fp64 product."""
+    vedic = V()
+    rng = np.random.default_rng(0x4C4F0201)
+    M, K, N = 8192, 1024, 4096
+    X, W, b = normal(rng, (M, K)), normal(rng, (K, N), std=0.02), normal(rng, (N,), std=0.01)
+    x16, Xr = dev_f16(X)
+    w16, Wr = dev_f16(W)
+    pre = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    H = host(vedic.gemm_bias_gelu(x16, w16, dev(b), preact=pre))
+    P = host(pre)
+    dot, absdot = o.gemm_f64_blas(o.NN, Xr, Wr)
+    t = dot + b.astype(np.float64)
+    assert o.inf_rel_err(P, t) <= FP16_TOL
+    assert_componentwise(P, t, absdot, K, rounded=np.abs(t) + np.abs(b.astype(np.float64)), label="preact (all)")
+    h = o.gelu_f64(t)
+    assert o.inf_rel_err(H, h) <= FP16_TOL
+    assert_componentwise(H, h, absdot, K, slope=GELU_SLOPE,
+                         rounded=GELU_SLOPE * (np.abs(t) + np.abs(b.astype(np.float64))) + 4.0 * np.abs(h),
+                         label="H (all)")
 
 
 @pytest.mark.parametrize("beta", [0.0, 1.0])

@@ -194,12 +194,12 @@ def test_fp16_output():
     b, B = dev_f16(B)
     got = host(vedic.gemm_fp16_fp16out(a, b))
     # one extra binary16 rounding of the result: relative 2^-11 on top
-    check(got, o.NN, A, B, tol=FP16_TOL + 2.0 ** -11, label="f16 out")
+    check(got, o.NN, A, B, tol=FP16_TOL + 2.0 ** -11, label="f16 out", f16_out=True)
     C0 = normal(rng, (M, N))
     c = dev(C0).half()
     got = host(vedic.gemm_fp16_fp16out(a, b, c, alpha=2.0, beta=0.5))
     C0r = o.f16_round(C0)
-    check(got, o.NN, A, B, tol=FP16_TOL + 2.0 ** -10, alpha=2.0, beta=0.5, C0=C0r, label="f16 out ab")
+    check(got, o.NN, A, B, tol=FP16_TOL + 2.0 ** -10, alpha=2.0, beta=0.5, C0=C0r, label="f16 out ab", f16_out=True)
 
 
 def test_no_write_outside_c():
@@ -296,7 +296,7 @@ def test_skinny_m_epilogues():
     got = host(vedic.gemm(vedic.OP_NN, a, b, dev(C0), alpha=0.5, beta=1.0))
     check(got, o.NN, A, B, tol=FP16_TOL, alpha=0.5, beta=1.0, C0=C0, label="skinny alpha/beta")
     got = host(vedic.gemm_fp16_fp16out(a, b))
-    check(got, o.NN, A, B, tol=FP16_TOL + 2.0 ** -11, label="skinny f16 out")
+    check(got, o.NN, A, B, tol=FP16_TOL + 2.0 ** -11, label="skinny f16 out", f16_out=True)
     # no write outside C: a view with a wider leading dimension
     buf = torch.full((M, N + 8), 3.0, dtype=torch.float32, device="cuda")
     vedic.gemm(vedic.OP_NN, a, b, buf[:, :N])
@@ -341,7 +341,7 @@ def test_split_k_epilogues():
     c16 = dev(C0).half()
     got = host(vedic.gemm(vedic.OP_TN, a, b, c16, alpha=2.0, beta=0.5, out_dtype=torch.float16))
     check(got, o.TN, A, B, tol=FP16_TOL + 2.0 ** -10, alpha=2.0, beta=0.5, C0=o.f16_round(C0),
-          label="split-K f16 out")
+          label="split-K f16 out", f16_out=True)
     buf = torch.full((M, N + 8), 5.0, dtype=torch.float32, device="cuda")
     vedic.gemm(vedic.OP_TN, a, b, buf[:, :N])
     assert np.all(host(buf)[:, N:] == 5.0)

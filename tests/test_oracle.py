@@ -440,3 +440,46 @@ def test_reference_backward_restatement_against_f64(seq, dh):
     got = o.attention_backward_reference(Q, K, V, dO, sc)
     want = o.flash_attention_bwd_f64(Q, K, V, dO, sc, 1)
     assert o.grad_rel_err(got, want) <= o.fp32_tolerance(max(seq, dh))
+
+
+def test_componentwise_bound_catches_binary16_rounding():
+    """A precision regression planted in the oracle's own output: C rounded
+    through binary16 (relative error up to 2^-12).  The 2e-3 infinity-norm
+    bound alone accepts it; the componentwise bound every GPU parity check
+    asserts (tests/_gpu_helpers.assert_componentwise) rejects it, and accepts
+    the unmodified fp32 restatement of the reference's vedic_gemm."""
+    from tests._gpu_helpers import assert_componentwise
+
+    rng = np.random.default_rng(11)
+    M, K, N = 256, 1024, 256
+    A = o.f16_round(rng.standard_normal((M, K), dtype=np.float32))
+    B = o.f16_round(rng.standard_normal((K, N), dtype=np.float32) * np.float32(0.02))
+    want, absdot = o.gemm_f64(o.NN, A, B)
+    good = o.vedic_gemm(A, B)
+    bad = o.f16_round(good)
+    assert o.inf_rel_err(good, want) <= o.FP16_TOLERANCE
+    assert o.inf_rel_err(bad, want) <= o.FP16_TOLERANCE  # the old bound misses it
+    assert_componentwise(good, want, absdot, K, label="fp32 restatement")
+    with pytest.raises(AssertionError, match="componentwise"):
+        assert_componentwise(bad, want, absdot, K, label="C through binary16")
+    # the same regression in a partial sum: the second half of K accumulated
+    # separately and rounded through binary16 before the final add
+    half = K // 2
+    p1 = o.vedic_gemm(A[:, :half], B[:half])
+    p2 = o.f16_round(o.vedic_gemm(A[:, half:], B[half:]))
+    with pytest.raises(AssertionError, match="componentwise"):
+        assert_componentwise(p1 + p2, want, absdot, K, label="partial through binary16")
+
+
+def test_componentwise_ratio_definition():
+    """componentwise_ratio on hand-made cases: exact results give 0; an error
+    of e on an element with absdot s gives e / s after the rounding allowance;
+    absdot = 0 with any error beyond the allowance gives inf."""
+    want = np.array([[1.0, -2.0]])
+    absdot = np.array([[4.0, 8.0]])
+    assert o.componentwise_ratio(want, want, absdot) == 0.0
+    got = want + np.array([[0.0, 1e-3]])
+    r = o.componentwise_ratio(got, want, absdot)
+    assert abs(r - (1e-3 - 2 * o.U32 * 2.0) / 8.0) < 1e-15
+    assert o.componentwise_ratio(np.array([[1e-3]]), np.array([[0.0]]), np.array([[0.0]])) == float("inf")
+    assert o.componentwise_ratio(np.array([[np.nan]]), np.array([[0.0]]), np.array([[1.0]])) == float("inf")
