@@ -9,6 +9,9 @@
 //   cuda_vedic_gemm, cuda_vedic_gemm_bias,
 //   cuda_vedic_gemm_uses_cublas, cuda_gelu       cuda/VedicGEMM.cuh:182-187
 //   cuda_add_bias (the add_bias_kernel launch)   cuda/VedicGEMM.cuh:191
+//   add_bias_kernel, cast_fp32_to_fp16_kernel,
+//   vedic_gemm_kernel (for raw <<<>>> launches)  cuda/VedicGEMM.cuh:191, MixedPrecision.cuh:149,
+//                                                 cuda/VedicGEMM.cu:39
 //   cuda_vedic_verify, VedicVerifyResult          cuda/VedicGEMM.cuh:162-167,193
 //   cuda_gemm_fp16_fp32out / _fp16out             cuda/VedicGEMM.cuh:251-252
 //   HalfTensor, half_alloc,
@@ -379,6 +382,50 @@ inline void cuda_flash_attention_bwd_heads(const float* const* Q, const float* c
     vedic_hip::check(vedic_flash_attention_bwd_heads(Q, K, V, O, dO, lse, dQ, dK, dV, nheads, seq, DH, scale,
                                                      causal ? 1 : 0, shunyam ? 1 : 0, window, stride, stream),
                      "cuda_flash_attention_bwd_heads");
+}
+
+// ------------------------------------------- kernels the callers launch raw
+//
+// The reference's callers and tests launch three of its kernels directly with
+// <<<grid, block>>> (add_bias_kernel: cuda/VedicGEMM.cuh:191, launched at
+// cuda/ModelGPU.cu:854 and tests/test_cuda_kernels.cu:140,201;
+// cast_fp32_to_fp16_kernel: cuda/MixedPrecision.cuh:149, launched at
+// cuda/ModelGPU.cu:826,846 and tests/test_cuda_kernels.cu:392;
+// vedic_gemm_kernel: cuda/VedicGEMM.cu:39, launched at cuda/train_gpu.cu:684).
+// HIP links device code per translation unit (no -fgpu-rdc), so the kernels
+// are defined here with internal linkage and such a launch compiles in the
+// caller's own file unchanged.  Each loops over its index space with the
+// launch's grid stride, so the grids those call sites compute cover the work,
+// and any other grid does too.  These are the compatibility kernels; the
+// library path (cuda_add_bias, cuda_cast_fp32_to_fp16, cuda_vedic_gemm) is
+// the fast one.
+
+// C[i][j] += bias[j] over an M x N matrix.
+static __global__ void add_bias_kernel(float* __restrict__ C, const float* __restrict__ bias, int M, int N) {
+    const int64_t total = (int64_t)M * N;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x)
+        C[i] += bias[i % N];
+}
+
+// dst[i] = binary16(clamp(src[i], -65504, 65504)), round to nearest even.
+static __global__ void cast_fp32_to_fp16_kernel(const float* __restrict__ src, __half* __restrict__ dst, int n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        dst[i] = __float2half(fmaxf(fminf(src[i], 65504.0f), -65504.0f));
+}
+
+// C[M x N] = A[M x K] . B[K x N], fp32, one output per thread: thread (x, y)
+// of block (bx, by) owns column bx * blockDim.x + x and row by * blockDim.y + y
+// (the 16 x 16 blocks of the reference's launches), stepping by the grid in
+// both directions; k ascends.
+static __global__ void vedic_gemm_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                         float* __restrict__ C, int M, int K, int N) {
+    for (int r = blockIdx.y * blockDim.y + threadIdx.y; r < M; r += gridDim.y * blockDim.y)
+        for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < N; c += gridDim.x * blockDim.x) {
+            const float* a = A + (int64_t)r * K;
+            float acc = 0.0f;
+            for (int k = 0; k < K; ++k) acc = fmaf(a[k], B[(int64_t)k * N + c], acc);
+            C[(int64_t)r * N + c] = acc;
+        }
 }
 
 // --------------------------------------------------- elementwise helpers

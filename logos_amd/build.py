@@ -85,17 +85,28 @@ def build_library(jobs: int = 6) -> str:
     return LIB
 
 
-CPP_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "vedic_hip_test.cpp")
-CPP_TEST_BIN = os.path.join(ROOT, "tests", "cpp", "vedic_hip_test")
+CPP_DIR = os.path.join(ROOT, "tests", "cpp")
+CPP_TEST_SRC = os.path.join(CPP_DIR, "vedic_hip_test.cpp")
+CPP_TEST_BIN = os.path.join(CPP_DIR, "vedic_hip_test")
+CPP_TENSOR_SRC = os.path.join(CPP_DIR, "vedic_tensor_test.cpp")
+CPP_TENSOR_BIN = os.path.join(CPP_DIR, "vedic_tensor_test")
 
 
 def build_cpp_test() -> str:
-    """Host-only C++ program over include/VedicGEMM_hip.hpp, linked against the
-    library with an rpath relative to itself (so it runs wherever the tree is)."""
-    tmp = CPP_TEST_BIN + ".tmp"
-    _run([hipcc(), "-O2", "-std=c++17", "-Wall", f"-I{os.path.join(ROOT, 'include')}", CPP_TEST_SRC,
-          f"-L{PKG}", "-llogos_vedic", "-Wl,-rpath,$ORIGIN/../../logos_amd", "-o", tmp])
-    os.replace(tmp, CPP_TEST_BIN)
+    """The C++ test programs of the drop-in headers: vedic_hip_test over
+    include/VedicGEMM_hip.hpp (its raw-launch kernels are device code, hence
+    gfx950) and vedic_tensor_test over include/VedicGEMM.hpp with the test
+    Tensor of tests/cpp/tensor_stub; each linked against the library with an
+    rpath relative to itself (so it runs wherever the tree is)."""
+    inc = f"-I{os.path.join(ROOT, 'include')}"
+    common = ["-O2", "-std=c++17", "-Wall", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
+              "-packed-fp32-ops", inc]
+    link = [f"-L{PKG}", "-llogos_vedic", "-Wl,-rpath,$ORIGIN/../../logos_amd"]
+    for src, out, extra in ((CPP_TEST_SRC, CPP_TEST_BIN, []),
+                            (CPP_TENSOR_SRC, CPP_TENSOR_BIN, [f"-I{os.path.join(CPP_DIR, 'tensor_stub')}"])):
+        tmp = out + ".tmp"
+        _run([hipcc(), *common, *extra, src, *link, "-o", tmp])
+        os.replace(tmp, out)
     return CPP_TEST_BIN
 
 

@@ -126,6 +126,56 @@ static void test_known_answers() {
     EXPECT(std::string(vedic_backend_name()) == "hip-native-gfx950", "backend name");
 }
 
+// The kernels the reference's callers launch raw, with the grids those call
+// sites compute (cuda/ModelGPU.cu:826,854; cuda/train_gpu.cu:684;
+// tests/test_cuda_kernels.cu:140,392): K1 add_bias, the cast of K6 (clamp,
+// rounding), and the 16 x 16 GEMM launch on an irregular shape.
+static void test_raw_launches() {
+    // K1 through the raw launch
+    std::vector<float> h(32);
+    for (int i = 0; i < 32; ++i) h[i] = (float)i;
+    GPUTensor Cb = upload(h, 4, 8), bb = upload({1, 2, 3, 4, 5, 6, 7, 8}, 1, 8);
+    const int sz = 4 * 8;
+    add_bias_kernel<<<(sz + 255) / 256, 256>>>(Cb.data, bb.data, 4, 8);
+    HIP_CHECK(hipGetLastError());
+    auto cb = download(Cb);
+    for (int i = 0; i < 32; ++i) EXPECT(cb[i] == h[i] + (float)(i % 8 + 1), "raw add_bias %d", i);
+
+    // K6: +-1e6 clamp to +-65504; (i - 128) * 0.5 round-trips; the raw cast equals the library's
+    const int n = 256;
+    std::vector<float> src(n);
+    for (int i = 0; i < n; ++i) src[i] = (float)(i - 128) * 0.5f;
+    src[0] = 1e6f;
+    src[1] = -1e6f;
+    GPUTensor s32 = upload(src, 1, n);
+    HalfTensor a16 = half_alloc(1, n), b16 = half_alloc(1, n);
+    cast_fp32_to_fp16_kernel<<<(n + 255) / 256, 256>>>(s32.data, a16.data, n);
+    HIP_CHECK(hipGetLastError());
+    cuda_cast_fp32_to_fp16(s32.data, b16.data, n);
+    std::vector<__half> ha(n), hb(n);
+    HIP_CHECK(hipMemcpy(ha.data(), a16.data, n * sizeof(__half), hipMemcpyDeviceToHost));
+    HIP_CHECK(hipMemcpy(hb.data(), b16.data, n * sizeof(__half), hipMemcpyDeviceToHost));
+    for (int i = 0; i < n; ++i) {
+        const float v = __half2float(ha[i]);
+        EXPECT(__half2float(hb[i]) == v, "raw cast == library cast at %d", i);
+        const float want = i == 0 ? 65504.0f : i == 1 ? -65504.0f : src[i];
+        EXPECT(v == want, "raw cast %d: %g vs %g", i, v, want);
+    }
+
+    // the raw 16 x 16 GEMM launch on 37 x 53 x 29
+    Rng r(7);
+    const int M = 37, K = 53, N = 29;
+    std::vector<float> A(M * K), B(K * N);
+    for (auto& x : A) x = (float)r.next();
+    for (auto& x : B) x = (float)r.next();
+    GPUTensor dA = upload(A, M, K), dB = upload(B, K, N), dC = gpu_alloc(M, N);
+    vedic_gemm_kernel<<<dim3((N + 15) / 16, (M + 15) / 16), dim3(16, 16)>>>(dA.data, dB.data, dC.data, M, K, N);
+    HIP_CHECK(hipGetLastError());
+    auto want = ref_gemm(NN, A, B, M, N, K);
+    const double err = inf_rel(download(dC), want);
+    EXPECT(err <= 1e-5 * std::sqrt((double)K), "raw vedic_gemm_kernel: %.3e", err);
+}
+
 static void test_fp32_layouts() {
     Rng r(42);
     const int M = 97, N = 131, K = 75;
@@ -327,6 +377,8 @@ int main() {
     try {
         test_known_answers();
         std::printf("known answers done\n");
+        test_raw_launches();
+        std::printf("raw launches done\n");
         test_fp32_layouts();
         std::printf("fp32 layouts done\n");
         test_backward_fusion();
