@@ -42,6 +42,7 @@
 #ifndef LOGOS_VEDIC_H
 #define LOGOS_VEDIC_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -120,6 +121,22 @@ typedef struct {
 /* The general entry point.  New: the reference has no single descriptor
  * call; every function below forwards to it. */
 int vedic_gemm(const vedic_gemm_desc_t* desc);
+
+/* vedic_gemm that allocates nothing, for callers that cannot call hipMalloc
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).  No counterpart in the reference.  Same semantics, kernels and
+ * results as vedic_gemm; the temporary memory vedic_gemm takes from the
+ * stream-ordered pool (split-K partial slabs, column partials, the AMP cast
+ * buffer) comes instead from a fixed per-GPU region of
+ * vedic_noalloc_scratch_bytes() bytes (32 MiB) compiled into the library and
+ * held until the process ends.  A call that needs more returns
+ * VEDIC_STATUS_TOO_LARGE before launching anything that writes C.  Every call
+ * on one GPU shares that region: calls that overlap on one GPU (two streams,
+ * two host threads) race, so serialise them. */
+int vedic_gemm_noalloc(const vedic_gemm_desc_t* desc);
+
+/* Size of the region vedic_gemm_noalloc draws from (per GPU). */
+size_t vedic_noalloc_scratch_bytes(void);
 
 /* ---- reference-compatible entry points ------------------------------- */
 

@@ -58,6 +58,35 @@ static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; 
 // Largest leading dimension (elements) the kernels' 32-bit tile offsets allow.
 static constexpr int64_t kMaxLd = int64_t(1) << 22;
 
+// Temporary device memory of one library call (split-K partial slabs, column
+// partials, an AMP cast buffer).  By default each piece is taken from the
+// device's stream-ordered pool (hipMallocAsync on the call's stream) and
+// returned to it the same way.  Bound to a fixed region instead (the
+// allocation-free entry point), pieces are carved from it in order and
+// nothing is allocated or freed; a request past its end sets `overflow` and
+// fails, and the call reports VEDIC_STATUS_TOO_LARGE.
+struct Workspace {
+    hipStream_t s = nullptr;
+    char* region = nullptr;  // non-null: carve from [region, region + cap)
+    size_t cap = 0, used = 0;
+    bool overflow = false;
+
+    bool fixed() const { return region != nullptr; }
+    template <typename T>
+    hipError_t get(T** p, size_t bytes) {
+        if (!fixed()) return hipMallocAsync(reinterpret_cast<void**>(p), bytes, s);
+        const size_t take = (bytes + 255) / 256 * 256;
+        if (take > cap - used) {
+            overflow = true;
+            return hipErrorOutOfMemory;
+        }
+        *p = reinterpret_cast<T*>(region + used);
+        used += take;
+        return hipSuccess;
+    }
+    hipError_t put(void* p) { return fixed() || !p ? hipSuccess : hipFreeAsync(p, s); }
+};
+
 // ------------------------------------------------------------ split-K
 
 // C = epi(alpha * sum_s ws[s] + beta * C_old + bias), the slices added in
@@ -146,17 +175,29 @@ static hipError_t launch_colsum_reduce(const float* part, int nblocks, int N, fl
 
 // Column sums of an M x N fp32 matrix through a stream-ordered workspace of
 // ceil(M / 64) x N partial sums.
-static hipError_t colsum_matrix(const float* X, int64_t ldx, int M, int N, float* out, float beta, hipStream_t s) {
-    constexpr int RB = 64;
-    const int nb = (M + RB - 1) / RB;
-    float* part = nullptr;
-    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&part), sizeof(float) * (size_t)nb * N, s);
-    if (e != hipSuccess) return e;
+constexpr int kColsumRows = 64;  // rows per partial of colsum_matrix
+
+// Floats of partial sums colsum_matrix needs for an M x N matrix.
+static size_t colsum_matrix_floats(int M, int N) { return (size_t)((M + kColsumRows - 1) / kColsumRows) * N; }
+
+// Column sums of an M x N fp32 matrix through `part`, a workspace of
+// colsum_matrix_floats(M, N) partial sums.
+static hipError_t colsum_matrix_into(const float* X, int64_t ldx, int M, int N, float* out, float beta, float* part,
+                                     hipStream_t s) {
+    const int nb = (M + kColsumRows - 1) / kColsumRows;
     hipLaunchKernelGGL(colsum_partial_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)nb), dim3(256), 0, s, X,
-                       ldx, M, N, RB, part);
-    e = hipGetLastError();
+                       ldx, M, N, kColsumRows, part);
+    hipError_t e = hipGetLastError();
     if (e == hipSuccess) e = launch_colsum_reduce(part, nb, N, out, beta, s);
-    const hipError_t f = hipFreeAsync(part, s);
+    return e;
+}
+
+static hipError_t colsum_matrix(const float* X, int64_t ldx, int M, int N, float* out, float beta, Workspace& ws) {
+    float* part = nullptr;
+    hipError_t e = ws.get(&part, sizeof(float) * colsum_matrix_floats(M, N));
+    if (e != hipSuccess) return e;
+    e = colsum_matrix_into(X, ldx, M, N, out, beta, part, ws.s);
+    const hipError_t f = ws.put(part);
     return e != hipSuccess ? e : f;
 }
 
@@ -259,11 +300,12 @@ static hipError_t launch_f16_direct(int op, const GemmArgs& a, hipStream_t s) {
 
 // Runs the product as `ks` slices into a stream-ordered workspace, then the
 // reduction with the caller's epilogue.
-static hipError_t launch_split(bool f16, int op, bool vec, const GemmArgs& a, int ks, hipStream_t s) {
+static hipError_t launch_split(bool f16, int op, bool vec, const GemmArgs& a, int ks, Workspace& wsp) {
+    hipStream_t s = wsp.s;
     const int kslice = split_kslice(a.K, ks, f16);
     const int64_t total = (int64_t)a.M * a.N;
     float* ws = nullptr;
-    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), sizeof(float) * (size_t)total * ks, s);
+    hipError_t e = wsp.get(&ws, sizeof(float) * (size_t)total * ks);
     if (e != hipSuccess) return e;
     GemmArgs p = a;
     p.C = ws;
@@ -289,7 +331,7 @@ static hipError_t launch_split(bool f16, int op, bool vec, const GemmArgs& a, in
         hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s, ws, ks, a);
         e = hipGetLastError();
     }
-    const hipError_t f = hipFreeAsync(ws, s);
+    const hipError_t f = wsp.put(ws);
     return e != hipSuccess ? e : f;
 }
 
@@ -329,10 +371,12 @@ struct ColsumHandoff {
 };
 
 static int amp_via_cast(const vedic_gemm_desc_t* d, float* const* heads, int nheads, int head_cols,
-                        ColsumHandoff* handoff);
+                        ColsumHandoff* handoff, Workspace* wsp);
 
+// wsp: where the call's temporary memory comes from (null: the stream-ordered
+// pool of the call's stream).
 static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads, int head_cols,
-                     ColsumHandoff* handoff = nullptr) {
+                     ColsumHandoff* handoff = nullptr, Workspace* wsp = nullptr) {
     if (!d) return VEDIC_STATUS_NULL_POINTER;
     if (d->M <= 0 || d->N <= 0 || d->K <= 0) return VEDIC_STATUS_BAD_DIM;
     const bool scatter = nheads > 0;
@@ -420,7 +464,7 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
     const bool f16 = d->in_dtype != VEDIC_DT_F32;
     // (an fp32 A's tile rows are twice as long in bytes)
     const bool direct = vec && d->lda < (amp ? kMaxLd / 2 : kMaxLd) && d->ldb < kMaxLd;
-    if (amp && (!direct || d->N > kAmpInKernelMaxN)) return amp_via_cast(d, heads, nheads, head_cols, handoff);
+    if (amp && (!direct || d->N > kAmpInKernelMaxN)) return amp_via_cast(d, heads, nheads, head_cols, handoff, wsp);
     // scattered C needs the kernels with a plain or bias epilogue kind
     if (scatter && !direct) return VEDIC_STATUS_BAD_LD;
     const bool skinny = direct && !amp && d->op == VEDIC_OP_NN && d->M <= 32;
@@ -428,26 +472,34 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
     const int ks = skinny || scatter || (f16 && !direct) ? 1 : choose_ksplit(d->M, d->N, d->K, device_cu_count(), f16);
 
     hipStream_t s = static_cast<hipStream_t>(d->stream);
+    Workspace pool;
+    pool.s = s;
+    Workspace& ws = wsp ? *wsp : pool;
     hipError_t e = hipSuccess;
     // Column sums: the fused epilogue writes one partial per 32-row block and
     // column, added afterwards in a fixed order.  A split product sums the
     // finished C instead.
     float* cs_part = nullptr;
     const int cs_blocks = (d->M + 31) / 32;
-    const bool guard = g_ws_guard.load(std::memory_order_relaxed) != 0;
+    const bool guard = !ws.fixed() && g_ws_guard.load(std::memory_order_relaxed) != 0;
     const int64_t guard_n = (int64_t)kGuardRows * d->N;  // guard words past the partials
+    float* split_cs = nullptr;  // a split product sums the finished C through these partials
+    if (d->colsum && ks > 1) {
+        e = ws.get(&split_cs, sizeof(float) * colsum_matrix_floats(d->M, d->N));
+        if (e != hipSuccess) return ws.overflow ? VEDIC_STATUS_TOO_LARGE : hip_status(e);
+    }
     if (d->colsum && ks == 1) {
         // with the guard: partials | guard rows | one hit counter
         const size_t bytes = sizeof(float) * (size_t)cs_blocks * d->N + (guard ? 4 * (size_t)guard_n + 4 : 0);
-        e = hipMallocAsync(reinterpret_cast<void**>(&cs_part), bytes, s);
-        if (e != hipSuccess) return hip_status(e);
+        e = ws.get(&cs_part, bytes);
+        if (e != hipSuccess) return ws.overflow ? VEDIC_STATUS_TOO_LARGE : hip_status(e);
         a.cs_part = cs_part;
         if (guard) {
             uint32_t* g = reinterpret_cast<uint32_t*>(cs_part + (size_t)cs_blocks * d->N);
             hipLaunchKernelGGL(guard_fill_kernel, dim3(64), dim3(256), 0, s, g, guard_n);
             e = hipGetLastError();
             if (e != hipSuccess) {
-                (void)hipFreeAsync(cs_part, s);
+                (void)ws.put(cs_part);
                 return hip_status(e);
             }
         }
@@ -462,7 +514,7 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
         if (!f16 && direct && ks2 == 2 && a.epi_kind == EK_PLAIN)
             e = launch_split2_atomic(d->op, a, kslice, s);
         else
-            e = launch_split(f16, kop, vec, a, ks, s);
+            e = launch_split(f16, kop, vec, a, ks, ws);
     } else if (f16 && direct) {
         e = launch_f16_direct(kop, a, s);
     } else if (f16) {
@@ -489,13 +541,18 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
         if (cs_part)
             e = launch_colsum_reduce(cs_part, cs_blocks, d->N, d->colsum, d->colsum_beta, s);
         else
-            e = colsum_matrix(static_cast<const float*>(d->C), d->ldc, d->M, d->N, d->colsum, d->colsum_beta, s);
+            e = colsum_matrix_into(static_cast<const float*>(d->C), d->ldc, d->M, d->N, d->colsum, d->colsum_beta,
+                                   split_cs, s);
     }
     if (cs_part) {
-        const hipError_t f = hipFreeAsync(cs_part, s);
+        const hipError_t f = ws.put(cs_part);
         if (e == hipSuccess) e = f;
     }
-    return hip_status(e);
+    if (split_cs) {
+        const hipError_t f = ws.put(split_cs);
+        if (e == hipSuccess) e = f;
+    }
+    return ws.overflow ? VEDIC_STATUS_TOO_LARGE : hip_status(e);
 }
 
 // dst[r][c] = binary16(clamp(src[r][c])) for an M x K fp32 matrix with
@@ -511,11 +568,14 @@ __global__ void cast_rows_f16_kernel(const float* __restrict__ src, int64_t lds,
 // rows): A is cast into a stream-ordered binary16 workspace first, as the
 // reference casts into a per-call buffer (cuda/ModelGPU.cu:825-827).
 static int amp_via_cast(const vedic_gemm_desc_t* d, float* const* heads, int nheads, int head_cols,
-                        ColsumHandoff* handoff) {
+                        ColsumHandoff* handoff, Workspace* wsp) {
     hipStream_t s = static_cast<hipStream_t>(d->stream);
+    Workspace pool;
+    pool.s = s;
+    Workspace& ws = wsp ? *wsp : pool;
     _Float16* a16 = nullptr;
-    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&a16), sizeof(_Float16) * (size_t)d->M * d->K, s);
-    if (e != hipSuccess) return hip_status(e);
+    hipError_t e = ws.get(&a16, sizeof(_Float16) * (size_t)d->M * d->K);
+    if (e != hipSuccess) return ws.overflow ? VEDIC_STATUS_TOO_LARGE : hip_status(e);
     hipLaunchKernelGGL(cast_rows_f16_kernel, dim3((unsigned)(d->M < 4096 ? d->M : 4096)), dim3(256), 0, s,
                        static_cast<const float*>(d->A), d->lda, a16, d->M, d->K);
     e = hipGetLastError();
@@ -525,13 +585,52 @@ static int amp_via_cast(const vedic_gemm_desc_t* d, float* const* heads, int nhe
         g.in_dtype = VEDIC_DT_F16;
         g.A = a16;
         g.lda = d->K;
-        st = gemm_impl(&g, heads, nheads, head_cols, handoff);
+        st = gemm_impl(&g, heads, nheads, head_cols, handoff, &ws);
     }
-    const hipError_t f = hipFreeAsync(a16, s);
+    const hipError_t f = ws.put(a16);
     return st != VEDIC_STATUS_OK ? st : hip_status(f);
 }
 
 extern "C" int vedic_gemm(const vedic_gemm_desc_t* d) { return gemm_impl(d, nullptr, 0, 0); }
+
+// ---------------------------------------- the entry point that allocates nothing
+
+// The temporary memory of vedic_gemm_noalloc: one array per GPU, held until
+// the process ends.  Host code never passes `scratch` itself (its host-side
+// name is not a device address); it uses the address hipGetSymbolAddress
+// returns for the current device, looked up once per device and kept.
+static constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+static std::atomic<char*> g_scratch_ptr[64];
+
+static hipError_t scratch_region(char** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    char* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        void* q = nullptr;
+        e = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        p = static_cast<char*>(q);
+        g_scratch_ptr[dev].store(p, std::memory_order_release);  // the same address if two threads race here
+    }
+    *out = p;
+    return hipSuccess;
+}
+
+extern "C" int vedic_gemm_noalloc(const vedic_gemm_desc_t* d) {
+    if (!d) return VEDIC_STATUS_NULL_POINTER;
+    Workspace ws;
+    ws.s = static_cast<hipStream_t>(d->stream);
+    hipError_t e = scratch_region(&ws.region);
+    if (e != hipSuccess) return hip_status(e);
+    ws.cap = kScratchBytes;
+    return gemm_impl(d, nullptr, 0, 0, nullptr, &ws);
+}
+
+extern "C" size_t vedic_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
 extern "C" void vedic_debug_set_workspace_guard(int on) { g_ws_guard.store(on ? 1 : 0); }
 
@@ -695,7 +794,9 @@ extern "C" int vedic_gemm_nt_gelu_bwd_f32(const float* dY, const float* W, const
 extern "C" int vedic_bias_grad(const float* dY, float* db, int M, int N, float beta, void* stream) {
     if (!dY || !db) return VEDIC_STATUS_NULL_POINTER;
     if (M <= 0 || N <= 0) return VEDIC_STATUS_BAD_DIM;
-    return hip_status(colsum_matrix(dY, N, M, N, db, beta, static_cast<hipStream_t>(stream)));
+    Workspace pool;
+    pool.s = static_cast<hipStream_t>(stream);
+    return hip_status(colsum_matrix(dY, N, M, N, db, beta, pool));
 }
 
 // ----------------------------------------------------------- elementwise

@@ -1,0 +1,101 @@
+"""vedic_gemm_noalloc: the GEMM entry point that allocates nothing.
+
+It runs the same kernels as vedic_gemm, with the temporary memory (split-K
+partial slabs, column partials, the AMP cast buffer) carved from a fixed
+per-GPU region compiled into the library instead of the stream-ordered pool.
+Each case calls it through the C ABI twice in a row, the second time on a
+smaller problem (the region keeps the first call's contents), and compares
+both results with vedic_gemm's bit for bit; a problem whose temporaries do not
+fit is refused with VEDIC_STATUS_TOO_LARGE and leaves C untouched."""
+import ctypes
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from logos_amd import _lib  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(fn, op, in_dtype, M, N, K, A, B, C, *, beta=0.0, epilogue=_lib.EPI_NONE, bias=None, preact=None,
+         colsum=None, colsum_beta=0.0):
+    d = _lib.GemmDesc(op=op, in_dtype=in_dtype, out_dtype=_lib.DT_F32, M=M, N=N, K=K,
+                      A=A.data_ptr(), lda=A.shape[1], B=B.data_ptr(), ldb=B.shape[1], C=C.data_ptr(), ldc=N,
+                      alpha=1.0, beta=beta, bias=bias.data_ptr() if bias is not None else None, epilogue=epilogue,
+                      preact=preact.data_ptr() if preact is not None else None,
+                      ld_preact=N if preact is not None else 0, stream=torch.cuda.current_stream().cuda_stream,
+                      colsum=colsum.data_ptr() if colsum is not None else None, colsum_beta=colsum_beta)
+    return fn(ctypes.byref(d))
+
+
+def _pair(lib, case, M, N, K, seed):
+    """(noalloc C, vedic_gemm C[, noalloc colsum, vedic_gemm colsum]) for one case."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    r = lambda *s, std=1.0: torch.randn(*s, generator=g, device="cuda") * std  # noqa: E731
+    if case == "splitk_tn_f16":  # few tiles over a long K: split into slices, beta = 1
+        A, B = r(K, M).half(), r(K, N, std=1e-2).half()
+        C0 = r(M, N, std=1e-3)
+        args = dict(op=_lib.OP_TN, in_dtype=_lib.DT_F16, beta=1.0)
+    elif case == "gelu_bwd_colsum":  # column partials of every 32-row block
+        A, B = r(M, K, std=1e-3).half(), r(N, K, std=0.02).half()
+        C0 = torch.zeros(M, N, device="cuda")
+        args = dict(op=_lib.OP_NT, in_dtype=_lib.DT_F16, epilogue=_lib.EPI_GELU_BWD, preact=r(M, N, std=2.0))
+    elif case == "splitk_f32_colsum":  # split fp32 product, column sums over the finished C
+        A, B = r(M, K), r(K, N, std=0.02)
+        C0 = torch.zeros(M, N, device="cuda")
+        args = dict(op=_lib.OP_NN, in_dtype=_lib.DT_F32, epilogue=_lib.EPI_BIAS, bias=r(N, std=0.1))
+    elif case == "amp_cast":  # fp32 activation, wide N: cast into the region first
+        A, B = r(M, K), r(K, N, std=0.02).half()
+        C0 = torch.zeros(M, N, device="cuda")
+        args = dict(op=_lib.OP_NN, in_dtype=_lib.DT_F32_F16, epilogue=_lib.EPI_BIAS_GELU, bias=r(N, std=0.01))
+    else:
+        raise ValueError(case)
+    want_cs = case in ("gelu_bwd_colsum", "splitk_f32_colsum")
+    out = []
+    for fn in (lib.vedic_gemm_noalloc, lib.vedic_gemm):
+        C = C0.clone()
+        cs = torch.full((N,), 0.5, device="cuda") if want_cs else None
+        rc = _run(fn, M=M, N=N, K=K, A=A, B=B, C=C, colsum=cs, colsum_beta=1.0 if want_cs else 0.0, **args)
+        assert rc == _lib.STATUS_OK, f"{case} {M}x{N}x{K}: {_lib.status_string(rc)}"
+        out.append((C, cs))
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("case,big,small", [
+    ("splitk_tn_f16", (1024, 1024, 8192), (512, 256, 4096)),
+    ("gelu_bwd_colsum", (8192, 4096, 1024), (1000, 520, 256)),
+    ("splitk_f32_colsum", (256, 512, 8192), (128, 192, 2048)),
+    ("amp_cast", (4096, 2048, 1024), (300, 1536, 520)),
+])
+def test_noalloc_matches_vedic_gemm(case, big, small):
+    lib = _lib.load()
+    for i, (M, N, K) in enumerate((big, small)):
+        print(f"noalloc {case} {M}x{N}x{K}", flush=True)
+        (c1, s1), (c2, s2) = _pair(lib, case, M, N, K, seed=100 * i + len(case))
+        assert torch.equal(c1, c2), f"{case} {M}x{N}x{K}: C differs from vedic_gemm"
+        if s1 is not None:
+            assert torch.equal(s1, s2), f"{case} {M}x{N}x{K}: column sums differ"
+
+
+def test_noalloc_refuses_what_does_not_fit():
+    lib = _lib.load()
+    cap = lib.vedic_noalloc_scratch_bytes()
+    assert cap == 32 << 20
+    # an fp32 activation of 8192 x 4096 cast for a wide product needs 64 MiB
+    M, K, N = 8192, 4096, 2048
+    A = torch.randn(M, K, device="cuda")
+    B = (torch.randn(K, N, device="cuda") * 0.02).half()
+    C = torch.full((M, N), 7.0, device="cuda")
+    rc = _run(lib.vedic_gemm_noalloc, _lib.OP_NN, _lib.DT_F32_F16, M, N, K, A, B, C)
+    assert rc == _lib.STATUS_TOO_LARGE
+    torch.cuda.synchronize()
+    assert bool((C == 7.0).all()), "a refused call wrote C"
+    # the same call through vedic_gemm runs (pool workspace), and a fitting one after the refusal still does
+    assert _run(lib.vedic_gemm, _lib.OP_NN, _lib.DT_F32_F16, M, N, K, A, B, C) == _lib.STATUS_OK
+    (c1, _), (c2, _) = _pair(lib, "splitk_tn_f16", 1024, 1024, 8192, seed=5)
+    assert torch.equal(c1, c2)
+    assert lib.vedic_gemm_noalloc(None) == _lib.STATUS_NULL_POINTER
