@@ -19,10 +19,12 @@ The default run prints one JSON line with the metric named in BASELINE.json plus
                 `traffic` is the HBM bytes per launch from the committed
                 rocprofv3 FETCH_SIZE / WRITE_SIZE summary, scaled by a copy
                 kernel of known size (None when no summary is committed);
-  cpu_baseline  the reference CPU path -- the reference's own vedic_gemm_bias +
-                gelu built from its sources into oracle/_ref when that was built,
-                else the bitwise restatement in oracle/ -- on a bounded sample of
-                the same workload, single-threaded as the reference is.
+  cpu_baseline  the reference CPU path on a bounded sample of the same workload:
+                all host cores (at most 16) running the bitwise restatement in
+                oracle/ sharded by 64-row blocks as `value`, and one thread (the
+                reference's own vedic_gemm built from its sources into
+                oracle/_ref where that exists, else the restatement) beside it
+                in `single_thread`, with the CPU model.
 """
 from __future__ import annotations
 
@@ -259,14 +261,36 @@ def cpu_baseline_attn(w: dict, seconds: float, seed: int = 7):
     }
 
 
-def cpu_baseline(w: dict, seconds: float, seed: int = 7):
-    """The reference CPU path (single thread) on a row sample of the workload's
-    GEMMs, repeated until about `seconds` of CPU time.  Rows of every GEMM are
-    independent and cost the same, so TFLOP/s over a row sample is the rate
-    of the whole GEMM."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def baseline_threads() -> int:
+    """Host threads for the all-cores CPU baseline: the cores this process may
+    use, at most 16 (the host share of one GPU on the GPU boxes)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def _cpu_gemm_sample(w: dict, seconds: float, nthreads: int, seed: int):
+    """(flops, seconds, kind, parts): the reference CPU path on row samples of
+    the workload's GEMMs, repeated until about `seconds`.  One thread runs the
+    reference's own vedic_gemm built in place when that exists (oracle/_ref),
+    else the bitwise restatement; several threads run the restatement sharded
+    by 64-row blocks (the same bits, each element summed in the same order)."""
     from oracle import oracle as o
 
-    kind = "reference" if o.ref_available() else "port"
+    kind = "reference" if nthreads == 1 and o.ref_available() else "port"
     rng = np.random.default_rng(seed)
     per_gemm = max(seconds / len(w["gemms"]), 0.5)
     total_flops = 0.0
@@ -274,8 +298,11 @@ def cpu_baseline(w: dict, seconds: float, seed: int = 7):
     parts = []
     for g in w["gemms"]:
         M, K, N, op = g["M"], g["K"], g["N"], g["op"]
-        # ~20 GFLOP/s single thread: rows for about per_gemm seconds, 1..M
-        rows = int(max(1, min(M, 2.0e10 * per_gemm / (2.0 * K * N))))
+        # ~20 GFLOP/s per thread: rows for about per_gemm seconds, 1..M
+        rows = int(max(1, min(M, 2.0e10 * nthreads * per_gemm / (2.0 * K * N))))
+        if nthreads > 1:
+            rows = max(64, rows // 64 * 64) if M >= 64 else rows
+            rows = min(rows, M)
         A = rng.standard_normal((rows, K), dtype=np.float32)
         B = (rng.standard_normal((K, N), dtype=np.float32) * np.float32(0.02))
         bias = (rng.standard_normal(N, dtype=np.float32) * np.float32(0.01))
@@ -303,12 +330,12 @@ def cpu_baseline(w: dict, seconds: float, seed: int = 7):
                     o.ref_bias_backward(C)
             else:
                 if op == "NN":
-                    C = (o.vedic_gemm_bias(A, B, bias, nthreads=1) if g["epi"] in ("bias", "bias_gelu")
-                         else o.vedic_gemm(A, B, nthreads=1))
+                    C = (o.vedic_gemm_bias(A, B, bias, nthreads=nthreads) if g["epi"] in ("bias", "bias_gelu")
+                         else o.vedic_gemm(A, B, nthreads=nthreads))
                 elif op == "NT":
-                    C = o.gemm_nt(A, B, nthreads=1)
+                    C = o.gemm_nt(A, B, nthreads=nthreads)
                 else:
-                    C = o.gemm_tn(A, B, nthreads=1)
+                    C = o.gemm_tn(A, B, nthreads=nthreads)
                 if g["epi"] == "bias_gelu":
                     C = o.gelu(C)
                 if g["epi"] == "gelu_bwd":
@@ -321,13 +348,28 @@ def cpu_baseline(w: dict, seconds: float, seed: int = 7):
         total_flops += reps * 2.0 * rows * K * N
         total_t += dt
         parts.append(f"{op} {rows}/{M} rows x{reps}")
+    return total_flops, total_t, kind, parts
+
+
+def cpu_baseline(w: dict, seconds: float, seed: int = 7):
+    """The reference CPU path on row samples of the workload's GEMMs: all host
+    cores (the restatement, sharded by 64-row blocks) as `value`, and one
+    thread (the reference's algorithm as written) beside it, each for about
+    half of `seconds`.  Rows of every GEMM are independent and cost the same,
+    so TFLOP/s over a row sample is the rate of the whole GEMM."""
+    n = baseline_threads()
+    f1, t1, k1, p1 = _cpu_gemm_sample(w, seconds / 2, 1, seed)
+    fn, tn, kn, pn = _cpu_gemm_sample(w, seconds / 2, n, seed)
+    flags = "-O3 -march=x86-64 -ffp-contract=off"
     return {
-        "value": total_flops / total_t / 1e12,
+        "value": fn / tn / 1e12,
         "unit": "TFLOP/s",
-        "cores": 1,
-        "kind": kind,
-        "sample": f"{'; '.join(parts)} ({total_flops / 1e9:.1f} GFLOP in {total_t:.1f} s), single thread, "
-                  f"reference flags -O3 -march=x86-64",
+        "cores": n,
+        "kind": kn,
+        "sample": f"{'; '.join(pn)} ({fn / 1e9:.1f} GFLOP in {tn:.1f} s), {n} threads by 64-row blocks, {flags}",
+        "single_thread": {"value": f1 / t1 / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": k1,
+                          "sample": f"{'; '.join(p1)} ({f1 / 1e9:.1f} GFLOP in {t1:.1f} s), {flags}"},
+        "cpu_model": cpu_model(),
         "threads_available": os.cpu_count(),
     }
 
