@@ -250,34 +250,6 @@ static int split_kslice(int K, int& ks, bool f16) {
     return kslice;
 }
 
-__global__ void zero_rows_kernel(float* __restrict__ C, int64_t ldc, int M, int N) {
-    for (int r = blockIdx.x; r < M; r += gridDim.x) {
-        float* row = C + (int64_t)r * ldc;
-        for (int c = threadIdx.x; c < N; c += blockDim.x) row[c] = 0.0f;
-    }
-}
-
-// A plain fp32 product in two contraction slices: C is zeroed, then both
-// slices add their raw partials into it with fp32 atomic adds.  The sum is
-// the same whichever slice lands first (0 + a + b = a + b = b + a in IEEE
-// arithmetic), so the result is deterministic, and neither a workspace nor a
-// reduction pass is needed.
-static hipError_t launch_split2_atomic(int op, const GemmArgs& a, int kslice, hipStream_t s) {
-    const int blocks = a.M < 4096 ? a.M : 4096;  // one row per workgroup and step
-    hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s, static_cast<float*>(a.C), a.ldc,
-                       a.M, a.N);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    GemmArgs p = a;
-    p.epi_kind = EK_ATOMIC;
-    p.ksplit = 2;
-    p.kslice = kslice;
-    p.c_split_stride = 0;
-    return op == VEDIC_OP_NN   ? launch_gemm_f32_direct_nn(p, s)
-           : op == VEDIC_OP_NT ? launch_gemm_f32_direct_nt(p, s)
-                               : launch_gemm_f32_direct_tn(p, s);
-}
-
 // The 16-byte-load fp16 kernels; op kOpAmp is NN with an fp32 A converted to
 // binary16 on its way into the kernel.
 constexpr int kOpAmp = 3;
@@ -469,7 +441,11 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
     if (scatter && !direct) return VEDIC_STATUS_BAD_LD;
     const bool skinny = direct && !amp && d->op == VEDIC_OP_NN && d->M <= 32;
     const int kop = amp ? kOpAmp : d->op;  // the fp16 kernels' op
-    const int ks = skinny || scatter || (f16 && !direct) ? 1 : choose_ksplit(d->M, d->N, d->K, device_cu_count(), f16);
+    // (fp32 products that the wave-split 32 x 64 tiles fill are not split over workgroups)
+    const bool wave_split = !f16 && direct && d->op != VEDIC_OP_TN && f32_wave_split(d->M, d->N, device_cu_count());
+    const int ks = skinny || scatter || wave_split || (f16 && !direct)
+                       ? 1
+                       : choose_ksplit(d->M, d->N, d->K, device_cu_count(), f16);
 
     hipStream_t s = static_cast<hipStream_t>(d->stream);
     Workspace pool;
@@ -509,12 +485,7 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
         // decode-time shapes: bound by streaming B once from HBM
         e = f16 ? launch_gemm_f16_skinny(a, s) : launch_gemm_f32_skinny(a, s);
     } else if (ks > 1) {
-        int ks2 = ks;
-        const int kslice = split_kslice(d->K, ks2, f16);
-        if (!f16 && direct && ks2 == 2 && a.epi_kind == EK_PLAIN)
-            e = launch_split2_atomic(d->op, a, kslice, s);
-        else
-            e = launch_split(f16, kop, vec, a, ks, ws);
+        e = launch_split(f16, kop, vec, a, ks, ws);
     } else if (f16 && direct) {
         e = launch_f16_direct(kop, a, s);
     } else if (f16) {

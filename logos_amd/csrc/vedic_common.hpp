@@ -88,6 +88,18 @@ inline bool f32_small_tiles(int M, int N, int cus) {
     return N > 64 && (int64_t)((M + 127) / 128) * ((N + 127) / 128) * 2 <= cus;
 }
 
+// fp32 products whose 64 x 64 tiles still number fewer than the CUs but whose
+// 32 x 64 tiles number at least half of them (512 x 1024:
+// 128 and 256 tiles): one 32 x 64 tile per workgroup, its contraction split
+// four ways among the workgroup's waves and the four partials added through
+// LDS in a fixed order -- no split over workgroups, no workspace, no atomics.
+inline bool f32_wave_split(int M, int N, int cus) {
+    if (!f32_small_tiles(M, N, cus)) return false;
+    const int64_t t64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64);
+    const int64_t t32 = (int64_t)((M + 31) / 32) * ((N + 63) / 64);
+    return t64 < cus && t32 * 2 >= cus;
+}
+
 struct GemmArgs {
     const void* A;
     const void* B;

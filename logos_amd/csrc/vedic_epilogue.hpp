@@ -26,7 +26,6 @@ enum EpiKind : int {
     EK_GENERIC = 5,        // any flag combination (runtime flags)
     EK_GELU_BWD = 6,       // C = acc * gelu'(P)    (+ column sums if cs_part)
     EK_LINEAR_CS = 7,      // C = alpha acc (+ b), with column sums
-    EK_ATOMIC = 8,         // C += acc by fp32 atomic adds: two contraction slices into a zeroed C
 };
 
 __host__ __device__ inline int epi_kind_of(int epi, float alpha, float beta) {
@@ -50,11 +49,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p) {
 
 __device__ __forceinline__ void st_f32(float v, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rs, (int)voff, (int)soff, 0);
-}
-
-// Atomic add without return; an out-of-range offset (kOob) drops it.
-__device__ __forceinline__ void atomic_add_f32(float v, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v, rs, (int)voff, (int)soff, 0);
 }
 
 __device__ __forceinline__ float ld_f32(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
@@ -183,8 +177,6 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, void* Cp, const floa
                 float v = acc[i][j][e];
                 if constexpr (KIND == EK_PLAIN) {
                     st_f32(v, rc, oc, sc);
-                } else if constexpr (KIND == EK_ATOMIC) {
-                    atomic_add_f32(v, rc, oc, sc);
                 } else if constexpr (KIND == EK_BIAS) {
                     st_f32(v + bj, rc, oc, sc);
                 } else if constexpr (KIND == EK_BIAS_GELU) {

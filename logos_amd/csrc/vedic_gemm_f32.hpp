@@ -102,26 +102,28 @@ __device__ __forceinline__ float4_t read_frag32(const char* lds, int rc0, int cc
     }
 }
 
-// The MFMAs of one 32-k stage, fragments double buffered across the four
-// chunks (reads of chunk cc + 1 interleaved with the MFMAs of chunk cc).
-template <bool A_KC, bool B_KC, int BM, int BN, int MI, int NI>
+// The MFMAs of one 32-k stage, fragments double buffered across its chunks
+// (reads of chunk cc + 1 interleaved with the MFMAs of chunk cc).  A wave
+// whose workgroup splits the contraction among WGK waves takes the CN = 4 /
+// WGK chunks from c0 on.
+template <bool A_KC, bool B_KC, int BM, int BN, int MI, int NI, int CN = 4>
 __device__ __forceinline__ void mfma_stage32(const char* la, const char* lb, int ar0, int bc0, int lane,
-                                             float16_t (&acc)[MI][NI]) {
+                                             float16_t (&acc)[MI][NI], int c0 = 0) {
     constexpr int NR = (A_KC ? MI : 4 * MI) + (B_KC ? NI : 4 * NI);  // LDS reads per chunk
     constexpr int NM = 4 * MI * NI;                                  // MFMAs per chunk
     float4_t af[2][MI], bf[2][NI];
 #pragma unroll
-    for (int i = 0; i < MI; ++i) af[0][i] = read_frag32<A_KC, BM>(la, ar0 + 32 * i, 0, lane);
+    for (int i = 0; i < MI; ++i) af[0][i] = read_frag32<A_KC, BM>(la, ar0 + 32 * i, c0, lane);
 #pragma unroll
-    for (int j = 0; j < NI; ++j) bf[0][j] = read_frag32<B_KC, BN>(lb, bc0 + 32 * j, 0, lane);
+    for (int j = 0; j < NI; ++j) bf[0][j] = read_frag32<B_KC, BN>(lb, bc0 + 32 * j, c0, lane);
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
+    for (int cc = 0; cc < CN; ++cc) {
         const int c = cc & 1, n = c ^ 1;
-        if (cc + 1 < 4) {
+        if (cc + 1 < CN) {
 #pragma unroll
-            for (int i = 0; i < MI; ++i) af[n][i] = read_frag32<A_KC, BM>(la, ar0 + 32 * i, cc + 1, lane);
+            for (int i = 0; i < MI; ++i) af[n][i] = read_frag32<A_KC, BM>(la, ar0 + 32 * i, c0 + cc + 1, lane);
 #pragma unroll
-            for (int j = 0; j < NI; ++j) bf[n][j] = read_frag32<B_KC, BN>(lb, bc0 + 32 * j, cc + 1, lane);
+            for (int j = 0; j < NI; ++j) bf[n][j] = read_frag32<B_KC, BN>(lb, bc0 + 32 * j, c0 + cc + 1, lane);
         }
 #pragma unroll
         for (int s = 0; s < 4; ++s)
@@ -133,7 +135,7 @@ __device__ __forceinline__ void mfma_stage32(const char* la, const char* lb, int
     }
     __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
 #pragma unroll
-    for (int cc = 0; cc + 1 < 4; ++cc) {
+    for (int cc = 0; cc + 1 < CN; ++cc) {
 #pragma unroll
         for (int x = 0; x < (NR < NM ? NR : NM); ++x) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -143,6 +145,40 @@ __device__ __forceinline__ void mfma_stage32(const char* la, const char* lb, int
         if (NM > NR) __builtin_amdgcn_sched_group_barrier(0x008, NM > NR ? NM - NR : 1, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+}
+
+// The fragments of CN chunks of one stage (from chunk c0), read ahead of the
+// MFMAs that use them: with the contraction split among a workgroup's waves
+// (one wave per SIMD, a few MFMAs per stage), the next stage's fragments are
+// read while this stage's MFMAs run, instead of after the barrier.
+template <int MI, int NI, int CN>
+struct StageFrags32 {
+    float4_t a[CN][MI], b[CN][NI];
+};
+
+template <bool A_KC, bool B_KC, int BM, int BN, int MI, int NI, int CN>
+__device__ __forceinline__ void read_stage32(StageFrags32<MI, NI, CN>& f, const char* la, const char* lb, int ar0,
+                                             int bc0, int c0, int lane) {
+#pragma unroll
+    for (int cc = 0; cc < CN; ++cc) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i) f.a[cc][i] = read_frag32<A_KC, BM>(la, ar0 + 32 * i, c0 + cc, lane);
+#pragma unroll
+        for (int j = 0; j < NI; ++j) f.b[cc][j] = read_frag32<B_KC, BN>(lb, bc0 + 32 * j, c0 + cc, lane);
+    }
+}
+
+template <int MI, int NI, int CN>
+__device__ __forceinline__ void mfma_frags32(const StageFrags32<MI, NI, CN>& f, float16_t (&acc)[MI][NI]) {
+#pragma unroll
+    for (int cc = 0; cc < CN; ++cc)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NI; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[cc][i][s], f.b[cc][j][s], acc[i][j], 0, 0, 0);
 }
 
 #define VEDIC_A_TILE32(k) \
@@ -156,10 +192,16 @@ __device__ __forceinline__ void mfma_stage32(const char* la, const char* lb, int
         sb.load(VEDIC_B_TILE32(k_), (lb), wave, lane, it.ke - k_);                       \
     } while (0)
 
-template <int OP, int BM, int BN, int ST, int WGM, int WGN, int KIND>
-__global__ void __launch_bounds__(WGM* WGN * 64) gemm_f32_kernel(GemmArgs args) {
+// WGK > 1: the workgroup's waves form WGK groups of WGM x WGN, group g
+// taking chunks [g CN, (g + 1) CN) of every stage (CN = 4 / WGK); after the
+// contraction groups 1..WGK-1 leave their accumulators in LDS and group 0
+// adds them in group order and runs the epilogue.
+template <int OP, int BM, int BN, int ST, int WGM, int WGN, int KIND, int WGK = 1>
+__global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f32_kernel(GemmArgs args) {
     constexpr int BK = 32;
-    constexpr int NW = WGM * WGN, WM = BM / WGM, WN = BN / WGN, MI = WM / 32, NI = WN / 32;
+    constexpr int NW = WGM * WGN * WGK, WM = BM / WGM, WN = BN / WGN, MI = WM / 32, NI = WN / 32;
+    constexpr int WMN = WGM * WGN, CN = 4 / WGK;
+    static_assert(WGK == 1 || WGK == 2 || WGK == 4, "the contraction splits into 1, 2 or 4 chunk groups");
     constexpr bool A_KC = OP != 2, B_KC = OP == 1;
     using SA = SideF32<A_KC, BM, NW>;
     using SB = SideF32<B_KC, BN, NW>;
@@ -178,10 +220,14 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f32_kernel(GemmArgs args) 
     __shared__ __attribute__((aligned(1024))) char t3[ST > 3 ? SBYTES : 16];
     char* const As[4] = {t0, t1, t2, t3};
     char* const Bs[4] = {t0 + SA::BYTES, t1 + SA::BYTES, t2 + SA::BYTES, t3 + SA::BYTES};
+    // accumulators of chunk groups 1..WGK-1, as float4 per lane
+    constexpr int RED4 = WGK > 1 ? (WGK - 1) * WMN * MI * NI * 4 * 64 : 1;
+    __shared__ __attribute__((aligned(16))) float4_t red[RED4];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int wm = wave / WGN, wn = wave % WGN;
+    const int wk = wave / WMN, wmn = wave % WMN;
+    const int wm = wmn / WGN, wn = wmn % WGN;
     const float* __restrict__ A = static_cast<const float*>(args.A);
     const float* __restrict__ B = static_cast<const float*>(args.B);
     const int K = args.K;
@@ -227,15 +273,71 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f32_kernel(GemmArgs args) 
         // stage kt's loads (with steps of different shapes it falls back to
         // waiting for every load in flight).
         const int nk = it.nk;
-        for (int k0 = 0; k0 < nk; k0 += ST) {
+        if constexpr (WGK == 1) {
+            for (int k0 = 0; k0 < nk; k0 += ST) {
 #pragma unroll
-            for (int s = 0; s < ST; ++s) {
-                const int kt = k0 + s;
-                wait_vmcnt<(ST - 2) * L>();  // stage kt has landed; ST - 2 later stages in flight
-                stage_barrier();
-                const int sl = (s + ST - 1) % ST;
-                VEDIC_ISSUE32(kt + ST - 1, As[sl], Bs[sl]);
-                if (kt < nk) mfma_stage32<A_KC, B_KC, BM, BN, MI, NI>(As[s], Bs[s], wm * WM, wn * WN, lane, acc);
+                for (int s = 0; s < ST; ++s) {
+                    const int kt = k0 + s;
+                    wait_vmcnt<(ST - 2) * L>();  // stage kt has landed; ST - 2 later stages in flight
+                    stage_barrier();
+                    const int sl = (s + ST - 1) % ST;
+                    VEDIC_ISSUE32(kt + ST - 1, As[sl], Bs[sl]);
+                    if (kt < nk) mfma_stage32<A_KC, B_KC, BM, BN, MI, NI>(As[s], Bs[s], wm * WM, wn * WN, lane, acc);
+                }
+            }
+        } else {
+            // Fragments one stage ahead.  Step kt: stage kt + 1 has landed
+            // (stages kt + 2 .. kt + ST - 1 in flight); after the barrier no
+            // wave still reads stage kt's buffer (its fragments were read in
+            // step kt - 1), so stage kt + ST is loaded into it, stage kt + 1's
+            // fragments are read, and stage kt's are multiplied.
+            StageFrags32<MI, NI, CN> fc, fn;
+            wait_vmcnt<(ST - 2) * L>();  // stage 0 (stages 1 .. ST - 2 in flight)
+            stage_barrier();
+            VEDIC_ISSUE32(ST - 1, As[ST - 1], Bs[ST - 1]);
+            read_stage32<A_KC, B_KC, BM, BN, MI, NI, CN>(fc, As[0], Bs[0], wm * WM, wn * WN, wk * CN, lane);
+            for (int k0 = 0; k0 < nk; k0 += ST) {
+#pragma unroll
+                for (int s = 0; s < ST; ++s) {
+                    const int kt = k0 + s;
+                    const int s1 = (s + 1) % ST;
+                    wait_vmcnt<(ST - 2) * L>();
+                    stage_barrier();
+                    VEDIC_ISSUE32(kt + ST, As[s], Bs[s]);
+                    read_stage32<A_KC, B_KC, BM, BN, MI, NI, CN>(fn, As[s1], Bs[s1], wm * WM, wn * WN, wk * CN, lane);
+                    if (kt < nk) mfma_frags32<MI, NI, CN>(fc, acc);
+                    fc = fn;
+                }
+            }
+        }
+        if constexpr (WGK > 1) {
+            // groups 1.. hand their partials to group 0, which adds them in
+            // group order: the same sum whatever the timing
+            if (wk > 0) {
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int j = 0; j < NI; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            red[((((wk - 1) * WMN + wmn) * MI * NI + i * NI + j) * 4 + q) * 64 + lane] =
+                                float4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                         acc[i][j][4 * q + 3]};
+            }
+            __syncthreads();
+            if (wk == 0) {
+#pragma unroll
+                for (int g = 1; g < WGK; ++g)
+#pragma unroll
+                    for (int i = 0; i < MI; ++i)
+#pragma unroll
+                        for (int j = 0; j < NI; ++j)
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                const float4_t v = red[((((g - 1) * WMN + wmn) * MI * NI + i * NI + j) * 4 + q) * 64 + lane];
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += v[e];
+                            }
             }
         }
 
@@ -258,10 +360,12 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f32_kernel(GemmArgs args) 
             for (int s = 0; s < ST - 1; ++s) VEDIC_ISSUE32(s, As[s], Bs[s]);
         }
         const bool full = (row0 + WM <= args.M) && (col0 + WN <= args.N);
-        if (KIND != EK_GENERIC && full)
-            epilogue<KIND, false, MI, NI>(args, cp, acc, row0, col0, lane, pre_bias ? bias_pre : nullptr);
-        else
-            epilogue<KIND, true, MI, NI>(args, cp, acc, row0, col0, lane, pre_bias ? bias_pre : nullptr);
+        if (WGK == 1 || wk == 0) {
+            if (KIND != EK_GENERIC && full)
+                epilogue<KIND, false, MI, NI>(args, cp, acc, row0, col0, lane, pre_bias ? bias_pre : nullptr);
+            else
+                epilogue<KIND, true, MI, NI>(args, cp, acc, row0, col0, lane, pre_bias ? bias_pre : nullptr);
+        }
         if (!more) break;
     }
     wait_vmcnt<0>();  // the trailing zero loads still write LDS
@@ -291,8 +395,18 @@ struct CfgF32Narrow {
     static constexpr int PER_CU = 2;
 };
 
+template <class Cfg, class = void>
+struct WavesK {
+    static constexpr int value = 1;
+};
+template <class Cfg>
+struct WavesK<Cfg, std::void_t<decltype(Cfg::WGK)>> {
+    static constexpr int value = Cfg::WGK;
+};
+
 template <int OP, int KIND, class Cfg>
 static hipError_t launch_f32(GemmArgs a, hipStream_t s) {
+    constexpr int WGK = WavesK<Cfg>::value;
     a.tiles_m = (a.M + Cfg::BM - 1) / Cfg::BM;
     a.tiles_n = (a.N + Cfg::BN - 1) / Cfg::BN;
     if (a.group_m <= 0) a.group_m = 8;
@@ -303,8 +417,8 @@ static hipError_t launch_f32(GemmArgs a, hipStream_t s) {
     const int64_t nwork = (int64_t)a.tiles_m * a.tiles_n * a.ksplit;
     const int64_t slots = (int64_t)device_cu_count() * Cfg::PER_CU;
     const int grid = (int)(nwork < slots ? nwork : slots);
-    hipLaunchKernelGGL((gemm_f32_kernel<OP, Cfg::BM, Cfg::BN, Cfg::ST, Cfg::WGM, Cfg::WGN, KIND>), dim3(grid),
-                       dim3(Cfg::WGM * Cfg::WGN * 64), 0, s, a);
+    hipLaunchKernelGGL((gemm_f32_kernel<OP, Cfg::BM, Cfg::BN, Cfg::ST, Cfg::WGM, Cfg::WGN, KIND, WGK>), dim3(grid),
+                       dim3(Cfg::WGM * Cfg::WGN * WGK * 64), 0, s, a);
     return hipGetLastError();
 }
 
@@ -320,7 +434,6 @@ static hipError_t launch_f32_kind(const GemmArgs& a, hipStream_t s) {
         case EK_ACCUM: return launch_f32<OP, EK_ACCUM, Cfg>(a, s);
         case EK_GELU_BWD: return launch_f32<OP, EK_GELU_BWD, Cfg>(a, s);
         case EK_LINEAR_CS: return launch_f32<OP, EK_LINEAR_CS, Cfg>(a, s);
-        case EK_ATOMIC: return launch_f32<OP, EK_ATOMIC, Cfg>(a, s);
         default: return launch_f32<OP, EK_GENERIC, Cfg>(a, s);
     }
 }
@@ -334,6 +447,16 @@ struct CfgF32Small {
     static constexpr int PER_CU = 2;
 };
 
+// One 32 x 64 tile per workgroup, the contraction split four ways among its
+// four waves (f32_wave_split; NN and NT, whose A rows are K-contiguous): each
+// wave owns the whole 32 x 64 output block (two accumulator chains) over one
+// 8-k chunk of every 32-k stage.  Four 12 KiB stages plus 24 KiB for the
+// partials.
+struct CfgF32WaveK {
+    static constexpr int BM = 32, BN = 64, ST = 4, WGM = 1, WGN = 1, WGK = 4;
+    static constexpr int PER_CU = 2;
+};
+
 static_assert(CfgF32Narrow::BN == 64, "f32_small_tiles assumes the narrow tile's 64 columns");
 
 // Narrow tiles when N fits one 64-wide tile column; small ones when 128 x 128
@@ -341,6 +464,10 @@ static_assert(CfgF32Narrow::BN == 64, "f32_small_tiles assumes the narrow tile's
 template <int OP>
 hipError_t launch_gemm_f32_direct_op(const GemmArgs& a, hipStream_t s) {
     if (a.N <= CfgF32Narrow::BN) return launch_f32_kind<OP, CfgF32Narrow>(a, s);
+    if constexpr (OP != 2) {  // (TN's A is M-contiguous: its LDS rows need at least 64 of M)
+        if (a.ksplit <= 1 && f32_wave_split(a.M, a.N, device_cu_count()))
+            return launch_f32_kind<OP, CfgF32WaveK>(a, s);
+    }
     if (f32_small_tiles(a.M, a.N, device_cu_count())) return launch_f32_kind<OP, CfgF32Small>(a, s);
     return launch_f32_kind<OP, CfgF32>(a, s);
 }

@@ -402,11 +402,62 @@ def test_split_k_fp32(opname, shape):
 
 
 @pytest.mark.parametrize("opname", list(OPS))
-def test_split_k_fp32_two_slices_atomic(opname):
-    """Plain fp32 products split into two slices add both into a zeroed C with
-    atomic adds (config 1's 512 x 1024 x 1024 is one): C may hold anything
-    beforehand, a row pitch wider than N leaves the gap untouched, and eight
-    runs agree bit for bit (two addends onto zero commute exactly)."""
+def test_fp32_config1_shape_subnormal(opname):
+    """The same shape with operands scaled so that every product, partial sum
+    and output is subnormal in fp32: partials added through LDS (NN, NT) or
+    the slice workspace (TN) keep the subnormal bits, so the result matches
+    the fp64 oracle as the normal-range product does, relative to its own
+    largest element (a flush to zero anywhere would lose it entirely)."""
+    vedic = V()
+    layout = OPS[opname]
+    M, N, K = 512, 1024, 1024
+    rng = np.random.default_rng(zlib.crc32(f"subnormal-{opname}".encode()))
+    A, B = _operands(rng, layout, M, N, K)
+    A = (A * np.float32(2.0 ** -70)).astype(np.float32)
+    B = (B * np.float32(2.0 ** -70)).astype(np.float32)
+    got = host(vedic.gemm(layout, dev(A), dev(B)))
+    want, _ = o.gemm_f64(layout, A, B)
+    assert np.max(np.abs(want)) < 2.0 ** -126, "the outputs are subnormal"
+    assert np.count_nonzero(got) > 0.99 * got.size, "subnormal outputs flushed to zero"
+    # subnormals carry fewer significant bits: compare at the subnormal spacing
+    err = np.max(np.abs(got.astype(np.float64) - want))
+    assert err <= 2.0 ** -149 * K, f"{opname}: error {err:.3e} beyond K subnormal ulps"
+
+
+@pytest.mark.parametrize("shape", [(500, 1000, 1000), (512, 1024, 96), (300, 640, 2049)])
+def test_fp32_wave_split_epilogues(shape):
+    """Odd shapes on the wave-split tiles (partial 32 x 64 tiles, K not a
+    multiple of 32) with every epilogue the parity tests cover."""
+    vedic = V()
+    M, N, K = shape
+    rng = np.random.default_rng(zlib.crc32(f"wavesplit-{shape}".encode()))
+    A, B = normal(rng, (M, K)), normal(rng, (K, N), std=0.05)
+    bias, C0 = normal(rng, (N,), std=0.1), normal(rng, (M, N), std=0.1)
+    a, b = dev(A), dev(B)
+    tol = fp32_tol(K)
+    check(host(vedic.gemm(o.NN, a, b)), o.NN, A, B, tol=tol, label="plain")
+    pre = torch.empty((M, N), device="cuda")
+    got = host(vedic.gemm(o.NN, a, b, bias=dev(bias), epilogue=vedic.EPI_BIAS_GELU, preact=pre))
+    check(got, o.NN, A, B, tol=tol, bias=bias, gelu=True, label="bias+gelu")
+    check(host(pre), o.NN, A, B, tol=tol, bias=bias, label="preact")
+    C = dev(C0)
+    check(host(vedic.gemm(o.NN, a, b, C, alpha=0.5, beta=1.0)), o.NN, A, B, tol=tol, alpha=0.5, beta=1.0, C0=C0,
+          label="alpha/beta")
+    cs = torch.zeros(N, device="cuda")
+    got = host(vedic.gemm(o.NN, a, b, colsum=cs))
+    assert np.allclose(host(cs), got.astype(np.float64).sum(0), rtol=1e-5, atol=1e-5)
+    BT = np.ascontiguousarray(B.T)
+    check(host(vedic.gemm(o.NT, a, dev(BT))), o.NT, A, BT, tol=tol, label="NT")
+
+
+@pytest.mark.parametrize("opname", list(OPS))
+def test_fp32_config1_shape_deterministic(opname):
+    """Config 1's 512 x 1024 x 1024 in every layout: NN and NT run one 32 x 64
+    tile per workgroup with the contraction split among its four waves and
+    summed through LDS in a fixed order; TN (whose A rows are M-contiguous)
+    splits over workgroups into a workspace reduced in slice order.  C may
+    hold anything beforehand, a row pitch wider than N leaves the gap
+    untouched, and eight runs agree bit for bit."""
     vedic = V()
     layout = OPS[opname]
     M, N, K = 512, 1024, 1024
