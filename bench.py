@@ -116,6 +116,10 @@ WORKLOADS.update({
     "flash_attn_bwd_fp32_16heads": dict(cfg=5, attn=_fa(bwd=True)),
 })
 COPY_WORKLOAD = "copy_256mib"  # calibration for the FETCH_SIZE / WRITE_SIZE counters
+# The library's own widening copy (vedic_cast_f16_to_f32 of 64 Mi values: 128 MiB
+# read, 256 MiB written) as a second calibration: its loads take the same path
+# as the GEMM kernels' operand loads.
+CAST_WORKLOAD = "cast_f16_f32_64mi"
 
 
 def parse():
@@ -126,11 +130,13 @@ def parse():
     # 75-77 us): the default warmup runs the kernel for ~40 ms first.
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=500)
-    ap.add_argument("--workload", default="ffn_up_fp16_bias_gelu", choices=sorted(WORKLOADS) + [COPY_WORKLOAD])
+    ap.add_argument("--workload", default="ffn_up_fp16_bias_gelu", choices=sorted(WORKLOADS) + [COPY_WORKLOAD, CAST_WORKLOAD])
     ap.add_argument("--all", action="store_true", help="every workload, one JSON line each")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the cpu_baseline sample (default run)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--profiled-steps", type=int, default=25,
+                    help="steps (--steps + --warmup) of the counter runs --summarize-traffic reads")
     ap.add_argument("--summarize-traffic", nargs=4, metavar="DIR",
                     help="FETCH, WRITE, copy FETCH, copy WRITE rocprofv3 output directories")
     return ap.parse_args()
@@ -155,14 +161,33 @@ def _pmc_kib(dirpath: str, counter: str, kernel_substr: str):
     return sum(vals) / len(vals), len(vals)
 
 
+def _pmc_library_total(dirpath: str, counter: str):
+    """Sum of `counter` over every dispatch of this library's kernels."""
+    total, n = 0.0, 0
+    for root, _, files in os.walk(dirpath):
+        for fn in files:
+            if fn.endswith("counter_collection.csv"):
+                with open(os.path.join(root, fn)) as f:
+                    for r in csv.DictReader(f):
+                        if r["Counter_Name"] == counter and "vedic" in r["Kernel_Name"] \
+                                and "at::native" not in r["Kernel_Name"]:
+                            total += float(r["Counter_Value"])
+                            n += 1
+    if not n:
+        raise SystemExit(f"no {counter} rows of the library's kernels under {dirpath}")
+    return total, n
+
+
 def summarize_traffic(args):
+    """HBM bytes per step of a workload: FETCH_SIZE and WRITE_SIZE summed over
+    the library's dispatches of the profiled run, divided by its steps
+    (--steps + --warmup of that run), each scaled by what the same counter
+    reads for torch's copy of 256 MiB (bench.py --workload copy_256mib)."""
     fetch_dir, write_dir, cfetch_dir, cwrite_dir = args.summarize_traffic
-    w = WORKLOADS[args.workload]
-    kern = ("flash_attn_kernel" if "attn" in w
-            else "gemm_f32_kernel" if w["gemms"][0]["dtype"] == "fp32" else "gemm_f16_kernel")
-    fetch, nf = _pmc_kib(fetch_dir, "FETCH_SIZE", kern)
-    write, nw = _pmc_kib(write_dir, "WRITE_SIZE", kern)
-    # torch's copy_ of 256 MiB (the runtime's copyBuffer blit) reads and writes exactly 256 MiB
+    steps = args.profiled_steps
+    fetch, _ = _pmc_library_total(fetch_dir, "FETCH_SIZE")
+    write, _ = _pmc_library_total(write_dir, "WRITE_SIZE")
+    fetch, write = fetch / steps, write / steps
     cfetch, _ = _pmc_kib(cfetch_dir, "FETCH_SIZE", "copyBuffer")
     cwrite, _ = _pmc_kib(cwrite_dir, "WRITE_SIZE", "copyBuffer")
     ref_kib = 256.0 * 1024
@@ -170,13 +195,15 @@ def summarize_traffic(args):
     hbm = (fetch * f_fetch + write * f_write) * 1024.0
     out = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.txt")
     with open(out, "w") as f:
-        f.write(f"# HBM traffic per launch of {kern} for bench.py --workload {args.workload}\n")
-        f.write("# rocprofv3 --pmc FETCH_SIZE, then --pmc WRITE_SIZE (KiB per dispatch), each scaled by\n")
-        f.write("# the same counter read on torch's copy of 256 MiB (bench.py --workload copy_256mib).\n")
+        f.write(f"# HBM traffic per step of bench.py --workload {args.workload} (the library's dispatches)\n")
+        f.write(f"# python3 bench.py --workload {args.workload} --profiled-steps {steps} --summarize-traffic "
+                f"{fetch_dir} {write_dir} {cfetch_dir} {cwrite_dir}\n")
+        f.write("# over rocprofv3 --pmc FETCH_SIZE, then --pmc WRITE_SIZE runs of bench.py --workload "
+                f"{args.workload} (KiB per dispatch),\n")
+        f.write("# each scaled by the same counter on torch's copy of 256 MiB (bench.py --workload copy_256mib).\n")
         f.write("# FETCH_SIZE counts L2-to-fabric reads: repeated fetches by different XCDs' L2s\n")
         f.write("# are all counted, whether the Infinity Cache or HBM serves them.\n")
-        f.write(f"fetch_kib_per_dispatch: {fetch:.1f}  (mean of {nf} dispatches)\n")
-        f.write(f"write_kib_per_dispatch: {write:.1f}  (mean of {nw} dispatches)\n")
+        f.write(f"fetch_kib_per_step: {fetch:.1f}\nwrite_kib_per_step: {write:.1f}\n")
         f.write(f"copy_fetch_kib: {cfetch:.1f}\ncopy_write_kib: {cwrite:.1f}\n")
         f.write(f"fetch_scale: {f_fetch:.4f}\nwrite_scale: {f_write:.4f}\n")
         f.write(f"hbm_bytes_per_launch: {int(hbm)}\n")
@@ -636,6 +663,26 @@ def run_copy(args, torch, dev):
     return {"workload": COPY_WORKLOAD, "ms_per_copy": round(ms, 5), "GB/s": round(gbs, 1)}
 
 
+def run_cast(args, torch, dev):
+    from logos_amd import _lib
+
+    lib = _lib.load()
+    n = 64 * 1024 * 1024
+    src = torch.randn(n, device=dev).half()
+    dst = torch.empty(n, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        rc = lib.vedic_cast_f16_to_f32(src.data_ptr(), dst.data_ptr(), n, s)
+        if rc:
+            raise RuntimeError(_lib.status_string(rc))
+
+    ms, _ = time_steps(step, args.steps, args.warmup, torch)
+    gbs = 6 * n / (ms * 1e-3) / 1e9
+    return {"workload": CAST_WORKLOAD, "ms_per_cast": round(ms, 5), "GB/s": round(gbs, 1),
+            "bytes_read": 2 * n, "bytes_written": 4 * n}
+
+
 def main():
     args = parse()
     if args.summarize_traffic:
@@ -654,6 +701,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.workload == COPY_WORKLOAD:
         print(json.dumps(run_copy(args, torch, dev)), flush=True)
+        return
+    if args.workload == CAST_WORKLOAD:
+        print(json.dumps(run_cast(args, torch, dev)), flush=True)
         return
     if args.all:
         for name in WORKLOADS:
