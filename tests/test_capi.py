@@ -119,3 +119,22 @@ def test_flash_attention_validation():
     assert b(p, p, p, p, p, p, p, p, p + 4, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED
     bh = lib.vedic_flash_attention_bwd_heads
     assert bh(*([arr] * 9), 33, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_TOO_LARGE
+
+
+def test_flash_attention_refusals():
+    """The attention entry points take DH 64 or 128 and no probability copy;
+    other DH up to 128 and a non-null attn pointer are refused with
+    VEDIC_STATUS_UNSUPPORTED (the reference accepts any DH <= 128 and fills
+    attn when given, cuda/VedicGEMM.cu:1065-1079), DH > 128 with BAD_DIM as the
+    reference throws there.  The checks come before any launch."""
+    lib = _lib.load()
+    p = 4096  # never dereferenced: the calls are refused on the host
+    f = lib.vedic_flash_attention_fwd
+    for dh in (16, 32, 48, 96, 127):
+        assert f(p, p, p, p, None, 256, dh, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED, dh
+    assert f(p, p, p, p, None, 256, 129, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_BAD_DIM
+    assert f(p, p, p, p, p, 256, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED
+    assert lib.vedic_flash_attention_fwd_lse(p, p, p, p, p, 256, 96, 0.125, 1, 0, 0, 1, None) == \
+        _lib.STATUS_UNSUPPORTED
+    assert lib.vedic_flash_attention_bwd(p, p, p, p, p, p, p, p, p, 256, 96, 0.125, 1, 0, 0, 1, None) == \
+        _lib.STATUS_UNSUPPORTED
