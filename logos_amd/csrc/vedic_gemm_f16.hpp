@@ -243,27 +243,29 @@ constexpr int kSgMfma = 0x008, kSgVmem = 0x010, kSgDsRead = 0x100;
 // NV > 0: the NV direct loads of a later stage, issued just before this call
 // in the same basic block, are placed one after every EVERY-th MFMA, so that
 // no wave blocks on a full texture-address queue while its MFMAs wait.
-template <bool A_KC, bool B_KC, int BM, int BN, int BK, int MI, int NI, int NV = 0, int EVERY = 1>
+// KN < BK / 16: the wave takes only the KN k steps from kk0 on (the
+// contraction of a stage split among a workgroup's waves).
+template <bool A_KC, bool B_KC, int BM, int BN, int BK, int MI, int NI, int NV = 0, int EVERY = 1, int KN = BK / 16>
 __device__ __forceinline__ void mfma_stage(const char* la, const char* lb, int ar0, int bc0, int lane,
-                                           float16_t (&acc)[MI][NI]) {
-    constexpr int KS = BK / 16;
+                                           float16_t (&acc)[MI][NI], int kk0 = 0) {
+    constexpr int KS = KN;
     constexpr int NR = (A_KC ? MI : 2 * MI) + (B_KC ? NI : 2 * NI);  // LDS reads per k step
     constexpr int NM = MI * NI;                                      // MFMAs per k step
     static_assert(NV <= KS * NM, "at most one load per MFMA");
     constexpr int EV = NV == 0 || NV * EVERY <= KS * NM ? EVERY : KS * NM / NV;  // spacing that fits
     half8_t af[2][MI], bf[2][NI];
 #pragma unroll
-    for (int i = 0; i < MI; ++i) af[0][i] = read_frag<A_KC, BM, BK>(la, ar0 + 32 * i, 0, lane);
+    for (int i = 0; i < MI; ++i) af[0][i] = read_frag<A_KC, BM, BK>(la, ar0 + 32 * i, kk0, lane);
 #pragma unroll
-    for (int j = 0; j < NI; ++j) bf[0][j] = read_frag<B_KC, BN, BK>(lb, bc0 + 32 * j, 0, lane);
+    for (int j = 0; j < NI; ++j) bf[0][j] = read_frag<B_KC, BN, BK>(lb, bc0 + 32 * j, kk0, lane);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
         const int c = kk & 1, n = c ^ 1;
         if (kk + 1 < KS) {
 #pragma unroll
-            for (int i = 0; i < MI; ++i) af[n][i] = read_frag<A_KC, BM, BK>(la, ar0 + 32 * i, kk + 1, lane);
+            for (int i = 0; i < MI; ++i) af[n][i] = read_frag<A_KC, BM, BK>(la, ar0 + 32 * i, kk0 + kk + 1, lane);
 #pragma unroll
-            for (int j = 0; j < NI; ++j) bf[n][j] = read_frag<B_KC, BN, BK>(lb, bc0 + 32 * j, kk + 1, lane);
+            for (int j = 0; j < NI; ++j) bf[n][j] = read_frag<B_KC, BN, BK>(lb, bc0 + 32 * j, kk0 + kk + 1, lane);
         }
 #pragma unroll
         for (int i = 0; i < MI; ++i)
@@ -367,9 +369,15 @@ __device__ __forceinline__ WorkItem work_of(const GemmArgs& a, int w, int ntiles
 
 // OP: 0 NN, 1 NT, 2 TN, 3 NN with an fp32 A converted to binary16 on its way
 // into LDS (the AMP path from fp32 activations).
-template <int OP, int BM, int BN, int BK, int ST, int WGM, int WGN, int KIND>
-__global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) {
-    constexpr int NW = WGM * WGN, WM = BM / WGM, WN = BN / WGN, MI = WM / 32, NI = WN / 32;
+// WGK > 1: the waves form WGK groups of WGM x WGN; group g takes k steps
+// [g KN, (g + 1) KN) of every stage (KN = BK / 16 / WGK), and after the
+// contraction groups 1.. leave their accumulators in the stage buffers for
+// group 0, which adds them in group order and runs the epilogue.
+template <int OP, int BM, int BN, int BK, int ST, int WGM, int WGN, int KIND, int WGK = 1>
+__global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f16_kernel(GemmArgs args) {
+    constexpr int WMN = WGM * WGN, NW = WMN * WGK, WM = BM / WGM, WN = BN / WGN, MI = WM / 32, NI = WN / 32;
+    constexpr int KN = BK / 16 / WGK;
+    static_assert(KN * WGK * 16 == BK, "the k steps of a stage divide among the wave groups");
     constexpr bool A32 = OP == 3;
     constexpr bool A_KC = OP != 2, B_KC = OP == 1;
     using SA = std::conditional_t<A32, SideA32<BM, BK, NW>, Side<A_KC, BM, BK, NW>>;
@@ -380,7 +388,7 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
     // 256 x 256 tiles: the stage's direct loads are spread one per MFMA instead
     // of issued together (2-3 % faster: fewer waves held at a full
     // texture-address queue); 128 x 128 tiles measured slower that way.
-    constexpr bool kInterleave = BM * BN >= 256 * 256;
+    constexpr bool kInterleave = BM * BN >= 256 * 256 && WGK == 1;
 
     // One LDS object per stage (A then B): reads of one stage provably do not
     // alias the direct loads into another.  The compiler follows only a few
@@ -396,7 +404,13 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform per wave
     const int lane = threadIdx.x & 63;
-    const int wm = wave / WGN, wn = wave % WGN;
+    const int wk = wave / WMN, wmn = wave % WMN;
+    const int wm = wmn / WGN, wn = wmn % WGN;
+    // the partial of group g >= 1, wave wmn, is number p = (g - 1) WMN + wmn;
+    // PPB of them share one stage buffer
+    constexpr int PBYTES = WM * WN * 4, PPB = PBYTES <= SBYTES ? SBYTES / PBYTES : 1;
+    static_assert(WGK == 1 || (PBYTES <= SBYTES && (WGK - 1) * WMN <= ST * PPB), "the partials fit the stage buffers");
+    static_assert(WGK == 1 || !A32, "no contraction split with an fp32 A");
     const _Float16* __restrict__ A = static_cast<const _Float16*>(args.A);
     const float* __restrict__ A32f = static_cast<const float*>(args.A);
     const _Float16* __restrict__ B = static_cast<const _Float16*>(args.B);
@@ -476,11 +490,56 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
                     }
                 } else {
                     VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
-                    if (kt < nk) mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI>(As[s], Bs[s], wm * WM, wn * WN, lane, acc);
+                    if (kt < nk)
+                        mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI, 0, 1, KN>(As[s], Bs[s], wm * WM, wn * WN, lane, acc,
+                                                                            wk * KN);
                 }
             }
         }
 
+        if constexpr (WGK > 1) {
+            // the trailing stage loads (zeros past the range) still write the
+            // buffers: wait for them and for every wave's last reads
+            wait_vmcnt<0>();
+            stage_barrier();
+            // (selects, not a table of the buffers: an array of LDS addresses
+            // indexed by the wave would become a constant in global memory)
+            auto part = [&](int p) -> char* {
+                const int q = p / PPB;
+                return (q == 0 ? t0 : q == 1 ? t1 : q == 2 ? t2 : t3) + (p % PPB) * PBYTES;
+            };
+            if (wk > 0) {
+                float4_t* dst = reinterpret_cast<float4_t*>(part((wk - 1) * WMN + wmn));
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int j = 0; j < NI; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            dst[((i * NI + j) * 4 + q) * 64 + lane] =
+                                float4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            }
+            wait_lgkmcnt0();
+            stage_barrier();
+            if (wk == 0) {
+#pragma unroll
+                for (int g = 1; g < WGK; ++g) {
+                    const float4_t* src = reinterpret_cast<const float4_t*>(part((g - 1) * WMN + wmn));
+#pragma unroll
+                    for (int i = 0; i < MI; ++i)
+#pragma unroll
+                        for (int j = 0; j < NI; ++j)
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                const float4_t v = src[((i * NI + j) * 4 + q) * 64 + lane];
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += v[e];
+                            }
+                }
+            }
+            // (the barrier before the next work item's first loads orders
+            // these reads before the buffers are written again)
+        }
         const int row0 = m0 + wm * WM, col0 = n0 + wn * WN;
         // split-K: this slice's raw partial goes to its own slab of the workspace
         void* const cp = args.ksplit > 1 ? static_cast<void*>(static_cast<float*>(args.C) + it.s * args.c_split_stride)
@@ -502,10 +561,12 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
             VEDIC_PROLOGUE();
         }
         const bool full = (row0 + WM <= args.M) && (col0 + WN <= args.N);
-        if (KIND != EK_GENERIC && full)
-            epilogue<KIND, false, MI, NI>(args, cp, acc, row0, col0, lane, pre_bias ? bias_pre : nullptr);
-        else
-            epilogue<KIND, true, MI, NI>(args, cp, acc, row0, col0, lane, pre_bias ? bias_pre : nullptr);
+        if (WGK == 1 || wk == 0) {
+            if (KIND != EK_GENERIC && full)
+                epilogue<KIND, false, MI, NI>(args, cp, acc, row0, col0, lane, pre_bias ? bias_pre : nullptr);
+            else
+                epilogue<KIND, true, MI, NI>(args, cp, acc, row0, col0, lane, pre_bias ? bias_pre : nullptr);
+        }
         if (!more) break;
         if constexpr (A32) {
             __syncthreads();
@@ -544,7 +605,7 @@ __global__ void __launch_bounds__(WGM* WGN * 64) gemm_f16_kernel(GemmArgs args) 
 #define VEDIC_F16_SMALL_EFF 75
 #endif
 struct CfgLarge {  // 256 x 256, eight waves of 128 x 64
-    static constexpr int BM = 256, BN = 256, BK = VEDIC_F16_LARGE_BK, ST = VEDIC_F16_LARGE_ST, WGM = 2, WGN = 4;
+    static constexpr int BM = 256, BN = 256, BK = VEDIC_F16_LARGE_BK, ST = VEDIC_F16_LARGE_ST, WGM = 2, WGN = 4, WGK = 1;
     static constexpr int PER_CU = 1;
 };
 #ifndef VEDIC_F16_SMALL_WGN
@@ -554,14 +615,34 @@ struct CfgLarge {  // 256 x 256, eight waves of 128 x 64
 #define VEDIC_F16_SMALL_ST 3
 #endif
 struct CfgSmall {  // 128 x 128, four waves of 64 x 64, two workgroups per CU (2 x 64 KiB of LDS)
-    static constexpr int BM = 128, BN = 128, BK = 64, ST = VEDIC_F16_SMALL_ST, WGM = 2, WGN = VEDIC_F16_SMALL_WGN;
+    static constexpr int BM = 128, BN = 128, BK = 64, ST = VEDIC_F16_SMALL_ST, WGM = 2, WGN = VEDIC_F16_SMALL_WGN, WGK = 1;
     static constexpr int PER_CU = VEDIC_F16_SMALL_PER_CU;
+};
+#ifndef VEDIC_F16_SMALLK
+#define VEDIC_F16_SMALLK 1
+#endif
+#ifndef VEDIC_F16_SMALLK_WGM
+#define VEDIC_F16_SMALLK_WGM 2
+#endif
+#ifndef VEDIC_F16_SMALLK_WGK
+#define VEDIC_F16_SMALLK_WGK 2
+#endif
+// 128 x 128, eight waves of 64 x 64 in two groups of four, each group taking
+// half of every stage's k steps (summed through LDS after the last stage):
+// with one tile per CU, two waves per SIMD instead of one.  3-7 % faster than
+// CfgSmall on the TN dW products (4096 x 1024 x 8192, 1024 x 3072 x 8192,
+// 1024 x 4096 x 8192); 128 x 64 waves in a single group of four measured no
+// faster than CfgSmall.
+struct CfgSmallK {
+    static constexpr int BM = 128, BN = 128, BK = 64, ST = 3, WGM = VEDIC_F16_SMALLK_WGM, WGN = 2,
+                         WGK = VEDIC_F16_SMALLK_WGK;
+    static constexpr int PER_CU = 1;
 };
 #ifndef VEDIC_F16_MID_ST
 #define VEDIC_F16_MID_ST 3
 #endif
 struct CfgMid {  // 256 x 128, eight waves of 64 x 64
-    static constexpr int BM = 256, BN = 128, BK = 64, ST = VEDIC_F16_MID_ST, WGM = 4, WGN = 2;
+    static constexpr int BM = 256, BN = 128, BK = 64, ST = VEDIC_F16_MID_ST, WGM = 4, WGN = 2, WGK = 1;
     static constexpr int PER_CU = 1;
 };
 
@@ -577,15 +658,30 @@ struct CfgMid {  // 256 x 128, eight waves of 64 x 64
 #define VEDIC_F16_NARROW_ST 4
 #endif
 struct CfgNarrow {
-    static constexpr int BM = 64, BN = 32, BK = VEDIC_F16_NARROW_BK, ST = VEDIC_F16_NARROW_ST, WGM = 2, WGN = 1;
+    static constexpr int BM = 64, BN = 32, BK = VEDIC_F16_NARROW_BK, ST = VEDIC_F16_NARROW_ST, WGM = 2, WGN = 1, WGK = 1;
     static constexpr int PER_CU = 1;
 };
 struct CfgNarrowT {
-    static constexpr int BM = 128, BN = 32, BK = VEDIC_F16_NARROW_BK, ST = 3, WGM = 4, WGN = 1;
+    static constexpr int BM = 128, BN = 32, BK = VEDIC_F16_NARROW_BK, ST = 3, WGM = 4, WGN = 1, WGK = 1;
     static constexpr int PER_CU = 1;
 };
 
 int device_cu_count();
+
+// Explicit instantiation of one configuration's kernels, every epilogue kind
+// (a launch of a kernel template instantiated only implicitly can miss its
+// host stub).
+#define VEDIC_F16_KERNEL(OP, Cfg, KIND) \
+    template __global__ void gemm_f16_kernel<OP, Cfg::BM, Cfg::BN, Cfg::BK, Cfg::ST, Cfg::WGM, Cfg::WGN, KIND, Cfg::WGK>(GemmArgs)
+#define VEDIC_F16_INSTANTIATE(OP, Cfg)            \
+    VEDIC_F16_KERNEL(OP, Cfg, EK_PLAIN);          \
+    VEDIC_F16_KERNEL(OP, Cfg, EK_BIAS);           \
+    VEDIC_F16_KERNEL(OP, Cfg, EK_BIAS_GELU);      \
+    VEDIC_F16_KERNEL(OP, Cfg, EK_BIAS_GELU_PRE);  \
+    VEDIC_F16_KERNEL(OP, Cfg, EK_ACCUM);          \
+    VEDIC_F16_KERNEL(OP, Cfg, EK_GENERIC);        \
+    VEDIC_F16_KERNEL(OP, Cfg, EK_GELU_BWD);       \
+    VEDIC_F16_KERNEL(OP, Cfg, EK_LINEAR_CS)
 
 #ifndef VEDIC_F16_COLUMN_SPLIT
 #define VEDIC_F16_COLUMN_SPLIT 1
@@ -627,8 +723,8 @@ static hipError_t launch_f16(GemmArgs a, hipStream_t s) {
     const int nwork = a.tiles_m * a.tiles_n * a.ksplit;
     const int slots = device_cu_count() * Cfg::PER_CU;
     const int grid = nwork < slots ? nwork : slots;
-    hipLaunchKernelGGL((gemm_f16_kernel<OP, Cfg::BM, Cfg::BN, Cfg::BK, Cfg::ST, Cfg::WGM, Cfg::WGN, KIND>),
-                       dim3(grid), dim3(Cfg::WGM * Cfg::WGN * 64), 0, s, a);
+    hipLaunchKernelGGL((gemm_f16_kernel<OP, Cfg::BM, Cfg::BN, Cfg::BK, Cfg::ST, Cfg::WGM, Cfg::WGN, KIND, Cfg::WGK>),
+                       dim3(grid), dim3(Cfg::WGM * Cfg::WGN * Cfg::WGK * 64), 0, s, a);
     return hipGetLastError();
 }
 
@@ -722,7 +818,12 @@ hipError_t launch_gemm_f16_direct_op(const GemmArgs& a, hipStream_t s) {
         switch (a.ksplit > 1 ? 2 : f16_tile_config(a.M, a.N, device_cu_count())) {
             case 0: return launch_f16_kind<OP, CfgLarge>(a, s);
             case 1: return launch_f16_kind<OP, CfgMid>(a, s);
-            default: return launch_f16_kind<OP, CfgSmall>(a, s);
+            default:
+                // (TN only: the NN and NT products keep the order of the
+                // AMP path's 128 x 128 tiles, so the two agree bit for bit)
+                if constexpr (OP == 2)
+                    if (VEDIC_F16_SMALLK && a.ksplit <= 1) return launch_f16_kind<OP, CfgSmallK>(a, s);
+                return launch_f16_kind<OP, CfgSmall>(a, s);
         }
     }
 }

@@ -5,38 +5,10 @@
 
 namespace vedic {
 
-template __global__ void gemm_f16_kernel<0, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_PLAIN>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_BIAS>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_BIAS_GELU>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_BIAS_GELU_PRE>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_ACCUM>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_GENERIC>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_GELU_BWD>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgLarge::BM, CfgLarge::BN, CfgLarge::BK, CfgLarge::ST, CfgLarge::WGM, CfgLarge::WGN, EK_LINEAR_CS>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_PLAIN>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_BIAS>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_BIAS_GELU>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_BIAS_GELU_PRE>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_ACCUM>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_GENERIC>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_GELU_BWD>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgSmall::BM, CfgSmall::BN, CfgSmall::BK, CfgSmall::ST, CfgSmall::WGM, CfgSmall::WGN, EK_LINEAR_CS>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgMid::BM, CfgMid::BN, CfgMid::BK, CfgMid::ST, CfgMid::WGM, CfgMid::WGN, EK_PLAIN>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgMid::BM, CfgMid::BN, CfgMid::BK, CfgMid::ST, CfgMid::WGM, CfgMid::WGN, EK_BIAS>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgMid::BM, CfgMid::BN, CfgMid::BK, CfgMid::ST, CfgMid::WGM, CfgMid::WGN, EK_BIAS_GELU>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgMid::BM, CfgMid::BN, CfgMid::BK, CfgMid::ST, CfgMid::WGM, CfgMid::WGN, EK_BIAS_GELU_PRE>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgMid::BM, CfgMid::BN, CfgMid::BK, CfgMid::ST, CfgMid::WGM, CfgMid::WGN, EK_ACCUM>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgMid::BM, CfgMid::BN, CfgMid::BK, CfgMid::ST, CfgMid::WGM, CfgMid::WGN, EK_GENERIC>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgMid::BM, CfgMid::BN, CfgMid::BK, CfgMid::ST, CfgMid::WGM, CfgMid::WGN, EK_GELU_BWD>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgMid::BM, CfgMid::BN, CfgMid::BK, CfgMid::ST, CfgMid::WGM, CfgMid::WGN, EK_LINEAR_CS>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_PLAIN>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_BIAS>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_BIAS_GELU>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_BIAS_GELU_PRE>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_ACCUM>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_GENERIC>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_GELU_BWD>(GemmArgs);
-template __global__ void gemm_f16_kernel<0, CfgNarrow::BM, CfgNarrow::BN, CfgNarrow::BK, CfgNarrow::ST, CfgNarrow::WGM, CfgNarrow::WGN, EK_LINEAR_CS>(GemmArgs);
+VEDIC_F16_INSTANTIATE(0, CfgLarge);
+VEDIC_F16_INSTANTIATE(0, CfgSmall);
+VEDIC_F16_INSTANTIATE(0, CfgMid);
+VEDIC_F16_INSTANTIATE(0, CfgNarrow);
 
 hipError_t launch_gemm_f16_direct_nn(const GemmArgs& a, hipStream_t s) {
     return launch_gemm_f16_direct_op<0>(a, s);
