@@ -310,13 +310,16 @@ int vedic_gemm_checked(const vedic_gemm_desc_t* desc, float tolerance, vedic_ver
  * Masked scores are left out of the sums; a row whose sum is <= 1e-9 is 0.
  * Replaces cuda_flash_attention_fwd (cuda/VedicGEMM.cuh:236, cuda/VedicGEMM.cu:1065-1104;
  * kernel :898-1063), called per head at cuda/ModelGPU.cu:959-968.
- * Limits: dh 64 or 128 (others VEDIC_STATUS_UNSUPPORTED; dh > 128 BAD_DIM,
- * where the reference throws); `attn` (the reference's optional copy of the
- * probabilities, NULL at its only call site) must be NULL (UNSUPPORTED
- * otherwise); 16-byte-aligned Q, K, V, out; stride >= 1 when the sparse mask
- * applies; seq * dh < 2^29.  A call on a single head splits long key ranges
- * over several workgroups and takes a stream-ordered workspace (hipMallocAsync
- * on `stream`, freed the same way) for the partial results. */
+ * Limits: 1 <= dh <= 128 (BAD_DIM otherwise, where the reference throws);
+ * `attn` (the reference's optional copy of the probabilities, NULL at its
+ * only call site) must be NULL (UNSUPPORTED otherwise); stride >= 1 when the
+ * sparse mask applies; seq * (dh <= 64 ? 64 : 128) < 2^29.  The kernels run
+ * at dh 64 and 128 on 16-byte-aligned matrices; any other dh, or an
+ * unaligned matrix, is copied into zero-padded [seq x 64] or [seq x 128]
+ * matrices first and the output copied back (the zero columns add exact
+ * zeros to every sum).  A call on a single head splits long key ranges over
+ * several workgroups; partial results and padded copies live in a
+ * stream-ordered workspace (hipMallocAsync on `stream`, freed the same way). */
 int vedic_flash_attention_fwd(const float* Q, const float* K, const float* V, float* out, float* attn, int seq,
                               int dh, float scale, int causal, int shunyam, int window, int stride, void* stream);
 
@@ -348,8 +351,9 @@ int vedic_flash_attention_fwd_heads(const float* const* Q, const float* const* K
  * two seq x seq buffers.  That code recomputes the probabilities with the
  * causal mask only; with shunyam set this function differentiates the
  * forward as computed (sparse mask included).  dQ, dK, dV are overwritten.
- * Limits as for the forward; takes a stream-ordered workspace of 8 * seq
- * bytes (hipMallocAsync on `stream`). */
+ * Limits and padding as for the forward; takes a stream-ordered workspace of
+ * 8 * seq bytes per head, plus the padded copies when dh is not 64 or 128 or
+ * a matrix is not 16-byte aligned (hipMallocAsync on `stream`). */
 int vedic_flash_attention_bwd(const float* Q, const float* K, const float* V, const float* O, const float* dO,
                               const float* lse, float* dQ, float* dK, float* dV, int seq, int dh, float scale,
                               int causal, int shunyam, int window, int stride, void* stream);

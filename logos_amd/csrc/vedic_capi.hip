@@ -1325,15 +1325,84 @@ extern "C" int vedic_gemm_checked(const vedic_gemm_desc_t* d, float tolerance, v
 #define VEDIC_FA_ITEMS_PER_4CU 11
 #endif
 
+// The attention kernels take head dimensions 64 and 128 and 16-byte-aligned
+// matrices.  Other head dimensions up to 128, and unaligned matrices, go
+// through zero-padded copies: [seq x dh] -> [seq x dhp] (dhp = 64 for
+// dh <= 64, else 128) in a stream-ordered workspace, and the outputs are
+// copied back.  The padding columns of Q, K, V and dO are zero, so every
+// score, row sum and product over the first dh columns is the same sum in
+// the same order with exact zeros added (x + 0 = x); the outputs' padding
+// columns are dropped.
+static int flash_dh_pad(int dh) { return dh <= 64 ? 64 : 128; }
+
+struct FlashPack {
+    const float* src[kMaxHeads];
+    float* dst[kMaxHeads];
+    int seq, dh, dhp;
+};
+
+// src [seq x dh] -> dst [seq x dhp], columns dh .. dhp - 1 zero; grid.y = head
+__global__ void __launch_bounds__(256) flash_pack_kernel(FlashPack p) {
+    const float* __restrict__ src = p.src[blockIdx.y];
+    float* __restrict__ dst = p.dst[blockIdx.y];
+    const int64_t n = (int64_t)p.seq * p.dhp;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i / p.dhp;
+        const int c = (int)(i - r * p.dhp);
+        dst[i] = c < p.dh ? src[r * p.dh + c] : 0.0f;
+    }
+}
+
+// src [seq x dhp] -> dst [seq x dh]; grid.y = head
+__global__ void __launch_bounds__(256) flash_unpack_kernel(FlashPack p) {
+    const float* __restrict__ src = p.src[blockIdx.y];
+    float* __restrict__ dst = p.dst[blockIdx.y];
+    const int64_t n = (int64_t)p.seq * p.dh;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i / p.dh;
+        const int c = (int)(i - r * p.dh);
+        dst[i] = src[r * p.dhp + c];
+    }
+}
+
+// One pack (unpack: !pack) of nheads matrices between the callers' [seq x dh]
+// and the padded [seq x dhp] copies at ws + h * seq * dhp.
+static hipError_t flash_repack(bool pack, const float* const* user, float* ws, int nheads, int seq, int dh, int dhp,
+                               hipStream_t s) {
+    FlashPack p{};
+    for (int h = 0; h < nheads; ++h) {
+        float* padded = ws + (int64_t)h * seq * dhp;
+        if (pack) {
+            p.src[h] = user[h];
+            p.dst[h] = padded;
+        } else {
+            p.src[h] = padded;
+            p.dst[h] = const_cast<float*>(user[h]);
+        }
+    }
+    p.seq = seq;
+    p.dh = dh;
+    p.dhp = dhp;
+    const int64_t n = (int64_t)seq * (pack ? dhp : dh);
+    const int64_t blocks = (n + 255) / 256;
+    const dim3 grid((unsigned)(blocks < 1024 ? blocks : 1024), (unsigned)nheads);
+    if (pack)
+        hipLaunchKernelGGL(flash_pack_kernel, grid, dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL(flash_unpack_kernel, grid, dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
 // Shape checks shared by the attention entry points.
 static int flash_check(int nheads, int max_heads, int seq, int dh, int shunyam, int window, int stride) {
     if (nheads < 1 || seq < 1 || dh < 1 || dh > 128) return VEDIC_STATUS_BAD_DIM;
     if (nheads > max_heads) return VEDIC_STATUS_TOO_LARGE;
-    if (dh != 64 && dh != 128) return VEDIC_STATUS_UNSUPPORTED;
-    if ((int64_t)seq * dh >= (int64_t(1) << 29)) return VEDIC_STATUS_TOO_LARGE;
+    if ((int64_t)seq * flash_dh_pad(dh) >= (int64_t(1) << 29)) return VEDIC_STATUS_TOO_LARGE;
     if (shunyam && seq > window && stride < 1) return VEDIC_STATUS_BAD_DIM;
     return VEDIC_STATUS_OK;
 }
+
+static int flash_launch(FlashArgs& a, int dh, hipStream_t s);
 
 static int flash_impl(const float* const* Q, const float* const* K, const float* const* V, float* const* out,
                       float* const* lse, int nheads, int seq, int dh, float scale, int causal, int shunyam,
@@ -1342,11 +1411,12 @@ static int flash_impl(const float* const* Q, const float* const* K, const float*
     if (chk != VEDIC_STATUS_OK) return chk;
     const bool sparse = shunyam && seq > window;
     if (!Q || !K || !V || !out) return VEDIC_STATUS_NULL_POINTER;
+    const int dhp = flash_dh_pad(dh);
+    bool repack = dh != dhp;
     FlashArgs a{};
     for (int h = 0; h < nheads; ++h) {
         if (!Q[h] || !K[h] || !V[h] || !out[h]) return VEDIC_STATUS_NULL_POINTER;
-        if (!aligned16(Q[h]) || !aligned16(K[h]) || !aligned16(V[h]) || !aligned16(out[h]))
-            return VEDIC_STATUS_UNSUPPORTED;
+        if (!aligned16(Q[h]) || !aligned16(K[h]) || !aligned16(V[h]) || !aligned16(out[h])) repack = true;
         a.q[h] = Q[h];
         a.k[h] = K[h];
         a.v[h] = V[h];
@@ -1382,11 +1452,44 @@ static int flash_impl(const float* const* Q, const float* const* K, const float*
     a.chunk = chunk;
     a.items = (int)items;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (chunk >= full) return hip_status(launch_flash_attn(a, dh, s));
+    if (!repack) return flash_launch(a, dh, s);
+    // padded copies of Q, K, V and the output, head after head
+    const int64_t per = (int64_t)nheads * seq * dhp;
+    float* ws = nullptr;
+    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), sizeof(float) * 4 * (size_t)per, s);
+    if (e != hipSuccess) return hip_status(e);
+    float* const pq = ws;
+    float* const pk = ws + per;
+    float* const pv = ws + 2 * per;
+    float* const po = ws + 3 * per;
+    int st = VEDIC_STATUS_OK;
+    e = flash_repack(true, Q, pq, nheads, seq, dh, dhp, s);
+    if (e == hipSuccess) e = flash_repack(true, K, pk, nheads, seq, dh, dhp, s);
+    if (e == hipSuccess) e = flash_repack(true, V, pv, nheads, seq, dh, dhp, s);
+    if (e == hipSuccess) {
+        for (int h = 0; h < nheads; ++h) {
+            const int64_t off = (int64_t)h * seq * dhp;
+            a.q[h] = pq + off;
+            a.k[h] = pk + off;
+            a.v[h] = pv + off;
+            a.o[h] = po + off;
+        }
+        st = flash_launch(a, dhp, s);
+        if (st == VEDIC_STATUS_OK) e = flash_repack(false, const_cast<const float* const*>(out), po, nheads, seq, dh, dhp, s);
+    }
+    const hipError_t f = hipFreeAsync(ws, s);
+    if (st != VEDIC_STATUS_OK) return st;
+    return hip_status(e != hipSuccess ? e : f);
+}
+
+// The forward on prepared arguments (head dimension 64 or 128, aligned).
+static int flash_launch(FlashArgs& a, int dh, hipStream_t s) {
+    const int full = a.nqg * kFaQ;
+    if (a.chunk >= full) return hip_status(launch_flash_attn(a, dh, s));
     // Workspace: the chunk partials, then the work-item counter.  The split
     // items go to a grid of resident workgroups (LDS allows three per CU at
     // DH 64, one at DH 128) that take them largest first.
-    const size_t bytes = sizeof(float) * (size_t)flash_slot_floats(dh) * (size_t)items * nheads;
+    const size_t bytes = sizeof(float) * (size_t)flash_slot_floats(dh) * (size_t)a.items * a.nheads;
     char* ws = nullptr;
     hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), bytes + 256, s);
     if (e != hipSuccess) return hip_status(e);
@@ -1426,12 +1529,14 @@ static int flash_bwd_impl(const float* const* Q, const float* const* K, const fl
     const int chk = flash_check(nheads, kFaBwdHeads, seq, dh, shunyam, window, stride);
     if (chk != VEDIC_STATUS_OK) return chk;
     if (!Q || !K || !V || !O || !dO || !lse || !dQ || !dK || !dV) return VEDIC_STATUS_NULL_POINTER;
+    const int dhp = flash_dh_pad(dh);
+    bool repack = dh != dhp;
     FlashBwdArgs a{};
     for (int h = 0; h < nheads; ++h) {
         const void* ps[9] = {Q[h], K[h], V[h], O[h], dO[h], lse[h], dQ[h], dK[h], dV[h]};
         for (const void* p : ps) {
             if (!p) return VEDIC_STATUS_NULL_POINTER;
-            if (p != lse[h] && !aligned16(p)) return VEDIC_STATUS_UNSUPPORTED;
+            if (p != lse[h] && !aligned16(p)) repack = true;
         }
         a.q[h] = Q[h];
         a.k[h] = K[h];
@@ -1452,10 +1557,40 @@ static int flash_bwd_impl(const float* const* Q, const float* const* K, const fl
     a.stride = a.sparse ? stride : 1;
     a.scale = scale;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&a.delta), sizeof(float) * 2 * (size_t)seq * nheads, s);
+    // workspace: the row statistics, then (padded path) the padded copies of
+    // Q, K, V, O, dO, dQ, dK, dV, head after head
+    const int64_t per = (int64_t)nheads * seq * dhp;
+    const size_t stat_floats = 2 * (size_t)seq * nheads;
+    const size_t pad_at = (stat_floats + 63) / 64 * 64;  // 256-byte aligned copies
+    float* ws = nullptr;
+    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws),
+                                  sizeof(float) * (repack ? pad_at + 8 * (size_t)per : stat_floats), s);
     if (e != hipSuccess) return hip_status(e);
-    e = launch_flash_attn_bwd(a, dh, s);
-    const hipError_t f = hipFreeAsync(a.delta, s);
+    a.delta = ws;
+    if (!repack) {
+        e = launch_flash_attn_bwd(a, dh, s);
+    } else {
+        float* const pad = ws + pad_at;
+        const float* const* ins[5] = {Q, K, V, O, dO};
+        for (int t = 0; t < 5 && e == hipSuccess; ++t) e = flash_repack(true, ins[t], pad + t * per, nheads, seq, dh, dhp, s);
+        for (int h = 0; h < nheads; ++h) {
+            const int64_t off = (int64_t)h * seq * dhp;
+            a.q[h] = pad + off;
+            a.k[h] = pad + per + off;
+            a.v[h] = pad + 2 * per + off;
+            a.o[h] = pad + 3 * per + off;
+            a.dout[h] = pad + 4 * per + off;
+            a.dq[h] = pad + 5 * per + off;
+            a.dk[h] = pad + 6 * per + off;
+            a.dv[h] = pad + 7 * per + off;
+        }
+        if (e == hipSuccess) e = launch_flash_attn_bwd(a, dhp, s);
+        float* const* outs[3] = {dQ, dK, dV};
+        for (int t = 0; t < 3 && e == hipSuccess; ++t)
+            e = flash_repack(false, const_cast<const float* const*>(outs[t]), pad + (5 + t) * per, nheads, seq, dh, dhp,
+                             s);
+    }
+    const hipError_t f = hipFreeAsync(ws, s);
     return hip_status(e != hipSuccess ? e : f);
 }
 

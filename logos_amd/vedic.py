@@ -404,8 +404,8 @@ def flash_attention_fwd(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, out: 
                         scale: float | None = None, causal: bool = True, shunyam: bool = False, window: int = 0,
                         stride: int = 1, attn: torch.Tensor | None = None,
                         lse: torch.Tensor | None = None) -> torch.Tensor:
-    """out = softmax(scale Q K^T + mask) V for one head, fp32 [seq x dh] (dh 64
-    or 128): cuda_flash_attention_fwd (cuda/VedicGEMM.cu:1065-1104).  scale
+    """out = softmax(scale Q K^T + mask) V for one head, fp32 [seq x dh] (dh 1
+    to 128): cuda_flash_attention_fwd (cuda/VedicGEMM.cu:1065-1104).  scale
     defaults to 1/sqrt(dh), the caller's value (cuda/ModelGPU.cu:963).  The
     mask drops keys after the query (causal) and, with shunyam and seq >
     window, keys outside [query - window, query] that are not multiples of

@@ -94,18 +94,19 @@ def test_python_mirror_rejects_cpu_tensors():
 
 def test_flash_attention_validation():
     """Argument checks of the attention entry points, all before any device
-    call: the reference throws for DH > 128 (cuda/VedicGEMM.cu:1074-1080)."""
+    call: the reference throws for DH > 128 (cuda/VedicGEMM.cu:1074-1080).
+    (Other DH and unaligned matrices are valid: they take the padded copies,
+    tests/test_gpu_flash_attention.py.)"""
     lib = _lib.load()
     p = 1 << 12  # aligned stand-in addresses; never dereferenced
     f = lib.vedic_flash_attention_fwd
     assert f(p, p, p, p, None, 0, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_BAD_DIM
     assert f(p, p, p, p, None, 16, 256, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_BAD_DIM
-    assert f(p, p, p, p, None, 16, 32, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED
     assert f(p, p, p, p, p, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED  # attn copy
     assert f(p, p, p, None, None, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_NULL_POINTER
-    assert f(p + 4, p, p, p, None, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED  # misaligned
     assert f(p, p, p, p, None, 16, 64, 0.125, 1, 1, 4, 0, None) == _lib.STATUS_BAD_DIM  # stride 0, sparse on
     assert f(p, p, p, p, None, 1 << 23, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_TOO_LARGE
+    assert f(p, p, p, p, None, 1 << 23, 33, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_TOO_LARGE  # padded to 64
     arr = (ctypes.c_void_p * 65)(*([p] * 65))
     g = lib.vedic_flash_attention_fwd_heads
     assert g(arr, arr, arr, arr, None, 65, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_TOO_LARGE
@@ -114,27 +115,28 @@ def test_flash_attention_validation():
     fl = lib.vedic_flash_attention_fwd_lse
     assert fl(p, p, p, p, None, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_NULL_POINTER
     b = lib.vedic_flash_attention_bwd
-    assert b(p, p, p, p, p, p, p, p, p, 16, 32, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED
     assert b(p, p, p, p, p, None, p, p, p, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_NULL_POINTER
-    assert b(p, p, p, p, p, p, p, p, p + 4, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED
     bh = lib.vedic_flash_attention_bwd_heads
     assert bh(*([arr] * 9), 33, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_TOO_LARGE
 
 
 def test_flash_attention_refusals():
-    """The attention entry points take DH 64 or 128 and no probability copy;
-    other DH up to 128 and a non-null attn pointer are refused with
-    VEDIC_STATUS_UNSUPPORTED (the reference accepts any DH <= 128 and fills
-    attn when given, cuda/VedicGEMM.cu:1065-1079), DH > 128 with BAD_DIM as the
-    reference throws there.  The checks come before any launch."""
+    """The attention entry points take any DH from 1 to 128, as the reference
+    (cuda/VedicGEMM.cu:1074-1079); DH outside that range is BAD_DIM (the
+    reference throws above 128), and a non-null attn pointer (the reference's
+    optional probability copy, NULL at its only call site) UNSUPPORTED.  The
+    checks come before any launch, so the pointers are never dereferenced."""
     lib = _lib.load()
     p = 4096  # never dereferenced: the calls are refused on the host
     f = lib.vedic_flash_attention_fwd
-    for dh in (16, 32, 48, 96, 127):
-        assert f(p, p, p, p, None, 256, dh, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED, dh
-    assert f(p, p, p, p, None, 256, 129, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_BAD_DIM
-    assert f(p, p, p, p, p, 256, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED
-    assert lib.vedic_flash_attention_fwd_lse(p, p, p, p, p, 256, 96, 0.125, 1, 0, 0, 1, None) == \
-        _lib.STATUS_UNSUPPORTED
-    assert lib.vedic_flash_attention_bwd(p, p, p, p, p, p, p, p, p, 256, 96, 0.125, 1, 0, 0, 1, None) == \
-        _lib.STATUS_UNSUPPORTED
+    for dh in (0, -1, 129, 256):
+        assert f(p, p, p, p, None, 256, dh, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_BAD_DIM, dh
+        assert lib.vedic_flash_attention_fwd_lse(p, p, p, p, p, 256, dh, 0.125, 1, 0, 0, 1, None) == \
+            _lib.STATUS_BAD_DIM, dh
+        assert lib.vedic_flash_attention_bwd(p, p, p, p, p, p, p, p, p, 256, dh, 0.125, 1, 0, 0, 1, None) == \
+            _lib.STATUS_BAD_DIM, dh
+    for dh in (1, 50, 64, 96, 128):
+        assert f(p, p, p, p, p, 256, dh, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED, dh
+    # the sparse mask needs a stride, and a null operand is refused
+    assert f(p, p, p, p, None, 256, 96, 0.125, 1, 1, 8, 0, None) == _lib.STATUS_BAD_DIM
+    assert f(p, None, p, p, None, 256, 96, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_NULL_POINTER

@@ -148,9 +148,9 @@ def test_full_size_unit_values_sum_to_one(full_heads):
 
 def test_rejections():
     v = vedic()
-    x = torch.zeros((64, 32), device="cuda")
+    x = torch.zeros((64, 129), device="cuda")
     with pytest.raises(ValueError):
-        v.flash_attention_fwd(x, x, x)  # DH 32
+        v.flash_attention_fwd(x, x, x)  # DH 129 (the reference throws above 128)
     y = torch.zeros((64, 64), device="cuda")
     with pytest.raises(ValueError):
         v.flash_attention_fwd(y, y, y, attn=torch.zeros((64, 64), device="cuda"))
@@ -253,6 +253,6 @@ def test_backward_rejections():
     lse = torch.zeros(64, device="cuda")
     with pytest.raises(ValueError):
         v.flash_attention_bwd(x, x, x, x, x, lse[:32])
-    y = torch.zeros((64, 32), device="cuda")
+    y = torch.zeros((64, 129), device="cuda")
     with pytest.raises(ValueError):
-        v.flash_attention_bwd(y, y, y, y, y, lse)
+        v.flash_attention_bwd(y, y, y, y, y, lse)  # DH 129
