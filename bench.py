@@ -114,6 +114,9 @@ WORKLOADS.update({
     "flash_attn_fwd_fp32_16heads": dict(cfg=5, attn=_fa()),
     "flash_attn_fwd_fp32_per_head": dict(cfg=5, attn=_fa(batched=False)),
     "flash_attn_bwd_fp32_16heads": dict(cfg=5, attn=_fa(bwd=True)),
+    # the same layer width split into 8 heads of DH 128 (the kernels' other width)
+    "flash_attn_fwd_fp32_8heads_dh128": dict(cfg=5, attn=_fa(dh=128, heads=8)),
+    "flash_attn_bwd_fp32_8heads_dh128": dict(cfg=5, attn=_fa(dh=128, heads=8, bwd=True)),
 })
 COPY_WORKLOAD = "copy_256mib"  # calibration for the FETCH_SIZE / WRITE_SIZE counters
 # The library's own widening copy (vedic_cast_f16_to_f32 of 64 Mi values: 128 MiB

@@ -218,10 +218,15 @@ flash_bwd_dq_kernel(FlashBwdArgs a) {
 
 // --------------------------------------------------------------- dK/dV pass
 
-template <int DH>
+// PART 0: dK and dV together.  At DH 128 the two do not fit one wave's
+// registers beside K and V (168 registers spilled), so they run as two
+// launches: PART 1 dV only (no V, no dP), PART 2 dK only; the second
+// recomputes S (five products per block instead of four) but nothing spills.
+template <int DH, int PART = 0>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 flash_bwd_dkdv_kernel(FlashBwdArgs a) {
     constexpr int KB = 32 * DH * 4, NLD = 2 * KB / 1024 / 4, HALF = DH / 2;
+    constexpr bool DO_DV = PART != 2, DO_DK = PART != 1;
     constexpr int SB = 2 * KB + 1024;  // Q block, dO block, then (lse2, D) of the 32 queries
     __shared__ __attribute__((aligned(1024))) char t0[SB];
     __shared__ __attribute__((aligned(1024))) char t1[SB];
@@ -248,7 +253,7 @@ flash_bwd_dkdv_kernel(FlashBwdArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 kf[4 * j + e] = vk[e];
-                vf[4 * j + e] = vv[e];
+                vf[4 * j + e] = DO_DK ? vv[e] : 0.0f;
             }
         }
     }
@@ -284,7 +289,7 @@ flash_bwd_dkdv_kernel(FlashBwdArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 s = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[e], kf[4 * j + e], s, 0, 0, 0);
-                dp = __builtin_amdgcn_mfma_f32_32x32x2f32(da[e], vf[4 * j + e], dp, 0, 0, 0);
+                if constexpr (DO_DK) dp = __builtin_amdgcn_mfma_f32_32x32x2f32(da[e], vf[4 * j + e], dp, 0, 0, 0);
             }
         }
         // s[4 gg + r]: query qb0 + 8 gg + 4 h + r against this lane's key
@@ -298,13 +303,17 @@ flash_bwd_dkdv_kernel(FlashBwdArgs a) {
             s[i] = pv;  // P
         }
         // dV^T[d][key] += sum over queries dO[q][d] P[q][key]
+        if constexpr (DO_DV) {
 #pragma unroll
-        for (int d = 0; d < DH / 32; ++d)
+            for (int d = 0; d < DH / 32; ++d)
 #pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const int qi = 8 * (t >> 2) + 4 * h + (t & 3);
-                dv[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb_elem<DH>(dl, qi, 32 * d + l32), s[t], dv[d], 0, 0, 0);
-            }
+                for (int t = 0; t < 16; ++t) {
+                    const int qi = 8 * (t >> 2) + 4 * h + (t & 3);
+                    dv[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb_elem<DH>(dl, qi, 32 * d + l32), s[t], dv[d], 0,
+                                                                 0, 0);
+                }
+        }
+        if constexpr (!DO_DK) return;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int qi = 8 * (i >> 2) + 4 * h + (i & 3);
@@ -358,8 +367,8 @@ flash_bwd_dkdv_kernel(FlashBwdArgs a) {
                 v[r] = dv[d][4 * gg + r];
                 w[r] = dk[d][4 * gg + r] * a.scale;
             }
-            *reinterpret_cast<float4_t*>(vrow + 32 * d + 8 * gg + 4 * h) = v;
-            *reinterpret_cast<float4_t*>(krow + 32 * d + 8 * gg + 4 * h) = w;
+            if constexpr (DO_DV) *reinterpret_cast<float4_t*>(vrow + 32 * d + 8 * gg + 4 * h) = v;
+            if constexpr (DO_DK) *reinterpret_cast<float4_t*>(krow + 32 * d + 8 * gg + 4 * h) = w;
         }
 }
 
@@ -370,7 +379,8 @@ hipError_t launch_flash_attn_bwd(const FlashBwdArgs& a, int dh, hipStream_t s) {
         hipLaunchKernelGGL(flash_bwd_dkdv_kernel<64>, grid, dim3(256), 0, s, a);
     } else {
         hipLaunchKernelGGL(flash_bwd_dq_kernel<128>, grid, dim3(256), 0, s, a);
-        hipLaunchKernelGGL(flash_bwd_dkdv_kernel<128>, grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((flash_bwd_dkdv_kernel<128, 1>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((flash_bwd_dkdv_kernel<128, 2>), grid, dim3(256), 0, s, a);
     }
     return hipGetLastError();
 }
