@@ -28,10 +28,15 @@
  * Memory: the caller allocates every output.  A product whose output has too
  * few tiles to fill the GPU and whose contraction is long (fp16: fewer than
  * 128 tiles of 128 x 128 and K >= 2048; fp32: K >= 256) runs split over K and
- * takes a stream-ordered fp32 workspace of S * M * N * 4 bytes (S <= 8) with
- * hipMallocAsync / hipFreeAsync on `stream`; every other call allocates
- * nothing.  Results never depend on the split or on timing: slices are added
- * in a fixed order.
+ * takes an fp32 workspace of S * M * N * 4 bytes (S <= 8).  Workspaces (this,
+ * column partials, the AMP cast buffer, attention partials and padded
+ * copies) come from a block of device memory kept per (device, stream):
+ * grown with hipMallocAsync on `stream` when a call needs more than it holds,
+ * reused by every later call on that stream (their work runs in stream
+ * order), and held until the process ends or vedic_workspace_release(stream).
+ * Host threads may share a stream: a call holds the block from its first
+ * request until its last kernel is enqueued.  Results never depend on the
+ * split or on timing: slices are added in a fixed order.
  *
  * Errors follow the reference's conventions: shape errors are
  * VEDIC_STATUS_BAD_DIM (the reference throws std::invalid_argument,
@@ -126,8 +131,8 @@ int vedic_gemm(const vedic_gemm_desc_t* desc);
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * allocation).  No counterpart in the reference.  Same semantics, kernels and
  * results as vedic_gemm; the temporary memory vedic_gemm takes from the
- * stream-ordered pool (split-K partial slabs, column partials, the AMP cast
- * buffer) comes instead from a fixed per-GPU region of
+ * stream's workspace block (split-K partial slabs, column partials, the AMP
+ * cast buffer) comes instead from a fixed per-GPU region of
  * vedic_noalloc_scratch_bytes() bytes (32 MiB) compiled into the library and
  * held until the process ends.  A call that needs more returns
  * VEDIC_STATUS_TOO_LARGE before launching anything that writes C.  Every call
@@ -137,6 +142,12 @@ int vedic_gemm_noalloc(const vedic_gemm_desc_t* desc);
 
 /* Size of the region vedic_gemm_noalloc draws from (per GPU). */
 size_t vedic_noalloc_scratch_bytes(void);
+
+/* Frees the workspace block kept for `stream` on the current device (in
+ * stream order, after the work queued on it); the next call on the stream
+ * allocates a new one.  New: the reference allocates per call and keeps
+ * nothing. */
+int vedic_workspace_release(void* stream);
 
 /* ---- reference-compatible entry points ------------------------------- */
 
@@ -183,8 +194,8 @@ int vedic_gemm_bias_gelu_f32(const float* X, const float* W, const float* bias, 
  * with W32, as the reference falls back to cuda_vedic_gemm(_bias) for a
  * parameter without a shadow.  A and C contiguous.  For N > 1024, or an A
  * whose base is not 16-byte aligned or whose K is not a multiple of 8, the
- * call casts A into a stream-ordered M x K binary16 workspace (hipMallocAsync
- * on `stream`) and runs the fp16 GEMM on it: each output tile converts its
+ * call casts A into an M x K binary16 workspace (the stream's workspace
+ * block) and runs the fp16 GEMM on it: each output tile converts its
  * own rows of A, ceil(N / 128) conversions per element, which loses to one
  * cast pass for wide products.  Results are the same bits either way. */
 int vedic_amp_gemm(const float* A, int M, int K, const void* W16, const float* W32, int N, float* C,
@@ -318,8 +329,8 @@ int vedic_gemm_checked(const vedic_gemm_desc_t* desc, float tolerance, vedic_ver
  * unaligned matrix, is copied into zero-padded [seq x 64] or [seq x 128]
  * matrices first and the output copied back (the zero columns add exact
  * zeros to every sum).  A call on a single head splits long key ranges over
- * several workgroups; partial results and padded copies live in a
- * stream-ordered workspace (hipMallocAsync on `stream`, freed the same way). */
+ * several workgroups; partial results and padded copies live in the
+ * stream's workspace block (see vedic_gemm). */
 int vedic_flash_attention_fwd(const float* Q, const float* K, const float* V, float* out, float* attn, int seq,
                               int dh, float scale, int causal, int shunyam, int window, int stride, void* stream);
 
@@ -351,9 +362,9 @@ int vedic_flash_attention_fwd_heads(const float* const* Q, const float* const* K
  * two seq x seq buffers.  That code recomputes the probabilities with the
  * causal mask only; with shunyam set this function differentiates the
  * forward as computed (sparse mask included).  dQ, dK, dV are overwritten.
- * Limits and padding as for the forward; takes a stream-ordered workspace of
- * 8 * seq bytes per head, plus the padded copies when dh is not 64 or 128 or
- * a matrix is not 16-byte aligned (hipMallocAsync on `stream`). */
+ * Limits and padding as for the forward; takes a workspace of 8 * seq bytes
+ * per head, plus the padded copies when dh is not 64 or 128 or a matrix is
+ * not 16-byte aligned (the stream's workspace block, see vedic_gemm). */
 int vedic_flash_attention_bwd(const float* Q, const float* K, const float* V, const float* O, const float* dO,
                               const float* lse, float* dQ, float* dK, float* dV, int seq, int dh, float scale,
                               int causal, int shunyam, int window, int stride, void* stream);

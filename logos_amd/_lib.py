@@ -77,6 +77,7 @@ SIGNATURES = {
     "vedic_gemm": (c_int, [ctypes.POINTER(GemmDesc)]),
     "vedic_gemm_noalloc": (c_int, [ctypes.POINTER(GemmDesc)]),
     "vedic_noalloc_scratch_bytes": (ctypes.c_size_t, []),
+    "vedic_workspace_release": (c_int, [c_vp]),
     "vedic_gemm_f32": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     "vedic_gemm_bias_f32": (c_int, [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     "vedic_gemm_f16_f32out": (c_int, [c_vp, c_int, c_int, c_vp, c_int, c_vp, c_float, c_float, c_vp]),

@@ -6,6 +6,9 @@
 #include <stdlib.h>
 
 #include <atomic>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "../../include/logos_vedic.h"
 #include "vedic_flash_attn.hpp"
@@ -58,33 +61,118 @@ static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; 
 // Largest leading dimension (elements) the kernels' 32-bit tile offsets allow.
 static constexpr int64_t kMaxLd = int64_t(1) << 22;
 
-// Temporary device memory of one library call (split-K partial slabs, column
-// partials, an AMP cast buffer).  By default each piece is taken from the
-// device's stream-ordered pool (hipMallocAsync on the call's stream) and
-// returned to it the same way.  Bound to a fixed region instead (the
-// allocation-free entry point), pieces are carved from it in order and
-// nothing is allocated or freed; a request past its end sets `overflow` and
-// fails, and the call reports VEDIC_STATUS_TOO_LARGE.
+// Temporary device memory of library calls (split-K partial slabs, column
+// partials, the AMP cast buffer, attention partials and padded copies) comes
+// from an arena per (device, stream): grown on demand and kept for the next
+// call on the same stream, whose work runs after this call's in stream
+// order, so one block of memory serves every call without an allocation per
+// call (a stream-ordered hipMallocAsync / hipFreeAsync pair left the GPU idle
+// 2-3 us between a call's kernels on MI355X).  An arena's lock is held from a
+// call's first request until the call has enqueued its last kernel: host
+// threads that share a stream would otherwise interleave their kernels over
+// the same memory.  Workspaces nested in one call (same thread) carve after
+// the outer one's pieces.  The memory is held until the process ends or
+// vedic_workspace_release is called for the stream.
+struct StreamArena {
+    std::recursive_mutex mu;
+    char* base = nullptr;
+    size_t cap = 0, used = 0, want = 0;
+};
+
+static std::mutex g_arenas_mu;
+static std::map<std::pair<int, hipStream_t>, StreamArena*> g_arenas;  // entries live until the process ends
+
+static StreamArena* arena_of(hipStream_t s) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lk(g_arenas_mu);
+    StreamArena*& a = g_arenas[std::make_pair(dev, s)];
+    if (!a) a = new StreamArena();
+    return a;
+}
+
+// One call's temporaries: pieces carved in order from the stream's arena (a
+// piece that does not fit comes from the stream-ordered pool, and the arena
+// grows to fit the whole call at the next call's first request).  Bound to a
+// fixed region instead (the allocation-free entry point), pieces are carved
+// from it and nothing is allocated or freed; a request past its end sets
+// `overflow` and fails, and the call reports VEDIC_STATUS_TOO_LARGE.
 struct Workspace {
     hipStream_t s = nullptr;
     char* region = nullptr;  // non-null: carve from [region, region + cap)
     size_t cap = 0, used = 0;
     bool overflow = false;
+    StreamArena* arena = nullptr;  // locked while this workspace is alive
+    size_t mark = 0;               // the arena's fill when this workspace took it
+    void* extra[8] = {};           // pieces from the pool (did not fit the arena)
+
+    Workspace() = default;
+    Workspace(const Workspace&) = delete;
+    Workspace& operator=(const Workspace&) = delete;
+    ~Workspace() {
+        for (void* p : extra)
+            if (p) (void)hipFreeAsync(p, s);
+        if (arena) {
+            arena->used = mark;
+            arena->mu.unlock();
+        }
+    }
 
     bool fixed() const { return region != nullptr; }
     template <typename T>
     hipError_t get(T** p, size_t bytes) {
-        if (!fixed()) return hipMallocAsync(reinterpret_cast<void**>(p), bytes, s);
         const size_t take = (bytes + 255) / 256 * 256;
-        if (take > cap - used) {
-            overflow = true;
-            return hipErrorOutOfMemory;
+        if (fixed()) {
+            if (take > cap - used) {
+                overflow = true;
+                return hipErrorOutOfMemory;
+            }
+            *p = reinterpret_cast<T*>(region + used);
+            used += take;
+            return hipSuccess;
         }
-        *p = reinterpret_cast<T*>(region + used);
-        used += take;
+        if (!arena) {
+            StreamArena* a = arena_of(s);
+            a->mu.lock();
+            arena = a;
+            mark = a->used;
+            if (a->used == 0 && a->want > a->cap) {
+                // grow (the old block is freed after the work queued on it)
+                if (a->base) (void)hipFreeAsync(a->base, s);
+                a->base = nullptr;
+                a->cap = 0;
+                if (hipMallocAsync(reinterpret_cast<void**>(&a->base), a->want, s) == hipSuccess)
+                    a->cap = a->want;
+                else
+                    a->base = nullptr;
+            }
+        }
+        StreamArena* a = arena;
+        if (take <= a->cap - a->used) {
+            *p = reinterpret_cast<T*>(a->base + a->used);
+            a->used += take;
+            return hipSuccess;
+        }
+        if (a->used + take > a->want) a->want = a->used + take;
+        for (void*& slot : extra)
+            if (!slot) {
+                const hipError_t e = hipMallocAsync(reinterpret_cast<void**>(p), bytes, s);
+                if (e == hipSuccess) slot = *p;
+                return e;
+            }
+        return hipErrorOutOfMemory;  // more than 8 pool pieces in one call: not reached by this library
+    }
+    // A piece's end of use in this call (its memory goes back at the end of
+    // the call; pool pieces are freed now).
+    hipError_t put(void* p) {
+        if (!p || fixed()) return hipSuccess;
+        for (void*& slot : extra)
+            if (slot == p) {
+                slot = nullptr;
+                return hipFreeAsync(p, s);
+            }
         return hipSuccess;
     }
-    hipError_t put(void* p) { return fixed() || !p ? hipSuccess : hipFreeAsync(p, s); }
 };
 
 // ------------------------------------------------------------ split-K
@@ -534,6 +622,27 @@ __global__ void cast_rows_f16_kernel(const float* __restrict__ src, int64_t lds,
         for (int c = threadIdx.x; c < K; c += blockDim.x) dst[(int64_t)r * K + c] = to_half_clamped(src[r * lds + c]);
 }
 
+// The same, eight values per thread and step (two 16-byte loads, one 16-byte
+// store): K and lds multiples of 8, src 16-byte aligned.
+__global__ void cast_rows8_f16_kernel(const float* __restrict__ src, int64_t lds, _Float16* __restrict__ dst, int M,
+                                      int K) {
+    const int k8 = K / 8;
+    const int64_t n = (int64_t)M * k8;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / k8;
+        const int c = (int)(i - r * k8) * 8;
+        const float4_t* s4 = reinterpret_cast<const float4_t*>(src + r * lds + c);
+        const float4_t a = s4[0], b = s4[1];
+        half8_t h;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            h[j] = to_half_clamped(a[j]);
+            h[4 + j] = to_half_clamped(b[j]);
+        }
+        *reinterpret_cast<half8_t*>(dst + r * K + c) = h;
+    }
+}
+
 // The AMP product for an fp32 A the in-kernel conversion cannot read
 // (unaligned base or leading dimension, K not a multiple of 8, very long
 // rows): A is cast into a stream-ordered binary16 workspace first, as the
@@ -547,8 +656,15 @@ static int amp_via_cast(const vedic_gemm_desc_t* d, float* const* heads, int nhe
     _Float16* a16 = nullptr;
     hipError_t e = ws.get(&a16, sizeof(_Float16) * (size_t)d->M * d->K);
     if (e != hipSuccess) return ws.overflow ? VEDIC_STATUS_TOO_LARGE : hip_status(e);
-    hipLaunchKernelGGL(cast_rows_f16_kernel, dim3((unsigned)(d->M < 4096 ? d->M : 4096)), dim3(256), 0, s,
-                       static_cast<const float*>(d->A), d->lda, a16, d->M, d->K);
+    if (d->K % 8 == 0 && d->lda % 8 == 0 && aligned16(d->A)) {
+        const int64_t n = (int64_t)d->M * (d->K / 8);
+        const int64_t blocks = (n + 255) / 256;
+        hipLaunchKernelGGL(cast_rows8_f16_kernel, dim3((unsigned)(blocks < 8192 ? blocks : 8192)), dim3(256), 0, s,
+                           static_cast<const float*>(d->A), d->lda, a16, d->M, d->K);
+    } else {
+        hipLaunchKernelGGL(cast_rows_f16_kernel, dim3((unsigned)(d->M < 4096 ? d->M : 4096)), dim3(256), 0, s,
+                           static_cast<const float*>(d->A), d->lda, a16, d->M, d->K);
+    }
     e = hipGetLastError();
     int st = hip_status(e);
     if (e == hipSuccess) {
@@ -602,6 +718,18 @@ extern "C" int vedic_gemm_noalloc(const vedic_gemm_desc_t* d) {
 }
 
 extern "C" size_t vedic_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int vedic_workspace_release(void* stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    StreamArena* a = arena_of(s);
+    std::lock_guard<std::recursive_mutex> lk(a->mu);
+    hipError_t e = hipSuccess;
+    if (a->base) e = hipFreeAsync(a->base, s);
+    a->base = nullptr;
+    a->cap = 0;
+    a->want = 0;
+    return hip_status(e);
+}
 
 extern "C" void vedic_debug_set_workspace_guard(int on) { g_ws_guard.store(on ? 1 : 0); }
 
@@ -1259,8 +1387,10 @@ extern "C" int vedic_gemm_checked(const vedic_gemm_desc_t* d, float tolerance, v
     const size_t fbytes = (sizeof(float) * (size_t)N + 7) / 8 * 8;
     const size_t bytes = fbytes + sizeof(double) * (size_t)K * 2;
     const size_t scr_a = dsum_scratch(ar, ac, a_rows), scr_b = dsum_scratch(br, bc, b_rows);
+    Workspace wsc;
+    wsc.s = s;
     char* ws = nullptr;
-    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), bytes + sizeof(double) * (scr_a + scr_b), s);
+    hipError_t e = wsc.get(&ws, bytes + sizeof(double) * (scr_a + scr_b));
     if (e != hipSuccess) return hip_status(e);
     float* d_cs = reinterpret_cast<float*>(ws);
     double* d_sa = reinterpret_cast<double*>(ws + fbytes);
@@ -1271,7 +1401,7 @@ extern "C" int vedic_gemm_checked(const vedic_gemm_desc_t* d, float tolerance, v
     g.colsum = d_cs;
     g.colsum_beta = 0.0f;
     ColsumHandoff ho{nullptr, 0};
-    int st = gemm_impl(&g, nullptr, 0, 0, &ho);
+    int st = gemm_impl(&g, nullptr, 0, 0, &ho, &wsc);
     if (st == VEDIC_STATUS_OK) {
         // sa[k] = sum_m op(A)[m][k]; sb[k] = sum_n op(B)[k][n]
         if (d->in_dtype == VEDIC_DT_F16) {
@@ -1306,10 +1436,10 @@ extern "C" int vedic_gemm_checked(const vedic_gemm_desc_t* d, float tolerance, v
         st = hip_status(e);
     }
     if (ho.part) {
-        const hipError_t f = hipFreeAsync(ho.part, s);
+        const hipError_t f = wsc.put(ho.part);
         if (st == VEDIC_STATUS_OK && f != hipSuccess) st = hip_status(f);
     }
-    const hipError_t f = hipFreeAsync(ws, s);
+    const hipError_t f = wsc.put(ws);
     if (st == VEDIC_STATUS_OK && f != hipSuccess) st = hip_status(f);
     return st;
 }
@@ -1402,7 +1532,7 @@ static int flash_check(int nheads, int max_heads, int seq, int dh, int shunyam, 
     return VEDIC_STATUS_OK;
 }
 
-static int flash_launch(FlashArgs& a, int dh, hipStream_t s);
+static int flash_launch(FlashArgs& a, int dh, Workspace& ws);
 
 static int flash_impl(const float* const* Q, const float* const* K, const float* const* V, float* const* out,
                       float* const* lse, int nheads, int seq, int dh, float scale, int causal, int shunyam,
@@ -1452,11 +1582,13 @@ static int flash_impl(const float* const* Q, const float* const* K, const float*
     a.chunk = chunk;
     a.items = (int)items;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (!repack) return flash_launch(a, dh, s);
+    Workspace wsf;
+    wsf.s = s;
+    if (!repack) return flash_launch(a, dh, wsf);
     // padded copies of Q, K, V and the output, head after head
     const int64_t per = (int64_t)nheads * seq * dhp;
     float* ws = nullptr;
-    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), sizeof(float) * 4 * (size_t)per, s);
+    hipError_t e = wsf.get(&ws, sizeof(float) * 4 * (size_t)per);
     if (e != hipSuccess) return hip_status(e);
     float* const pq = ws;
     float* const pk = ws + per;
@@ -1474,16 +1606,17 @@ static int flash_impl(const float* const* Q, const float* const* K, const float*
             a.v[h] = pv + off;
             a.o[h] = po + off;
         }
-        st = flash_launch(a, dhp, s);
+        st = flash_launch(a, dhp, wsf);
         if (st == VEDIC_STATUS_OK) e = flash_repack(false, const_cast<const float* const*>(out), po, nheads, seq, dh, dhp, s);
     }
-    const hipError_t f = hipFreeAsync(ws, s);
+    const hipError_t f = wsf.put(ws);
     if (st != VEDIC_STATUS_OK) return st;
     return hip_status(e != hipSuccess ? e : f);
 }
 
 // The forward on prepared arguments (head dimension 64 or 128, aligned).
-static int flash_launch(FlashArgs& a, int dh, hipStream_t s) {
+static int flash_launch(FlashArgs& a, int dh, Workspace& wsf) {
+    hipStream_t s = wsf.s;
     const int full = a.nqg * kFaQ;
     if (a.chunk >= full) return hip_status(launch_flash_attn(a, dh, s));
     // Workspace: the chunk partials, then the work-item counter.  The split
@@ -1491,13 +1624,13 @@ static int flash_launch(FlashArgs& a, int dh, hipStream_t s) {
     // DH 64, one at DH 128) that take them largest first.
     const size_t bytes = sizeof(float) * (size_t)flash_slot_floats(dh) * (size_t)a.items * a.nheads;
     char* ws = nullptr;
-    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), bytes + 256, s);
+    hipError_t e = wsf.get(&ws, bytes + 256);
     if (e != hipSuccess) return hip_status(e);
     a.part = reinterpret_cast<float*>(ws);
     a.queue = reinterpret_cast<int*>(ws + bytes);
     a.queue_grid = (dh == 64 ? 3 : 1) * device_cu_count();
     e = launch_flash_attn(a, dh, s);
-    const hipError_t f = hipFreeAsync(ws, s);
+    const hipError_t f = wsf.put(ws);
     return hip_status(e != hipSuccess ? e : f);
 }
 
@@ -1562,9 +1695,10 @@ static int flash_bwd_impl(const float* const* Q, const float* const* K, const fl
     const int64_t per = (int64_t)nheads * seq * dhp;
     const size_t stat_floats = 2 * (size_t)seq * nheads;
     const size_t pad_at = (stat_floats + 63) / 64 * 64;  // 256-byte aligned copies
+    Workspace wsb;
+    wsb.s = s;
     float* ws = nullptr;
-    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws),
-                                  sizeof(float) * (repack ? pad_at + 8 * (size_t)per : stat_floats), s);
+    hipError_t e = wsb.get(&ws, sizeof(float) * (repack ? pad_at + 8 * (size_t)per : stat_floats));
     if (e != hipSuccess) return hip_status(e);
     a.delta = ws;
     if (!repack) {
@@ -1590,7 +1724,7 @@ static int flash_bwd_impl(const float* const* Q, const float* const* K, const fl
             e = flash_repack(false, const_cast<const float* const*>(outs[t]), pad + (5 + t) * per, nheads, seq, dh, dhp,
                              s);
     }
-    const hipError_t f = hipFreeAsync(ws, s);
+    const hipError_t f = wsb.put(ws);
     return hip_status(e != hipSuccess ? e : f);
 }
 
