@@ -42,11 +42,6 @@
 
 #include <type_traits>
 
-// 1: the last k step of each stage is carried past the next stage barrier
-// (mfma_stage_carry)
-#ifndef VEDIC_F16_CARRY
-#define VEDIC_F16_CARRY 0
-#endif
 
 #include "vedic_common.hpp"
 #include "vedic_epilogue.hpp"
@@ -309,51 +304,6 @@ __device__ __forceinline__ void mfma_stage(const char* la, const char* lb, int a
     }
 }
 
-// The MFMAs of one stage, with the last k step of each stage carried into
-// the next: on entry af[1] / bf[1] hold the previous stage's last fragments
-// (zero at the start of a tile), whose MFMAs go first, while this stage's
-// first reads are in flight; this stage's last fragments are left in
-// af[1] / bf[1] for the next stage (or the tile's final step).  After the
-// stage barrier a wave then has MFMAs to issue at once instead of waiting
-// for its first LDS reads.  Loads of a later stage (NV > 0) are spread as in
-// mfma_stage.
-template <bool A_KC, bool B_KC, int BM, int BN, int BK, int MI, int NI, int NV = 0, int EVERY = 1>
-__device__ __forceinline__ void mfma_stage_carry(const char* la, const char* lb, int ar0, int bc0, int lane,
-                                                 float16_t (&acc)[MI][NI], half8_t (&af)[2][MI], half8_t (&bf)[2][NI]) {
-    constexpr int KS = BK / 16;
-    static_assert(KS % 2 == 0, "the carried fragments sit in buffer 1");
-    constexpr int NR = (A_KC ? MI : 2 * MI) + (B_KC ? NI : 2 * NI);
-    constexpr int NM = MI * NI;
-    static_assert(NV <= KS * NM, "at most one load per MFMA");
-    constexpr int EV = NV == 0 || NV * EVERY <= KS * NM ? EVERY : KS * NM / NV;
-    // step t = 0 .. KS - 1: the MFMAs of k step t - 1 (t = 0: the carried
-    // one) while k step t is read into buffer t & 1
-#pragma unroll
-    for (int t = 0; t < KS; ++t) {
-        const int b = t & 1, u = b ^ 1;
-#pragma unroll
-        for (int i = 0; i < MI; ++i) af[b][i] = read_frag<A_KC, BM, BK>(la, ar0 + 32 * i, t, lane);
-#pragma unroll
-        for (int j = 0; j < NI; ++j) bf[b][j] = read_frag<B_KC, BN, BK>(lb, bc0 + 32 * j, t, lane);
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-            for (int j = 0; j < NI; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[u][i], bf[u][j], acc[i][j], 0, 0, 0);
-    }
-#pragma unroll
-    for (int t = 0; t < KS; ++t) {
-#pragma unroll
-        for (int x = 0; x < NM; ++x) {
-            const int m = t * NM + x;
-            __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-            if (x < NR) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
-            if (NV > 0 && (m + 1) % EV == 0 && (m + 1) / EV <= NV) __builtin_amdgcn_sched_group_barrier(kSgVmem, 1, 0);
-        }
-        if (NR > NM) __builtin_amdgcn_sched_group_barrier(kSgDsRead, NR > NM ? NR - NM : 1, 0);
-    }
-}
-
 // Logical tile t -> (tm, tn): GROUP_M tile rows at a time, column-major inside.
 __device__ __forceinline__ void tile_of(const GemmArgs& a, int t, int& tm, int& tn) {
     const int gm = a.group_m;
@@ -440,8 +390,6 @@ __global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f16_kernel(GemmArgs 
     // of issued together (2-3 % faster: fewer waves held at a full
     // texture-address queue); 128 x 128 tiles measured slower that way.
     constexpr bool kInterleave = BM * BN >= 256 * 256 && WGK == 1;
-    // the last k step of each stage carried past the next stage barrier
-    constexpr bool kCarry = VEDIC_F16_CARRY && !A32 && WGK == 1 && (BK / 16) % 2 == 0;
 
     // One LDS object per stage (A then B): reads of one stage provably do not
     // alias the direct loads into another.  The compiler follows only a few
@@ -497,13 +445,6 @@ __global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f16_kernel(GemmArgs 
         for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int j = 0; j < NI; ++j) acc[i][j] = float16_t{};
-        half8_t caf[2][MI], cbf[2][NI];  // carried fragments (kCarry): none at the start of a tile
-        if constexpr (kCarry) {
-#pragma unroll
-            for (int i = 0; i < MI; ++i) caf[1][i] = half8_t{};
-#pragma unroll
-            for (int j = 0; j < NI; ++j) cbf[1][j] = half8_t{};
-        }
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
             const int col = n0 + wn * WN + 32 * j + lane % 32;
@@ -530,9 +471,6 @@ __global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f16_kernel(GemmArgs 
                     wait_lgkmcnt0();
                 } else {
                     wait_vmcnt<(ST - 2) * L>();  // stage kt has landed; ST - 2 later stages in flight
-                    // carried reads of the previous stage are done before
-                    // its buffer can be loaded again
-                    if constexpr (kCarry) wait_lgkmcnt0();
                 }
                 stage_barrier();
                 const int sl = (s + ST - 1) % ST;
@@ -547,19 +485,10 @@ __global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f16_kernel(GemmArgs 
                     // the loads and the MFMAs in one block, one load after each of the first L MFMAs
                     if (kt < nk) {
                         VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
-                        if constexpr (kCarry)
-                            mfma_stage_carry<A_KC, B_KC, BM, BN, BK, MI, NI, L, 1>(As[s], Bs[s], wm * WM, wn * WN, lane,
-                                                                                  acc, caf, cbf);
-                        else
-                            mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI, L, 1>(As[s], Bs[s], wm * WM, wn * WN, lane, acc);
+                        mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI, L, 1>(As[s], Bs[s], wm * WM, wn * WN, lane, acc);
                     } else {
                         VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
                     }
-                } else if constexpr (kCarry) {
-                    VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
-                    if (kt < nk)
-                        mfma_stage_carry<A_KC, B_KC, BM, BN, BK, MI, NI>(As[s], Bs[s], wm * WM, wn * WN, lane, acc, caf,
-                                                                         cbf);
                 } else {
                     VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
                     if (kt < nk)
@@ -569,14 +498,6 @@ __global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f16_kernel(GemmArgs 
             }
         }
 
-        if constexpr (kCarry) {
-            // the last stage's last k step
-#pragma unroll
-            for (int i = 0; i < MI; ++i)
-#pragma unroll
-                for (int j = 0; j < NI; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(caf[1][i], cbf[1][j], acc[i][j], 0, 0, 0);
-        }
         if constexpr (WGK > 1) {
             // the trailing stage loads (zeros past the range) still write the
             // buffers: wait for them and for every wave's last reads
