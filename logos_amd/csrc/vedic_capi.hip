@@ -5,7 +5,10 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <immintrin.h>
+
 #include <atomic>
+#include <chrono>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -1033,13 +1036,16 @@ constexpr int kDsumChunk = 64;
 
 // res[0] = sum_j cs[j], res[1] = sum_k sa[k] sb[k], res[2] = sum_j bias[j]
 // (bias may be null), by one workgroup with a fixed stride-1024 order and a
-// fixed tree.
+// fixed tree; then `flag` (host memory) = seq, released at system scope after
+// the three results, so a host thread polling the flag may read them.
 constexpr int kFinThreads = 1024;
 __global__ void __launch_bounds__(kFinThreads) checksum_finalize_kernel(const float* __restrict__ cs, int N,
                                                                         const double* __restrict__ sa,
                                                                         const double* __restrict__ sb, int K,
                                                                         const float* __restrict__ bias,
-                                                                        double* __restrict__ res) {
+                                                                        double* __restrict__ res,
+                                                                        unsigned long long* flag,
+                                                                        unsigned long long seq) {
     __shared__ double red[3][kFinThreads];
     double s0 = 0.0, s1 = 0.0, s2 = 0.0;
 #pragma unroll 8
@@ -1058,7 +1064,12 @@ __global__ void __launch_bounds__(kFinThreads) checksum_finalize_kernel(const fl
             for (int t = 0; t < 3; ++t) red[t][threadIdx.x] += red[t][threadIdx.x + w];
         __syncthreads();
     }
-    if (threadIdx.x < 3) res[threadIdx.x] = red[threadIdx.x][0];
+    if (threadIdx.x < 3) {
+        res[threadIdx.x] = red[threadIdx.x][0];
+        __threadfence_system();
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(flag, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // Doubles of scratch the column partials need for a column sum of `rows` x `cols`.
@@ -1259,6 +1270,23 @@ struct PinnedSlot {
     }
 };
 
+// Waits until the finalize kernel has published call `seq` in the slot's
+// flag: polls the host-memory flag for up to 20 ms (the result is usually
+// there within microseconds of the kernel's end, where a stream
+// synchronisation takes tens of microseconds to return), then falls back to
+// hipStreamSynchronize, which also reports any error of the queued work.
+static hipError_t wait_slot(const unsigned long long* flag, unsigned long long seq, hipStream_t s) {
+    const auto t0 = std::chrono::steady_clock::now();
+    for (unsigned spin = 0;; ++spin) {
+        if (__atomic_load_n(flag, __ATOMIC_ACQUIRE) == seq) return hipSuccess;
+        if ((spin & 1023) == 1023 && std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(20)) break;
+        _mm_pause();
+    }
+    hipError_t e = hipStreamSynchronize(s);
+    if (e == hipSuccess && __atomic_load_n(flag, __ATOMIC_ACQUIRE) != seq) e = hipErrorUnknown;
+    return e;
+}
+
 static double* result_slot(double** dev, hipError_t& e) {
     static thread_local PinnedSlot slot;
     e = hipSuccess;
@@ -1416,14 +1444,17 @@ extern "C" int vedic_gemm_checked(const vedic_gemm_desc_t* d, float tolerance, v
                                         dsum_job(B, d->ldb, br, bc, b_rows, d_sb, d_scr_b), ho, N, d_cs, s);
         }
         double* res_dev = nullptr;
-        const double* res = nullptr;  // 3 doubles, written by the finalize kernel
+        const double* res = nullptr;  // 3 doubles, then the flag, written by the finalize kernel
+        static thread_local unsigned long long g_check_seq = 0;
+        const unsigned long long seq = ++g_check_seq;
         if (e == hipSuccess) res = result_slot(&res_dev, e);
         if (e == hipSuccess) {
             hipLaunchKernelGGL(checksum_finalize_kernel, dim3(1), dim3(kFinThreads), 0, s, d_cs, N, d_sa, d_sb, K,
-                               want_bias ? d->bias : nullptr, res_dev);
+                               want_bias ? d->bias : nullptr, res_dev,
+                               reinterpret_cast<unsigned long long*>(res_dev + 3), seq);
             e = hipGetLastError();
         }
-        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e == hipSuccess) e = wait_slot(reinterpret_cast<const unsigned long long*>(res + 3), seq, s);
         if (e == hipSuccess) {
             const double host[3] = {res[0], res[1], res[2]};
             const double pred = (double)d->alpha * host[1] + (double)M * host[2];

@@ -80,10 +80,19 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Workgroup barrier without the fences of __syncthreads; the empty asm
-// statements keep the compiler from moving memory operations across it.
+// Workgroup barrier for the stage pipelines, without the global-memory
+// fences of __syncthreads.  Each wave first waits for its own LDS reads to
+// return (lgkmcnt(0)): after the barrier another wave may start direct loads
+// into a buffer this wave has just read, and the compiler places a stage's
+// last MFMAs -- and the waits for their fragments -- after the barrier.  A
+// read still in flight there could be overtaken by the new data, which
+// arrives within a few hundred cycles for the zero loads past a work item's
+// range (no memory access), and sooner still when another kernel's
+// workgroup on the same CU holds up the LDS.  The empty asm statements keep
+// the compiler from moving memory operations across the barrier.
 __device__ __forceinline__ void stage_barrier() {
     asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0), vmcnt and expcnt untouched
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 }

@@ -126,3 +126,45 @@ def test_threads_sharing_a_stream():
     for t, r in enumerate(refs):
         for g in outs[t]:
             assert torch.equal(g, r)
+
+
+def test_checked_gemm_with_work_queued_ahead_and_threads():
+    """vedic_gemm_checked returns once its last kernel has published the
+    result in host memory (polled, with a stream synchronisation as the
+    fallback).  With a long product queued ahead on the same stream, and with
+    four host threads each on its own stream, every call returns the values
+    of a quiet single-thread call, bit for bit."""
+    vedic = V()
+    rng = np.random.default_rng(4)
+    M, N, K = 1024, 2048, 1024
+    cases = [(dev(normal(rng, (M, K))).half(), dev(normal(rng, (K, N), std=0.02)).half()) for _ in range(4)]
+    refs = []
+    for a, b in cases:
+        C, r = vedic.gemm_checked(vedic.OP_NN, a, b)
+        refs.append((C.clone(), r.checksum_C, r.checksum_vedic))
+    big_a = dev(normal(rng, (8192, 4096))).half()
+    big_b = dev(normal(rng, (4096, 4096), std=0.02)).half()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            vedic.gemm(vedic.OP_NN, big_a, big_b)  # about a millisecond of queued work
+        C, r = vedic.gemm_checked(vedic.OP_NN, *cases[0])
+        assert torch.equal(C, refs[0][0]) and (r.checksum_C, r.checksum_vedic) == refs[0][1:]
+    torch.cuda.synchronize()
+    errors = []
+
+    def work(t):
+        st = torch.cuda.Stream()
+        with torch.cuda.stream(st):
+            for _ in range(20):
+                C, r = vedic.gemm_checked(vedic.OP_NN, *cases[t])
+                if not (torch.equal(C, refs[t][0]) and (r.checksum_C, r.checksum_vedic) == refs[t][1:]):
+                    errors.append(t)
+
+    threads = [threading.Thread(target=work, args=(t,)) for t in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    torch.cuda.synchronize()
+    assert not errors
