@@ -164,19 +164,32 @@ def _pmc_kib(dirpath: str, counter: str, kernel_substr: str):
     return sum(vals) / len(vals), len(vals)
 
 
-def _pmc_library_total(dirpath: str, counter: str):
-    """Sum of `counter` over every dispatch of this library's kernels."""
+# Kernels of the profiled process that are not the library's: torch's own
+# (input set-up) and the runtime's blits.
+_NOT_LIBRARY = ("at::native", "copyBuffer", "fillBuffer", "elementwise_kernel")
+# Kernels whose global reads are 64-byte requests (FETCH_SIZE counts them at
+# their size); every other kernel's reads are 128-byte requests, which
+# FETCH_SIZE counts as 64 bytes on gfx950 (hence the copy calibration).
+_FETCH_64B = ("gemm_skinny_kernel<vedic::SkinnyF16",)
+
+
+def _pmc_library_total(dirpath: str, counter: str, only_64b=None):
+    """Sum of `counter` over every dispatch of this library's kernels (only_64b:
+    True for the 64-byte-request kernels only, False for the others)."""
     total, n = 0.0, 0
     for root, _, files in os.walk(dirpath):
         for fn in files:
             if fn.endswith("counter_collection.csv"):
                 with open(os.path.join(root, fn)) as f:
                     for r in csv.DictReader(f):
-                        if r["Counter_Name"] == counter and "vedic" in r["Kernel_Name"] \
-                                and "at::native" not in r["Kernel_Name"]:
-                            total += float(r["Counter_Value"])
-                            n += 1
-    if not n:
+                        name = r["Kernel_Name"]
+                        if r["Counter_Name"] != counter or any(x in name for x in _NOT_LIBRARY):
+                            continue
+                        if only_64b is not None and any(x in name for x in _FETCH_64B) != only_64b:
+                            continue
+                        total += float(r["Counter_Value"])
+                        n += 1
+    if not n and only_64b is None:
         raise SystemExit(f"no {counter} rows of the library's kernels under {dirpath}")
     return total, n
 
@@ -188,14 +201,15 @@ def summarize_traffic(args):
     reads for torch's copy of 256 MiB (bench.py --workload copy_256mib)."""
     fetch_dir, write_dir, cfetch_dir, cwrite_dir = args.summarize_traffic
     steps = args.profiled_steps
-    fetch, _ = _pmc_library_total(fetch_dir, "FETCH_SIZE")
+    fetch, _ = _pmc_library_total(fetch_dir, "FETCH_SIZE", only_64b=False)
+    fetch64, _ = _pmc_library_total(fetch_dir, "FETCH_SIZE", only_64b=True)
     write, _ = _pmc_library_total(write_dir, "WRITE_SIZE")
-    fetch, write = fetch / steps, write / steps
+    fetch, fetch64, write = fetch / steps, fetch64 / steps, write / steps
     cfetch, _ = _pmc_kib(cfetch_dir, "FETCH_SIZE", "copyBuffer")
     cwrite, _ = _pmc_kib(cwrite_dir, "WRITE_SIZE", "copyBuffer")
     ref_kib = 256.0 * 1024
     f_fetch, f_write = ref_kib / cfetch, ref_kib / cwrite
-    hbm = (fetch * f_fetch + write * f_write) * 1024.0
+    hbm = (fetch * f_fetch + fetch64 + write * f_write) * 1024.0
     out = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.txt")
     with open(out, "w") as f:
         f.write(f"# HBM traffic per step of bench.py --workload {args.workload} (the library's dispatches)\n")
@@ -205,8 +219,10 @@ def summarize_traffic(args):
                 f"{args.workload} (KiB per dispatch),\n")
         f.write("# each scaled by the same counter on torch's copy of 256 MiB (bench.py --workload copy_256mib).\n")
         f.write("# FETCH_SIZE counts L2-to-fabric reads: repeated fetches by different XCDs' L2s\n")
-        f.write("# are all counted, whether the Infinity Cache or HBM serves them.\n")
-        f.write(f"fetch_kib_per_step: {fetch:.1f}\nwrite_kib_per_step: {write:.1f}\n")
+        f.write("# are all counted, whether the Infinity Cache or HBM serves them.  The decode\n")
+        f.write("# kernel's fp16 reads are 64-byte requests, counted at their size: their FETCH is not scaled.\n")
+        f.write(f"fetch_kib_per_step: {fetch:.1f}\nfetch_64b_kib_per_step: {fetch64:.1f}\n"
+                f"write_kib_per_step: {write:.1f}\n")
         f.write(f"copy_fetch_kib: {cfetch:.1f}\ncopy_write_kib: {cwrite:.1f}\n")
         f.write(f"fetch_scale: {f_fetch:.4f}\nwrite_scale: {f_write:.4f}\n")
         f.write(f"hbm_bytes_per_launch: {int(hbm)}\n")
