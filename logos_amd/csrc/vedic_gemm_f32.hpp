@@ -450,10 +450,11 @@ struct CfgF32Small {
 // One 32 x 64 tile per workgroup, the contraction split four ways among its
 // four waves (f32_wave_split; NN and NT, whose A rows are K-contiguous): each
 // wave owns the whole 32 x 64 output block (two accumulator chains) over one
-// 8-k chunk of every 32-k stage.  Four 12 KiB stages plus 24 KiB for the
-// partials.
+// 8-k chunk of every 32-k stage.  Two 12 KiB stages plus 24 KiB for the
+// partials (512 x 1024 x 1024: 15.9-16.7 us against 17.3-18.0 us with four
+// stages and 16.6-16.9 us with three, same bits).
 struct CfgF32WaveK {
-    static constexpr int BM = 32, BN = 64, ST = 4, WGM = 1, WGN = 1, WGK = 4;
+    static constexpr int BM = 32, BN = 64, ST = 2, WGM = 1, WGN = 1, WGK = 4;
     static constexpr int PER_CU = 2;
 };
 
