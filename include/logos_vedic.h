@@ -321,10 +321,16 @@ int vedic_gemm_checked(const vedic_gemm_desc_t* desc, float tolerance, vedic_ver
  * Masked scores are left out of the sums; a row whose sum is <= 1e-9 is 0.
  * Replaces cuda_flash_attention_fwd (cuda/VedicGEMM.cuh:236, cuda/VedicGEMM.cu:1065-1104;
  * kernel :898-1063), called per head at cuda/ModelGPU.cu:959-968.
+ * attn (NULL, or [seq x seq]): the reference's optional probability copy,
+ * with the reference's values (its flash kernel walks the keys in tiles of 32
+ * with a running row maximum): an allowed key k gets expf(s_k - m_t) / l,
+ * m_t the running maximum after the tile holding k and l the row sum; a
+ * masked key keeps its previous content times 1 / l (the reference's final
+ * pass scales the whole row; 0 for a row with l <= 1e-9).  Computed by a
+ * second kernel after the output, two passes over the keys.
  * Limits: 1 <= dh <= 128 (BAD_DIM otherwise, where the reference throws);
- * `attn` (the reference's optional copy of the probabilities, NULL at its
- * only call site) must be NULL (UNSUPPORTED otherwise); stride >= 1 when the
- * sparse mask applies; seq * (dh <= 64 ? 64 : 128) < 2^29.  The kernels run
+ * stride >= 1 when the sparse mask applies; seq * (dh <= 64 ? 64 : 128) <
+ * 2^29.  The kernels run
  * at dh 64 and 128 on 16-byte-aligned matrices; any other dh, or an
  * unaligned matrix, is copied into zero-padded [seq x 64] or [seq x 128]
  * matrices first and the output copied back (the zero columns add exact

@@ -33,6 +33,7 @@ SOURCES = [
     "vedic_gemm_skinny.hip",
     "vedic_flash_attn.hip",
     "vedic_flash_attn_bwd.hip",
+    "vedic_flash_probs.hip",
     "vedic_capi.hip",
 ]
 

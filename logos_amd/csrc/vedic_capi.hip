@@ -1668,8 +1668,20 @@ static int flash_launch(FlashArgs& a, int dh, Workspace& wsf) {
 extern "C" int vedic_flash_attention_fwd(const float* Q, const float* K, const float* V, float* out, float* attn,
                                          int seq, int dh, float scale, int causal, int shunyam, int window,
                                          int stride, void* stream) {
-    if (attn != nullptr) return VEDIC_STATUS_UNSUPPORTED;
-    return flash_impl(&Q, &K, &V, &out, nullptr, 1, seq, dh, scale, causal, shunyam, window, stride, stream);
+    const int st = flash_impl(&Q, &K, &V, &out, nullptr, 1, seq, dh, scale, causal, shunyam, window, stride, stream);
+    if (st != VEDIC_STATUS_OK || attn == nullptr) return st;
+    // the reference's probability copy, after the output (same masks and scale)
+    FlashArgs a{};
+    a.q[0] = Q;
+    a.k[0] = K;
+    a.nheads = 1;
+    a.seq = seq;
+    a.causal = causal ? 1 : 0;
+    a.sparse = (shunyam && seq > window) ? 1 : 0;
+    a.window = window;
+    a.stride = a.sparse ? stride : 1;
+    a.scale = scale;
+    return hip_status(launch_flash_probs(a, dh, attn, static_cast<hipStream_t>(stream)));
 }
 
 extern "C" int vedic_flash_attention_fwd_lse(const float* Q, const float* K, const float* V, float* out, float* lse,

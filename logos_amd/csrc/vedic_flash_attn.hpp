@@ -56,6 +56,9 @@ __device__ __forceinline__ float fa_lse(float m2, float l) {
 int64_t flash_items_per_head(int seq, int chunk, int causal);
 int flash_slot_floats(int dh);
 hipError_t launch_flash_attn(const FlashArgs& a, int dh, hipStream_t s);
+// The reference's optional probability copy attn[seq x seq] of head 0 of `a`
+// (Q rows of dh values, any dh <= 128; vedic_flash_probs.hip).
+hipError_t launch_flash_probs(const FlashArgs& a, int dh, float* attn, hipStream_t s);
 
 // Backward: heads per launch (nine pointer arrays in the kernel arguments).
 constexpr int kFaBwdHeads = 32;

@@ -409,9 +409,13 @@ def flash_attention_fwd(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, out: 
     defaults to 1/sqrt(dh), the caller's value (cuda/ModelGPU.cu:963).  The
     mask drops keys after the query (causal) and, with shunyam and seq >
     window, keys outside [query - window, query] that are not multiples of
-    stride.  `attn` (the reference's optional probability copy) must be None.
-    lse (optional float32 [seq] GPU tensor) receives each row's log-sum-exp
-    ln(sum over allowed keys of e^(scale q.k)), for flash_attention_bwd."""
+    stride.  attn (optional contiguous float32 [seq x seq] GPU tensor)
+    receives the reference's probability copy, with the reference's values:
+    allowed entries expf(s - m_t) / l (m_t the running maximum after the
+    32-key tile holding the key), masked entries their previous content / l.
+    lse (optional float32 [seq] GPU tensor, not together with attn) receives
+    each row's log-sum-exp ln(sum over allowed keys of e^(scale q.k)), for
+    flash_attention_bwd."""
     seq, dh = _head(Q, "Q")
     _head(K, "K", seq, dh)
     _head(V, "V", seq, dh)
@@ -423,11 +427,15 @@ def flash_attention_fwd(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, out: 
     flags = (float(scale), int(causal), int(shunyam), int(window), int(stride), _stream())
     if lse is not None:
         if attn is not None:
-            raise ValueError("attn must be None")
+            raise ValueError("attn and lse are separate calls")
         _vec(lse, "lse", seq)
         _check(_lib.load().vedic_flash_attention_fwd_lse(Q.data_ptr(), K.data_ptr(), V.data_ptr(), out.data_ptr(),
                                                          lse.data_ptr(), seq, dh, *flags))
         return out
+    if attn is not None:
+        if not isinstance(attn, torch.Tensor) or not attn.is_cuda or attn.dtype != torch.float32 \
+                or tuple(attn.shape) != (seq, seq) or not attn.is_contiguous():
+            raise ValueError(f"attn must be a contiguous float32 [{seq} x {seq}] GPU matrix")
     ap = None if attn is None else attn.data_ptr()
     _check(_lib.load().vedic_flash_attention_fwd(Q.data_ptr(), K.data_ptr(), V.data_ptr(), out.data_ptr(), ap, seq,
                                                  dh, *flags))

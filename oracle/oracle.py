@@ -454,6 +454,42 @@ def flash_attention_f64(Q, K, V, scale, causal=True, shunyam=False, window=0, st
     return np.where(den > 0, (P @ V) / np.where(den > 0, den, 1.0), 0.0)
 
 
+def flash_attention_probs(Q, K, scale, causal=True, shunyam=False, window=0, stride=1, prior=None,
+                          rows=None) -> np.ndarray:
+    """The reference's optional probability copy `Aptr` (cuda/VedicGEMM.cu:906,
+    1033-1037, 1056-1060) restated in fp32: keys walked in tiles of 32
+    (FA_TILE) with the running row maximum m (-1e30 before any allowed key);
+    an allowed key of tile t is written expf(s - m_t), m_t the maximum after
+    tile t; the row sum l accumulates with the online rescaling; finally the
+    whole row, masked entries included (never written, so they keep `prior`),
+    is multiplied by 1/l (0 if l <= 1e-9).  prior: the buffer's previous
+    content (zeros if None).  rows: optional query subset (rows are
+    independent); the result then has one row per entry."""
+    Q, K = _f32(Q), _f32(K)
+    seq = K.shape[0]
+    idx = np.arange(seq) if rows is None else np.asarray(rows)
+    f = np.float32
+    S = (Q[idx] @ K.T).astype(f) * f(scale)
+    allowed = attention_mask(seq, causal, shunyam, window, stride)[idx]
+    S = np.where(allowed, S, f(-1e30))
+    n = len(idx)
+    out = np.zeros((n, seq), dtype=f) if prior is None else np.array(prior, dtype=f, copy=True)
+    m = np.full(n, -1e30, dtype=f)
+    l = np.zeros(n, dtype=f)
+    for k0 in range(0, seq, 32):
+        blk = S[:, k0:k0 + 32]
+        ok = allowed[:, k0:k0 + 32]
+        mn = np.maximum(m, blk.max(axis=1))
+        ln = l * np.exp(m - mn)
+        e = np.exp(blk - mn[:, None]).astype(f)
+        for j in range(blk.shape[1]):  # the reference's order of additions
+            ln = np.where(ok[:, j], ln + e[:, j], ln).astype(f)
+        out[:, k0:k0 + 32] = np.where(ok, e, out[:, k0:k0 + 32])
+        m, l = mn, ln
+    inv = np.where(l > f(1e-9), f(1) / np.where(l > 0, l, f(1)), f(0)).astype(f)
+    return (out * inv[:, None]).astype(f)
+
+
 def flash_attention(Q, K, V, scale, causal=True, shunyam=False, window=0, stride=1) -> np.ndarray:
     """The reference's flash_attention_kernel restated on the CPU (fp32)."""
     Q, K, V = _f32(Q), _f32(K), _f32(V)

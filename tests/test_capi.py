@@ -102,7 +102,6 @@ def test_flash_attention_validation():
     f = lib.vedic_flash_attention_fwd
     assert f(p, p, p, p, None, 0, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_BAD_DIM
     assert f(p, p, p, p, None, 16, 256, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_BAD_DIM
-    assert f(p, p, p, p, p, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED  # attn copy
     assert f(p, p, p, None, None, 16, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_NULL_POINTER
     assert f(p, p, p, p, None, 16, 64, 0.125, 1, 1, 4, 0, None) == _lib.STATUS_BAD_DIM  # stride 0, sparse on
     assert f(p, p, p, p, None, 1 << 23, 64, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_TOO_LARGE
@@ -122,21 +121,20 @@ def test_flash_attention_validation():
 
 def test_flash_attention_refusals():
     """The attention entry points take any DH from 1 to 128, as the reference
-    (cuda/VedicGEMM.cu:1074-1079); DH outside that range is BAD_DIM (the
-    reference throws above 128), and a non-null attn pointer (the reference's
-    optional probability copy, NULL at its only call site) UNSUPPORTED.  The
-    checks come before any launch, so the pointers are never dereferenced."""
+    (cuda/VedicGEMM.cu:1074-1079), and the optional probability copy; DH
+    outside that range is BAD_DIM (the reference throws above 128), with or
+    without the copy.  The checks come before any launch, so the pointers are
+    never dereferenced."""
     lib = _lib.load()
     p = 4096  # never dereferenced: the calls are refused on the host
     f = lib.vedic_flash_attention_fwd
     for dh in (0, -1, 129, 256):
         assert f(p, p, p, p, None, 256, dh, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_BAD_DIM, dh
+        assert f(p, p, p, p, p, 256, dh, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_BAD_DIM, dh
         assert lib.vedic_flash_attention_fwd_lse(p, p, p, p, p, 256, dh, 0.125, 1, 0, 0, 1, None) == \
             _lib.STATUS_BAD_DIM, dh
         assert lib.vedic_flash_attention_bwd(p, p, p, p, p, p, p, p, p, 256, dh, 0.125, 1, 0, 0, 1, None) == \
             _lib.STATUS_BAD_DIM, dh
-    for dh in (1, 50, 64, 96, 128):
-        assert f(p, p, p, p, p, 256, dh, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_UNSUPPORTED, dh
     # the sparse mask needs a stride, and a null operand is refused
-    assert f(p, p, p, p, None, 256, 96, 0.125, 1, 1, 8, 0, None) == _lib.STATUS_BAD_DIM
-    assert f(p, None, p, p, None, 256, 96, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_NULL_POINTER
+    assert f(p, p, p, p, p, 256, 96, 0.125, 1, 1, 8, 0, None) == _lib.STATUS_BAD_DIM
+    assert f(p, None, p, p, p, 256, 96, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_NULL_POINTER

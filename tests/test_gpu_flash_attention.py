@@ -153,7 +153,7 @@ def test_rejections():
         v.flash_attention_fwd(x, x, x)  # DH 129 (the reference throws above 128)
     y = torch.zeros((64, 64), device="cuda")
     with pytest.raises(ValueError):
-        v.flash_attention_fwd(y, y, y, attn=torch.zeros((64, 64), device="cuda"))
+        v.flash_attention_fwd(y, y, y, attn=torch.zeros((64, 63), device="cuda"))  # not [seq x seq]
     with pytest.raises(ValueError):
         v.flash_attention_fwd(y, y[:32], y)
 

@@ -483,3 +483,63 @@ def test_componentwise_ratio_definition():
     assert abs(r - (1e-3 - 2 * o.U32 * 2.0) / 8.0) < 1e-15
     assert o.componentwise_ratio(np.array([[1e-3]]), np.array([[0.0]]), np.array([[0.0]])) == float("inf")
     assert o.componentwise_ratio(np.array([[np.nan]]), np.array([[0.0]]), np.array([[1.0]])) == float("inf")
+
+
+# ------------------------------------------- attention probability copy (Aptr)
+
+def _probs_closed_form(Q, K, scale, mask, prior):
+    """float64 closed form of the reference's Aptr values: an allowed key of
+    32-key tile t gets exp(s - M_t) / l with M_t = max of the allowed scores
+    of tiles 0..t and l = sum over allowed keys of exp(s - M_row); a masked key
+    prior / l.  (Derived from the kernel's walk: m only grows, and the online
+    rescaling makes l the plain sum at the final maximum.)"""
+    S = scale * (np.asarray(Q, np.float64) @ np.asarray(K, np.float64).T)
+    seq = S.shape[0]
+    Sm = np.where(mask, S, -np.inf)
+    tile_max = np.stack([Sm[:, k0:k0 + 32].max(axis=1) for k0 in range(0, seq, 32)], axis=1)
+    run = np.maximum.accumulate(tile_max, axis=1)
+    Mt = np.repeat(run, 32, axis=1)[:, :seq]
+    Mrow = run[:, -1:]
+    l = np.where(mask, np.exp(S - Mrow), 0.0).sum(axis=1, keepdims=True)
+    inv = np.where(l > 1e-9, 1.0 / np.where(l > 0, l, 1.0), 0.0)
+    return np.where(mask, np.exp(S - Mt), prior) * inv
+
+
+@pytest.mark.parametrize("seq,causal,shunyam,window,stride", [
+    (20, 1, 0, 0, 1), (32, 0, 0, 0, 1), (31, 1, 1, 4, 5),   # one tile: plain softmax
+    (100, 1, 0, 0, 1), (100, 0, 0, 0, 1), (97, 1, 1, 8, 7), (130, 0, 1, 3, 10)])
+def test_flash_probs_restatement_against_closed_form(seq, causal, shunyam, window, stride):
+    rng = np.random.default_rng(seq + 3 * window)
+    Q = rng.standard_normal((seq, 16), dtype=np.float32)
+    K = rng.standard_normal((seq, 16), dtype=np.float32)
+    prior = rng.standard_normal((seq, seq), dtype=np.float32)
+    mask = o.attention_mask(seq, causal, shunyam, window, stride)
+    got = o.flash_attention_probs(Q, K, 0.5, causal, shunyam, window, stride, prior)
+    want = _probs_closed_form(Q, K, 0.5, mask, prior)
+    assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-3)) < 2e-5
+    if seq <= 32:  # a single tile: the allowed entries are the softmax probabilities
+        S = 0.5 * (Q.astype(np.float64) @ K.T.astype(np.float64))
+        P = np.where(mask, np.exp(S - np.where(mask, S, -np.inf).max(1, keepdims=True)), 0.0)
+        P /= P.sum(1, keepdims=True)
+        assert np.max(np.abs(np.where(mask, got, 0.0) - P)) < 1e-6
+
+
+def test_flash_probs_stale_maximum_is_kept():
+    """A row whose maximum sits in a later tile: the entries of the earlier
+    tiles exceed their softmax probability by exp(M_row - M_t) -- the
+    reference's values, which a plain softmax would miss -- while the tile
+    holding the maximum and later ones are the softmax."""
+    seq = 96
+    Q = np.zeros((seq, 2), np.float32)
+    K = np.zeros((seq, 2), np.float32)
+    Q[:, 0] = 1.0
+    K[:, 0] = 0.0
+    K[70, 0] = 3.0  # the row maximum: key 70, tile 2
+    got = o.flash_attention_probs(Q, K, 1.0, causal=False)
+    S = np.zeros(seq)
+    S[70] = 3.0
+    soft = np.exp(S - 3.0) / np.exp(S - 3.0).sum()
+    row = got[80].astype(np.float64)
+    assert np.allclose(row[64:], soft[64:], rtol=1e-5)
+    assert np.allclose(row[:64], soft[:64] * np.exp(3.0), rtol=1e-5)
+    assert not np.allclose(row[:64], soft[:64], rtol=1e-2)
