@@ -42,10 +42,14 @@ constexpr int kSkStage = 8192;   // bytes per stage per wave: 4 KiB of A + 4 KiB
 
 // fp16 operands, 64-deep stages.  Direct loads without branches: each lane
 // keeps its byte offset and the first contraction index of its chunk, and an
-// out-of-range chunk takes the out-of-range offset.
+// out-of-range chunk takes the out-of-range offset.  NA: A-side load
+// instructions per stage, each 8 rows of A: only the first NA = ceil(M / 8)
+// are issued (the LDS rows of the others are never written; the MFMA rows
+// they feed are output rows past M, which are not stored).
+template <int NA>
 struct SkinnyF16 {
     static constexpr int BK = 64;
-    static constexpr int L = 8;  // direct-load instructions per stage per wave
+    static constexpr int L = NA + 4;  // direct-load instructions per stage per wave
     static constexpr bool kUniformRounds = false;
     using T = _Float16;
     uint32_t aoff[4], boff[4];
@@ -71,7 +75,7 @@ struct SkinnyF16 {
         const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(static_cast<const T*>(a.A) + k0);
         const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(static_cast<const T*>(a.B) + (int64_t)k0 * a.ldb);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NA; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(dst + i * 1024), 16,
                                                      ak[i] + 8 <= krem ? aoff[i] : kOob, 0, 0, 0);
 #pragma unroll
@@ -89,10 +93,11 @@ struct SkinnyF16 {
     }
 };
 
-// fp32 operands, 32-deep stages.
+// fp32 operands, 32-deep stages; NA as for fp16.
+template <int NA>
 struct SkinnyF32 {
     static constexpr int BK = 32;
-    static constexpr int L = 8;
+    static constexpr int L = NA + 4;
     static constexpr bool kUniformRounds = true;
     using T = float;
     // Instruction i of a side fills bytes [1024 i, 1024 (i + 1)) of the
@@ -117,7 +122,7 @@ struct SkinnyF32 {
         const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(static_cast<const T*>(a.A) + k0);
         const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(static_cast<const T*>(a.B) + (int64_t)k0 * a.ldb);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NA; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(dst + i * 1024), 16,
                                                      ak[i] + 4 <= krem ? aoff[i] : kOob, 0, 0, 0);
 #pragma unroll
@@ -222,12 +227,17 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs a) {
     epilogue<KIND, true, 1, 1>(a, a.C, sum, 0, n0, lane);
 }
 
-template __global__ void gemm_skinny_kernel<SkinnyF16, EK_PLAIN>(GemmArgs);
-template __global__ void gemm_skinny_kernel<SkinnyF16, EK_BIAS>(GemmArgs);
-template __global__ void gemm_skinny_kernel<SkinnyF16, EK_GENERIC>(GemmArgs);
-template __global__ void gemm_skinny_kernel<SkinnyF32, EK_PLAIN>(GemmArgs);
-template __global__ void gemm_skinny_kernel<SkinnyF32, EK_BIAS>(GemmArgs);
-template __global__ void gemm_skinny_kernel<SkinnyF32, EK_GENERIC>(GemmArgs);
+#define VEDIC_SKINNY_KERNELS(Sk)                                \
+    template __global__ void gemm_skinny_kernel<Sk, EK_PLAIN>(GemmArgs); \
+    template __global__ void gemm_skinny_kernel<Sk, EK_BIAS>(GemmArgs);  \
+    template __global__ void gemm_skinny_kernel<Sk, EK_GENERIC>(GemmArgs)
+VEDIC_SKINNY_KERNELS(SkinnyF16<1>);
+VEDIC_SKINNY_KERNELS(SkinnyF16<2>);
+VEDIC_SKINNY_KERNELS(SkinnyF16<4>);
+VEDIC_SKINNY_KERNELS(SkinnyF32<1>);
+VEDIC_SKINNY_KERNELS(SkinnyF32<2>);
+VEDIC_SKINNY_KERNELS(SkinnyF32<4>);
+#undef VEDIC_SKINNY_KERNELS
 
 template <class Sk>
 static hipError_t launch_skinny(const GemmArgs& a, hipStream_t s) {
@@ -243,10 +253,18 @@ static hipError_t launch_skinny(const GemmArgs& a, hipStream_t s) {
 
 // fp16: A, B 16-byte aligned, lda / ldb multiples of 8 and < 2^22, N a
 // multiple of 8 (checked by the caller); M <= 32, op NN.
-hipError_t launch_gemm_f16_skinny(const GemmArgs& a, hipStream_t s) { return launch_skinny<SkinnyF16>(a, s); }
+hipError_t launch_gemm_f16_skinny(const GemmArgs& a, hipStream_t s) {
+    if (a.M <= 8) return launch_skinny<SkinnyF16<1>>(a, s);
+    if (a.M <= 16) return launch_skinny<SkinnyF16<2>>(a, s);
+    return launch_skinny<SkinnyF16<4>>(a, s);
+}
 
 // fp32: A, B 16-byte aligned, lda / ldb multiples of 4 and < 2^22, N a
 // multiple of 4 (checked by the caller); M <= 32, op NN.
-hipError_t launch_gemm_f32_skinny(const GemmArgs& a, hipStream_t s) { return launch_skinny<SkinnyF32>(a, s); }
+hipError_t launch_gemm_f32_skinny(const GemmArgs& a, hipStream_t s) {
+    if (a.M <= 8) return launch_skinny<SkinnyF32<1>>(a, s);
+    if (a.M <= 16) return launch_skinny<SkinnyF32<2>>(a, s);
+    return launch_skinny<SkinnyF32<4>>(a, s);
+}
 
 }  // namespace vedic
