@@ -420,7 +420,6 @@ __global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f16_kernel(GemmArgs 
     // PPB of them share one stage buffer
     constexpr int PBYTES = WM * WN * 4, PPB = PBYTES <= SBYTES ? SBYTES / PBYTES : 1;
     static_assert(WGK == 1 || (PBYTES <= SBYTES && (WGK - 1) * WMN <= ST * PPB), "the partials fit the stage buffers");
-    static_assert(WGK == 1 || !A32, "no contraction split with an fp32 A");
     const _Float16* __restrict__ A = static_cast<const _Float16*>(args.A);
     const float* __restrict__ A32f = static_cast<const float*>(args.A);
     const _Float16* __restrict__ B = static_cast<const _Float16*>(args.B);
@@ -487,7 +486,9 @@ __global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f16_kernel(GemmArgs 
                     // register loads, then the MFMAs, then the conversion into
                     // stage kt - 1's buffer, free since the barrier above
                     VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
-                    if (kt < nk) mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI>(As[s], Bs[s], wm * WM, wn * WN, lane, acc);
+                    if (kt < nk)
+                        mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI, 0, 1, KN>(As[s], Bs[s], wm * WM, wn * WN, lane, acc,
+                                                                            wk * KN);
                     wait_vmcnt<SB::NLD>();
                     sa.commit(As[sl], wave, lane);
                 } else if constexpr (kInterleave) {
@@ -643,8 +644,14 @@ struct CfgSmall {  // 128 x 128, four waves of 64 x 64, two workgroups per CU (2
 // CfgSmall on the TN dW products (4096 x 1024 x 8192, 1024 x 3072 x 8192,
 // 1024 x 4096 x 8192); 128 x 64 waves in a single group of four measured no
 // faster than CfgSmall.
+#ifndef VEDIC_F16_SMALLK_BK
+#define VEDIC_F16_SMALLK_BK 64
+#endif
+#ifndef VEDIC_F16_SMALLK_ST
+#define VEDIC_F16_SMALLK_ST 3
+#endif
 struct CfgSmallK {
-    static constexpr int BM = 128, BN = 128, BK = 64, ST = 3, WGM = VEDIC_F16_SMALLK_WGM, WGN = 2,
+    static constexpr int BM = 128, BN = 128, BK = VEDIC_F16_SMALLK_BK, ST = VEDIC_F16_SMALLK_ST, WGM = VEDIC_F16_SMALLK_WGM, WGN = 2,
                          WGK = VEDIC_F16_SMALLK_WGK;
     static constexpr int PER_CU = 1;
 };
@@ -667,8 +674,16 @@ struct CfgMid {  // 256 x 128, eight waves of 64 x 64
 #ifndef VEDIC_F16_NARROW_ST
 #define VEDIC_F16_NARROW_ST 4
 #endif
+#ifndef VEDIC_F16_NARROW_WGK
+#define VEDIC_F16_NARROW_WGK 4
+#endif
+// 64 x 32, two 32 x 32 waves per k group, four groups each taking two of a
+// stage's eight k steps (eight waves): an 8192 x 64 x 1024 product 6.97 ->
+// 6.05 us against one group of two waves (more loads in flight per CU);
+// two groups 6.29, eight groups over 256-deep stages 7.3-7.7.
 struct CfgNarrow {
-    static constexpr int BM = 64, BN = 32, BK = VEDIC_F16_NARROW_BK, ST = VEDIC_F16_NARROW_ST, WGM = 2, WGN = 1, WGK = 1;
+    static constexpr int BM = 64, BN = 32, BK = VEDIC_F16_NARROW_BK, ST = VEDIC_F16_NARROW_ST, WGM = 2, WGN = 1,
+                         WGK = VEDIC_F16_NARROW_WGK;
     static constexpr int PER_CU = 1;
 };
 struct CfgNarrowT {
