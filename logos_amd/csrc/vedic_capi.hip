@@ -198,14 +198,13 @@ __global__ void splitk_reduce4_kernel(const float* __restrict__ ws, int S, GemmA
         if (epi & EPI_ALPHA) v *= a.alpha;
         if (epi & EPI_BETA) v += a.beta * *cp;
         if (epi & EPI_BIAS) v += *reinterpret_cast<const float4_t*>(a.bias + j);
-        float4_t* pp = reinterpret_cast<float4_t*>(a.preact + (int64_t)i * a.ldp + j);
-        if (epi & EPI_PREACT) *pp = v;
+        if (epi & EPI_PREACT) *reinterpret_cast<float4_t*>(a.preact + (int64_t)i * a.ldp + j) = v;
         if (epi & EPI_GELU) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
         }
         if (epi & EPI_GELU_BWD) {
-            const float4_t pv = *pp;
+            const float4_t pv = *reinterpret_cast<const float4_t*>(a.preact + (int64_t)i * a.ldp + j);
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] *= gelu_tanh_grad(pv[e]);
         }
