@@ -8,6 +8,13 @@ RapidCheck is not available offline (it is fetched at configure time,
 CMakeLists.txt:241-247), so the property tests draw their cases from a seeded
 numpy generator with the reference's ranges instead of RapidCheck's.
 
+  M1   tests/test_math_unit.cpp:217-257    shapes 4^3 .. 128x256x128, U(-1, 1); max error
+                                           < 1e-2, C[0,0] and C[M-1,N-1] within 1e-3
+  M9   tests/test_math_unit.cpp:943-1004   non-divisible shapes, U(-0.5, 0.5); max error < 1e-2,
+                                           C[0,0], C[M-1,N-1] and C[mid] within 1e-3; a 64^3
+                                           product (U(-0.1, 0.1)) with a finite sum
+  S6   tests/test_syntax_build.cu:196-260  3 x 5 x 7 from (i % 5) - 2 and (i % 7) - 3, and with
+                                           the bias 0.25 col; within 1e-4 (exact here)
   RC1  tests/test_rapidcheck.cpp:85-114   M, K, N in [1, 32], values k * 0.01,
                                            k in [-100, 100]; mat_close atol 2e-4, rtol 1e-4
   RC2  tests/test_rapidcheck.cpp:125-170  square sizes around VEDIC_BLOCK = 64,
@@ -61,6 +68,59 @@ def mat_close(got, want, atol, rtol):
 def grid_values(rng, shape, lo, hi, step):
     """Values k * step for k uniform in [lo, hi] (RapidCheck's inRange(lo, hi + 1) mapped)."""
     return (rng.integers(lo, hi + 1, size=shape).astype(np.float32) * np.float32(step)).astype(np.float32)
+
+
+@pytest.mark.parametrize("M,K,N", [(4, 4, 4), (8, 16, 8), (32, 64, 32), (64, 128, 64), (128, 256, 128)])
+def test_m1_random_shapes(M, K, N):
+    vedic = V()
+    rng = np.random.default_rng(42)
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    got = host(vedic.vedic_gemm(dev(A), dev(B)))
+    naive = o.reference_gemm(A, B)
+    assert got.shape == (M, N)
+    assert np.abs(got - naive).max() < 1e-2
+    assert abs(got[0, 0] - naive[0, 0]) < 1e-3 and abs(got[-1, -1] - naive[-1, -1]) < 1e-3
+    check(got, o.NN, A, B, tol=fp32_tol(K), label=f"M1 {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("M,K,N", [(3, 5, 7), (17, 33, 19), (31, 63, 15), (100, 200, 150)])
+def test_m9_non_divisible_shapes(M, K, N):
+    vedic = V()
+    rng = np.random.default_rng(77)
+    A = rng.uniform(-0.5, 0.5, (M, K)).astype(np.float32)
+    B = rng.uniform(-0.5, 0.5, (K, N)).astype(np.float32)
+    got = host(vedic.vedic_gemm(dev(A), dev(B)))
+    naive = o.reference_gemm(A, B)
+    assert got.shape == (M, N)
+    assert np.abs(got - naive).max() < 1e-2
+    for i, j in ((0, 0), (M - 1, N - 1), (M // 2, N // 2)):
+        assert abs(got[i, j] - naive[i, j]) < 1e-3, (i, j)
+    check(got, o.NN, A, B, tol=fp32_tol(K), label=f"M9 {M}x{K}x{N}")
+
+
+def test_m9_exact_block_shape():
+    vedic = V()
+    rng = np.random.default_rng(11)
+    A = rng.uniform(-0.1, 0.1, (64, 64)).astype(np.float32)
+    B = rng.uniform(-0.1, 0.1, (64, 64)).astype(np.float32)
+    got = host(vedic.vedic_gemm(dev(A), dev(B)))
+    assert got.shape == (64, 64) and np.isfinite(got.sum())
+    check(got, o.NN, A, B, tol=fp32_tol(64), label="M9 64^3")
+
+
+def test_s6_irregular_shape_and_bias():
+    vedic = V()
+    A = ((np.arange(15) % 5) - 2).astype(np.float32).reshape(3, 5)
+    B = ((np.arange(35) % 7) - 3).astype(np.float32).reshape(5, 7)
+    b = np.float32(0.25) * np.arange(7, dtype=np.float32)
+    exact = A.astype(np.float64) @ B.astype(np.float64)
+    got = host(vedic.vedic_gemm(dev(A), dev(B)))
+    assert np.abs(got - exact).max() < 1e-4
+    assert np.array_equal(got, exact.astype(np.float32))  # small integers: every sum exact
+    got = host(vedic.vedic_gemm_bias(dev(A), dev(B), dev(b)))
+    assert np.abs(got - (exact + b)).max() < 1e-4
+    assert np.array_equal(got, (exact + b).astype(np.float32))
 
 
 def test_rc1_vedic_gemm_matches_the_naive_loop():
