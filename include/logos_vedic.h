@@ -143,9 +143,9 @@ int vedic_gemm_noalloc(const vedic_gemm_desc_t* desc);
 /* Size of the region vedic_gemm_noalloc draws from (per GPU). */
 size_t vedic_noalloc_scratch_bytes(void);
 
-/* Frees the workspace block kept for `stream` on the current device (in
- * stream order, after the work queued on it); the next call on the stream
- * allocates a new one.  Call it before destroying a stream the library has
+/* Frees the workspace block kept for `stream` on the current device, and the
+ * attention work-queue counter kept with it (in stream order, after the work
+ * queued on them); the next call on the stream allocates new ones.  Call it before destroying a stream the library has
  * used: blocks are keyed by the stream handle, and a stream created later
  * with the same handle would otherwise inherit the block while work of the
  * destroyed stream may still be using it.  New: the reference allocates per

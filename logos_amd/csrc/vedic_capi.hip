@@ -94,6 +94,44 @@ static StreamArena* arena_of(hipStream_t s) {
     return a;
 }
 
+// The attention kernels' work-queue counter of a (device, stream): an int in
+// a block of its own (no other temporary of a call can overwrite it), set to
+// zero by a kernel when the block is allocated and put back to zero by the
+// merge kernel that ends every launch that uses it, so a call needs no reset
+// launch of its own.  Freed by vedic_workspace_release.
+static std::mutex g_fq_mu;
+static std::map<std::pair<int, hipStream_t>, int*> g_flash_queues;
+
+static int* flash_queue_of(hipStream_t s, hipError_t& e) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lk(g_fq_mu);
+    int*& q = g_flash_queues[std::make_pair(dev, s)];
+    e = hipSuccess;
+    if (!q) {
+        int* p = nullptr;
+        e = hipMallocAsync(reinterpret_cast<void**>(&p), 256, s);
+        if (e == hipSuccess) e = launch_flash_queue_reset(p, s);
+        if (e != hipSuccess) {
+            if (p) (void)hipFreeAsync(p, s);
+            return nullptr;
+        }
+        q = p;
+    }
+    return q;
+}
+
+static hipError_t flash_queue_release(hipStream_t s) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lk(g_fq_mu);
+    auto it = g_flash_queues.find(std::make_pair(dev, s));
+    if (it == g_flash_queues.end()) return hipSuccess;
+    const hipError_t e = hipFreeAsync(it->second, s);
+    g_flash_queues.erase(it);
+    return e;
+}
+
 // One call's temporaries: pieces carved in order from the stream's arena (a
 // piece that does not fit comes from the stream-ordered pool, and the arena
 // grows to fit the whole call at the next call's first request).  Bound to a
@@ -770,7 +808,8 @@ extern "C" int vedic_workspace_release(void* stream) {
     a->base = nullptr;
     a->cap = 0;
     a->want = 0;
-    return hip_status(e);
+    const hipError_t f = flash_queue_release(s);
+    return hip_status(e != hipSuccess ? e : f);
 }
 
 extern "C" void vedic_debug_set_workspace_guard(int on) { g_ws_guard.store(on ? 1 : 0); }
@@ -1689,17 +1728,24 @@ static int flash_launch(FlashArgs& a, int dh, Workspace& wsf) {
     hipStream_t s = wsf.s;
     const int full = a.nqg * kFaQ;
     if (a.chunk >= full) return hip_status(launch_flash_attn(a, dh, s));
-    // Workspace: the chunk partials, then the work-item counter.  The split
-    // items go to a grid of resident workgroups (LDS allows three per CU at
-    // DH 64, one at DH 128) that take them largest first.
+    // Workspace: the chunk partials.  The split items go to a grid of
+    // resident workgroups (LDS allows three per CU at DH 64, one at DH 128)
+    // that take them largest first from the stream's work-queue counter.
     const size_t bytes = sizeof(float) * (size_t)flash_slot_floats(dh) * (size_t)a.items * a.nheads;
     char* ws = nullptr;
-    hipError_t e = wsf.get(&ws, bytes + 256);
+    hipError_t e = wsf.get(&ws, bytes);
     if (e != hipSuccess) return hip_status(e);
     a.part = reinterpret_cast<float*>(ws);
-    a.queue = reinterpret_cast<int*>(ws + bytes);
+    a.queue = flash_queue_of(s, e);
+    if (e != hipSuccess) {
+        (void)wsf.put(ws);
+        return hip_status(e);
+    }
     a.queue_grid = (dh == 64 ? 3 : 1) * device_cu_count();
     e = launch_flash_attn(a, dh, s);
+    // a launch that failed may leave the counter off zero: the next call
+    // allocates and clears a new one
+    if (e != hipSuccess) (void)flash_queue_release(s);
     const hipError_t f = wsf.put(ws);
     return hip_status(e != hipSuccess ? e : f);
 }

@@ -264,13 +264,21 @@ __global__ void flash_queue_reset(int* queue) {
     if (threadIdx.x == 0) *queue = 0;
 }
 
+hipError_t launch_flash_queue_reset(int* queue, hipStream_t s) {
+    hipLaunchKernelGGL(flash_queue_reset, dim3(1), dim3(64), 0, s, queue);
+    return hipGetLastError();
+}
+
 // Combines the chunk partials of every split query group, chunks in
 // ascending order: M = max m_c, L = sum l_c 2^(m_c - M), O = sum O_c 2^(m_c - M) / L
 // (row maxima in base 2, as the attention kernel keeps them).
+// It also returns the work-queue counter to zero for the next queued launch
+// on the stream (the attention kernel before it in stream order is done).
 template <int DH>
 __global__ void __launch_bounds__(256) flash_merge_kernel(FlashArgs a) {
     // one thread per 4 output values; grid (kFaQ DH / 1024, query groups, heads)
     const int g = blockIdx.y, head = blockIdx.z;
+    if (a.queue != nullptr && blockIdx.x == 0 && g == 0 && head == 0 && threadIdx.x == 0) *a.queue = 0;
     const int nch = fa_nchunks(a, g);
     if (nch == 1) return;
     const int idx = blockIdx.x * 256 + threadIdx.x;  // < kFaQ * DH / 4
@@ -310,10 +318,9 @@ int flash_slot_floats(int dh) { return kFaQ * dh + 2 * kFaQ; }
 
 hipError_t launch_flash_attn(const FlashArgs& a, int dh, hipStream_t s) {
     dim3 grid((unsigned)(a.items * a.nheads));
-    if (a.queue != nullptr) {
-        hipLaunchKernelGGL(flash_queue_reset, dim3(1), dim3(64), 0, s, a.queue);
-        grid = dim3((unsigned)std::min(a.items * a.nheads, a.queue_grid));
-    }
+    // (a.queue is zero here: set so when its block was made, and put back by
+    // the merge kernel that ends every queued launch)
+    if (a.queue != nullptr) grid = dim3((unsigned)std::min(a.items * a.nheads, a.queue_grid));
     const bool q = a.queue != nullptr;
     if (dh == 64) {
         if (q) hipLaunchKernelGGL((flash_attn_kernel<64, true>), grid, dim3(256), 0, s, a);

@@ -21,7 +21,8 @@ struct FlashArgs {
     float* o[kMaxHeads];
     float* lse[kMaxHeads];  // optional per head: ln of the softmax denominator of each query row
     float* part;  // chunk partials: [heads][items][kFaQ * DH + 2 * kFaQ]; null when unsplit
-    int* queue;   // work-item counter (persistent grid of queue_grid workgroups); null: one item per workgroup
+    int* queue;   // work-item counter (persistent grid of queue_grid workgroups), zero at launch and put
+                  // back to zero by the merge kernel; null: one item per workgroup
     int queue_grid;
     int nheads, seq, nqg;
     int chunk;  // keys per work item, a multiple of kFaQ
@@ -56,6 +57,8 @@ __device__ __forceinline__ float fa_lse(float m2, float l) {
 int64_t flash_items_per_head(int seq, int chunk, int causal);
 int flash_slot_floats(int dh);
 hipError_t launch_flash_attn(const FlashArgs& a, int dh, hipStream_t s);
+// Sets a work-queue counter to zero (once, when its memory is allocated).
+hipError_t launch_flash_queue_reset(int* queue, hipStream_t s);
 // The reference's optional probability copy attn[seq x seq] of head 0 of `a`
 // (Q rows of dh values, any dh <= 128; vedic_flash_probs.hip).
 hipError_t launch_flash_probs(const FlashArgs& a, int dh, float* attn, hipStream_t s);

@@ -168,3 +168,34 @@ def test_checked_gemm_with_work_queued_ahead_and_threads():
         th.join()
     torch.cuda.synchronize()
     assert not errors
+
+
+def test_attention_queue_counter_between_calls():
+    """The one-head attention forward takes its split key ranges from a
+    work-queue counter kept per (device, stream) and put back to zero by the
+    merge kernel: calls interleaved with split-K GEMMs (which reuse the
+    workspace block), on a second stream, and after vedic_workspace_release
+    (which frees the counter) all give the first call's bits."""
+    vedic = V()
+    lib = _lib.load()
+    rng = np.random.default_rng(4)
+    seq, dh = 4096, 64
+    Q, K, Vv = (dev(normal(rng, (seq, dh))) for _ in range(3))
+    ref = vedic.flash_attention_fwd(Q, K, Vv)
+    split = split_case(rng, 1024, 1024, 8192)
+    r_split = run_split(vedic, *split)
+    torch.cuda.synchronize()
+    got, splits = [], []
+    for s in (torch.cuda.current_stream(), torch.cuda.Stream()):
+        with torch.cuda.stream(s):
+            for rep in range(3):
+                got.append(vedic.flash_attention_fwd(Q, K, Vv))
+                splits.append(run_split(vedic, *split))
+                got.append(vedic.flash_attention_fwd(Q, K, Vv))
+            assert lib.vedic_workspace_release(s.cuda_stream) == 0
+            got.append(vedic.flash_attention_fwd(Q, K, Vv))
+    torch.cuda.synchronize()
+    for g in got:
+        assert torch.equal(g, ref)
+    for g in splits:
+        assert torch.equal(g, r_split)
