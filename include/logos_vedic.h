@@ -145,11 +145,11 @@ size_t vedic_noalloc_scratch_bytes(void);
 
 /* Frees the workspace block kept for `stream` on the current device, and the
  * attention work-queue counter kept with it (in stream order, after the work
- * queued on them); the next call on the stream allocates new ones.  Call it before destroying a stream the library has
- * used: blocks are keyed by the stream handle, and a stream created later
- * with the same handle would otherwise inherit the block while work of the
- * destroyed stream may still be using it.  New: the reference allocates per
- * call and keeps nothing. */
+ * queued on them); the next call on the stream allocates new ones.  Call it
+ * before destroying a stream the library has used: blocks are keyed by the
+ * stream handle, and a stream created later with the same handle would
+ * otherwise inherit the block while work of the destroyed stream may still be
+ * using it.  New: the reference allocates per call and keeps nothing. */
 int vedic_workspace_release(void* stream);
 
 /* ---- reference-compatible entry points ------------------------------- */
