@@ -270,8 +270,10 @@ hipError_t launch_flash_queue_reset(int* queue, hipStream_t s) {
 }
 
 // Combines the chunk partials of every split query group, chunks in
-// ascending order: M = max m_c, L = sum l_c 2^(m_c - M), O = sum O_c 2^(m_c - M) / L
-// (row maxima in base 2, as the attention kernel keeps them).
+// ascending order with a running maximum M: per chunk c, M' = max(M, m_c),
+// L = L 2^(M - M') + l_c 2^(m_c - M'), O likewise; then O / L (row maxima in
+// base 2, as the attention kernel keeps them).  The order is fixed, so the
+// result does not depend on timing.
 // It also returns the work-queue counter to zero for the next queued launch
 // on the stream (the attention kernel before it in stream order is done).
 template <int DH>
@@ -287,18 +289,20 @@ __global__ void __launch_bounds__(256) flash_merge_kernel(FlashArgs a) {
     if (query >= a.seq) return;
     constexpr int SLOT = kFaQ * DH + 2 * kFaQ;
     const float* base = a.part + ((int64_t)head * a.items + fa_prefix(a, g)) * SLOT;
-    float M = kFaMasked;
-    // loads of different chunks are independent: unrolled so they are in flight together
-#pragma unroll 8
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, base[(int64_t)c * SLOT + kFaQ * DH + qi]);
-    float L = 0.0f;
+    float M = kFaMasked, L = 0.0f;
     float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    // one pass with a running maximum: the chunks' loads are independent and
+    // unrolled so they are in flight together; the rescaling is a short chain
 #pragma unroll 8
     for (int c = 0; c < nch; ++c) {
         const float* sl = base + (int64_t)c * SLOT;
-        const float w = __builtin_amdgcn_exp2f(sl[kFaQ * DH + qi] - M);
-        L += sl[kFaQ * DH + kFaQ + qi] * w;
-        acc += *reinterpret_cast<const float4_t*>(sl + qi * DH + 4 * d4) * w;
+        const float mc = sl[kFaQ * DH + qi], lc = sl[kFaQ * DH + kFaQ + qi];
+        const float4_t oc = *reinterpret_cast<const float4_t*>(sl + qi * DH + 4 * d4);
+        const float Mn = fmaxf(M, mc);
+        const float so = __builtin_amdgcn_exp2f(M - Mn), w = __builtin_amdgcn_exp2f(mc - Mn);
+        L = L * so + lc * w;
+        acc = acc * so + oc * w;
+        M = Mn;
     }
     const float inv = L > 1e-9f ? 1.0f / L : 0.0f;
     *reinterpret_cast<float4_t*>(a.o[head] + (int64_t)query * DH + 4 * d4) = acc * inv;
