@@ -289,7 +289,7 @@ __global__ void colsum_partial_kernel(const float* __restrict__ X, int64_t ldx, 
     const int i0 = blockIdx.y * rows_per_block;
     const int i1 = min(M, i0 + rows_per_block);
     float acc = 0.0f;
-#pragma unroll 4
+#pragma unroll 16
     for (int i = i0; i < i1; ++i) acc += X[(int64_t)i * ldx + j];
     part[(int64_t)blockIdx.y * N + j] = acc;
 }
@@ -309,7 +309,9 @@ __device__ __forceinline__ void colsum_reduce_block(const float* __restrict__ pa
     const int b0 = min(nblocks, g * q), b1 = min(nblocks, b0 + q);
     float acc = 0.0f;
     if (j < N) {
-#pragma unroll 4
+        // (unrolled so a thread's loads are in flight together; the additions
+        // stay in ascending b)
+#pragma unroll 16
         for (int b = b0; b < b1; ++b) acc += part[(int64_t)b * N + j];
     }
     sh[g][c] = acc;
