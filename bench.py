@@ -71,7 +71,9 @@ WORKLOADS = {
     "ffn_bwd_dh_gelu_nt_fp16": dict(cfg=3, gemms=[_g(8192, 1024, 4096, op="NT", epi="gelu_bwd")]),
     # the Q/K/V projection of one layer: the reference's 48 per-head GEMMs
     # (cuda/ModelGPU.cu:894-906) against one packed GEMM scattered into the same 48 head buffers
-    "qkv_per_head_fp16": dict(cfg=5, gemms=[_g(8192, 1024, 64) for _ in range(48)]),
+    # the reference's per-head projections (cuda/ModelGPU.cu:900-906): 48 calls on
+    # the same activation X with each head's own [1024 x 64] weight
+    "qkv_per_head_fp16": dict(cfg=5, share_a=True, gemms=[_g(8192, 1024, 64) for _ in range(48)]),
     "qkv_packed_scatter_fp16": dict(cfg=5, gemms=[_g(8192, 1024, 3072, heads=48)]),
     # one attention head's GEMMs at seq = 8192, DH = 64, strict fp32 as in the reference
     # (cuda/train_gpu.cu:422-479, 672-692): scores = Q K^T / sqrt(DH) (NT, alpha),
@@ -433,6 +435,7 @@ def make_step(w: dict, dev, torch):
     stream = torch.cuda.current_stream()
     keep = []
     items = []
+    shared_a = None  # share_a: every GEMM reads the first one's A (one activation, several weights)
     for g in w["gemms"]:
         M, K, N, op = g["M"], g["K"], g["N"], g["op"]
         a_shape = (K, M) if op == "TN" else (M, K)
@@ -447,6 +450,12 @@ def make_step(w: dict, dev, torch):
             A, B = A.half(), B.half()
         elif g["dtype"] == "amp":
             B = B.half()
+        a_again = False
+        if w.get("share_a"):
+            if shared_a is None:
+                shared_a = A
+            else:
+                A, a_again = shared_a, True
         g["_cast"] = (A32, A) if A32 is not None else None
         keep.append(A32)
         C = torch.randn((M, N), generator=gen, device=dev) * 1e-3 if g["beta"] else torch.empty((M, N), device=dev)
@@ -468,7 +477,8 @@ def make_step(w: dict, dev, torch):
             colsum=db.data_ptr() if gbwd else None, colsum_beta=1.0)
         es = 2 if g["dtype"] == "fp16" else 4
         es_b = 4 if g["dtype"] == "fp32" else 2
-        hbm = M * K * es + K * N * es_b + M * N * 4 * (2 if g["beta"] else 1) + (N * 4 if g["epi"] != "none" else 0)
+        hbm = (0 if a_again else M * K * es) + K * N * es_b + M * N * 4 * (2 if g["beta"] else 1) + \
+            (N * 4 if g["epi"] != "none" else 0)
         if g["cast_a"]:
             hbm += M * K * 6  # the cast pass: fp32 read, binary16 written
         if gbwd:
