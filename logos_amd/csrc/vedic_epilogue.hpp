@@ -25,7 +25,7 @@ enum EpiKind : int {
     EK_ACCUM = 4,          // C = C + acc           (beta = 1, the dW accumulation)
     EK_GENERIC = 5,        // any flag combination (runtime flags)
     EK_GELU_BWD = 6,       // C = acc * gelu'(P)    (+ column sums if cs_part)
-    EK_LINEAR_CS = 7,      // C = alpha acc (+ b), with column sums
+    EK_LINEAR_CS = 7,      // C = alpha acc (+ b), with column sums if cs_part
 };
 
 __host__ __device__ inline int epi_kind_of(int epi, float alpha, float beta) {
@@ -33,6 +33,9 @@ __host__ __device__ inline int epi_kind_of(int epi, float alpha, float beta) {
     if ((epi & EPI_COLSUM) && (epi & ~(EPI_COLSUM | EPI_ALPHA | EPI_BIAS)) == 0) return EK_LINEAR_CS;
     if (epi & EPI_COLSUM) return EK_GENERIC;
     if (epi == 0) return EK_PLAIN;
+    // C = alpha acc alone: the linear kind with no bias and no column sums
+    // (fma(acc, alpha, 0) is the rounded product, the generic kind's result)
+    if (epi == EPI_ALPHA) return EK_LINEAR_CS;
     if (epi == EPI_BIAS) return EK_BIAS;
     if (epi == (EPI_BIAS | EPI_GELU)) return EK_BIAS_GELU;
     if (epi == (EPI_BIAS | EPI_GELU | EPI_PREACT)) return EK_BIAS_GELU_PRE;

@@ -162,6 +162,34 @@ def test_epilogues_alpha_beta_preact(dtype, opname):
         check(got, layout, A, B, tol=tol, alpha=0.5, beta=1.0, C0=C0, label="alpha/beta")
 
 
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("opname", list(OPS))
+def test_alpha_alone_is_the_rounded_product(dtype, opname):
+    """C = alpha op(A) op(B) with no other epilogue term is the fp32 product C
+    of the same call with alpha = 1, multiplied by alpha and rounded once --
+    on every path: the 256 x 256, 128 x 128 and narrow tiles, the skinny
+    kernel, split K (alpha applied after the slices are added) and the
+    element-wise kernel for unaligned operands."""
+    vedic = V()
+    layout = OPS[opname]
+    rng = np.random.default_rng(1234)
+    alpha = np.float32(0.3)
+    shapes = [(8192, 256, 64), (300, 264, 520), (1000, 40, 200), (16, 1024, 512), (256, 256, 4096),
+              (77, 141, 96), (513, 257, 130)]
+    for (M, N, K) in shapes:
+        if layout != o.NN and M <= 32:
+            continue  # the skinny kernel is NN only
+        A, B = _operands(rng, layout, M, N, K)
+        if dtype == "f16":
+            a, _ = dev_f16(A)
+            b, _ = dev_f16(B)
+        else:
+            a, b = dev(A), dev(B)
+        plain = host(vedic.gemm(layout, a, b))
+        scaled = host(vedic.gemm(layout, a, b, alpha=float(alpha)))
+        assert np.array_equal(scaled, plain * alpha), f"{opname} {dtype} {M}x{N}x{K}"
+
+
 def test_leading_dimensions_and_unaligned_views():
     vedic = V()
     rng = np.random.default_rng(5)
