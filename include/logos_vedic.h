@@ -28,9 +28,10 @@
  * Memory: the caller allocates every output.  A product whose output has too
  * few tiles to fill the GPU and whose contraction is long (fp16: fewer than
  * 128 tiles of 128 x 128 and K >= 2048; fp32: K >= 256) runs split over K and
- * takes an fp32 workspace of S * M * N * 4 bytes (S <= 8).  Workspaces (this,
- * column partials, the AMP cast buffer, attention partials and padded
- * copies) come from a block of device memory kept per (device, stream):
+ * takes an fp32 workspace of S * M * N * 4 bytes (S <= 8; S <= 16 for fp32
+ * products with N <= 64).  Workspaces (this, column partials, the AMP cast
+ * buffer, attention partials and padded copies) come from a block of device
+ * memory kept per (device, stream):
  * grown with hipMallocAsync on `stream` when a call needs more than it holds,
  * reused by every later call on that stream (their work runs in stream
  * order), and held until the process ends or vedic_workspace_release(stream).
