@@ -75,6 +75,10 @@ WORKLOADS = {
     # the same activation X with each head's own [1024 x 64] weight
     "qkv_per_head_fp16": dict(cfg=5, share_a=True, gemms=[_g(8192, 1024, 64) for _ in range(48)]),
     "qkv_packed_scatter_fp16": dict(cfg=5, gemms=[_g(8192, 1024, 3072, heads=48)]),
+    # the FFN-down with its bias and the residual add in the epilogue: the
+    # reference's amp_gemm_bias into a temporary, then residual_add_kernel
+    # (cuda/ModelGPU.cu:1044-1048); C holds the residual stream X
+    "ffn_down_bias_residual_fp16": dict(cfg=5, gemms=[_g(8192, 4096, 1024, epi="bias_residual")]),
     # one attention head's GEMMs at seq = 8192, DH = 64, strict fp32 as in the reference
     # (cuda/train_gpu.cu:422-479, 672-692): scores = Q K^T / sqrt(DH) (NT, alpha),
     # out = P V (NN), dP = dO V^T (NT), dV += P^T dO (TN, beta = 1), dQ = dS K (NN), dK = dS^T Q (TN);
@@ -357,6 +361,7 @@ def _cpu_gemm_sample(w: dict, seconds: float, nthreads: int, seed: int):
         if g["dtype"] in ("fp16", "amp"):
             A, B = o.f16_round(A), o.f16_round(B)
         Hs = (rng.standard_normal((rows, N), dtype=np.float32) * np.float32(2.0)) if g["epi"] == "gelu_bwd" else None
+        Xs = rng.standard_normal((rows, N), dtype=np.float32) if g["epi"] == "bias_residual" else None
         if op == "NT":
             B = np.ascontiguousarray(B.T)
         if op == "TN":
@@ -366,7 +371,8 @@ def _cpu_gemm_sample(w: dict, seconds: float, nthreads: int, seed: int):
         while True:
             if kind == "reference":
                 if op == "NN":
-                    C = o.ref_vedic_gemm_bias(A, B, bias) if g["epi"] in ("bias", "bias_gelu") else o.ref_vedic_gemm(A, B)
+                    C = (o.ref_vedic_gemm_bias(A, B, bias) if g["epi"] in ("bias", "bias_gelu", "bias_residual")
+                         else o.ref_vedic_gemm(A, B))
                 elif op == "NT":
                     C = o.ref_gemm_nt(A, B)
                 else:
@@ -376,9 +382,12 @@ def _cpu_gemm_sample(w: dict, seconds: float, nthreads: int, seed: int):
                 if g["epi"] == "gelu_bwd":  # ffn_backward's gelu_backward + bias_backward
                     C = o.ref_gelu_backward(Hs, C)
                     o.ref_bias_backward(C)
+                if g["epi"] == "bias_residual":  # the residual add after the FFN-down
+                    C = Xs + C
             else:
                 if op == "NN":
-                    C = (o.vedic_gemm_bias(A, B, bias, nthreads=nthreads) if g["epi"] in ("bias", "bias_gelu")
+                    C = (o.vedic_gemm_bias(A, B, bias, nthreads=nthreads)
+                         if g["epi"] in ("bias", "bias_gelu", "bias_residual")
                          else o.vedic_gemm(A, B, nthreads=nthreads))
                 elif op == "NT":
                     C = o.gemm_nt(A, B, nthreads=nthreads)
@@ -389,6 +398,8 @@ def _cpu_gemm_sample(w: dict, seconds: float, nthreads: int, seed: int):
                 if g["epi"] == "gelu_bwd":
                     C = o.gelu_bwd_reference_f32(C, Hs)
                     C.sum(axis=0)
+                if g["epi"] == "bias_residual":
+                    C = Xs + C
             reps += 1
             if time.perf_counter() - t0 >= per_gemm:
                 break
@@ -458,10 +469,12 @@ def make_step(w: dict, dev, torch):
                 A, a_again = shared_a, True
         g["_cast"] = (A32, A) if A32 is not None else None
         keep.append(A32)
-        C = torch.randn((M, N), generator=gen, device=dev) * 1e-3 if g["beta"] else torch.empty((M, N), device=dev)
+        resid = g["epi"] == "bias_residual"
+        C = (torch.randn((M, N), generator=gen, device=dev) * (1.0 if resid else 1e-3) if g["beta"] or resid
+             else torch.empty((M, N), device=dev))
         keep += [A, B, bias, C]
         epi = {"none": _lib.EPI_NONE, "bias": _lib.EPI_BIAS, "bias_gelu": _lib.EPI_BIAS_GELU,
-               "gelu_bwd": _lib.EPI_GELU_BWD}[g["epi"]]
+               "gelu_bwd": _lib.EPI_GELU_BWD, "bias_residual": _lib.EPI_BIAS_RESIDUAL}[g["epi"]]
         gbwd = g["epi"] == "gelu_bwd"
         H = torch.randn((M, N), generator=gen, device=dev) * 2.0 if gbwd else None
         db = torch.zeros((N,), device=dev) if gbwd else None
@@ -472,12 +485,12 @@ def make_step(w: dict, dev, torch):
             out_dtype=_lib.DT_F32,
             M=M, N=N, K=K, A=A.data_ptr(), lda=A.shape[1], B=B.data_ptr(), ldb=B.shape[1],
             C=C.data_ptr(), ldc=N, alpha=g["alpha"], beta=g["beta"],
-            bias=bias.data_ptr() if g["epi"] in ("bias", "bias_gelu") else None, epilogue=epi,
+            bias=bias.data_ptr() if g["epi"] in ("bias", "bias_gelu", "bias_residual") else None, epilogue=epi,
             preact=H.data_ptr() if gbwd else None, ld_preact=N if gbwd else 0, stream=stream.cuda_stream,
             colsum=db.data_ptr() if gbwd else None, colsum_beta=1.0)
         es = 2 if g["dtype"] == "fp16" else 4
         es_b = 4 if g["dtype"] == "fp32" else 2
-        hbm = (0 if a_again else M * K * es) + K * N * es_b + M * N * 4 * (2 if g["beta"] else 1) + \
+        hbm = (0 if a_again else M * K * es) + K * N * es_b + M * N * 4 * (2 if g["beta"] or resid else 1) + \
             (N * 4 if g["epi"] != "none" else 0)
         if g["cast_a"]:
             hbm += M * K * 6  # the cast pass: fp32 read, binary16 written

@@ -19,6 +19,7 @@
  *     pre   = t                                  (stored if preact != NULL)
  *     C     = gelu_tanh(t) or t                  (per the epilogue)
  *     C     = t * gelu_tanh'(P)                  (VEDIC_EPI_GELU_BWD, P read from preact)
+ *     C     = C_old + t                          (VEDIC_EPI_*RESIDUAL, beta = 0; t after the bias)
  *     colsum[j] = colsum_beta * colsum[j] + sum_i C[i][j]   (if colsum != NULL)
  * where gelu_tanh(x) = 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3)))
  * (include/FeedForward.hpp:11-13).  For alpha = 1, beta = 0 the bias is added
@@ -79,8 +80,16 @@ typedef enum {
     VEDIC_EPI_BIAS = 1,      /* + bias[j]                 */
     VEDIC_EPI_BIAS_GELU = 2, /* gelu_tanh(t + bias[j])    */
     VEDIC_EPI_GELU = 3,      /* gelu_tanh(t)              */
-    VEDIC_EPI_GELU_BWD = 4   /* t * gelu_tanh'(P[i][j]), P = the cached
+    VEDIC_EPI_GELU_BWD = 4,  /* t * gelu_tanh'(P[i][j]), P = the cached
                                 pre-activation, read through `preact` */
+    VEDIC_EPI_RESIDUAL = 5,  /* C_old + t: C holds the residual stream on entry
+                                (beta must be 0; fp32 C; `preact`, if set,
+                                receives t) -- the reference's projection
+                                followed by residual_add_kernel,
+                                cuda/ModelGPU.cu:57-60, 1005-1012 */
+    VEDIC_EPI_BIAS_RESIDUAL = 6 /* C_old + (t + bias[j]): the reference's
+                                FFN-down amp_gemm_bias into a temporary, then
+                                residual_add_kernel (cuda/ModelGPU.cu:1044-1048) */
 } vedic_epilogue_t;
 
 typedef enum {

@@ -30,6 +30,7 @@ STATUS_UNSUPPORTED = 9
 
 OP_NN, OP_NT, OP_TN = 0, 1, 2
 EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU, EPI_GELU_BWD = 0, 1, 2, 3, 4
+EPI_RESIDUAL, EPI_BIAS_RESIDUAL = 5, 6
 DT_F32, DT_F16, DT_F32_F16 = 0, 1, 2
 
 

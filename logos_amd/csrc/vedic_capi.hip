@@ -237,6 +237,7 @@ __global__ void splitk_reduce4_kernel(const float* __restrict__ ws, int S, GemmA
         if (epi & EPI_BETA) v += a.beta * *cp;
         if (epi & EPI_BIAS) v += *reinterpret_cast<const float4_t*>(a.bias + j);
         if (epi & EPI_PREACT) *reinterpret_cast<float4_t*>(a.preact + (int64_t)i * a.ldp + j) = v;
+        if (epi & EPI_RESID) v = *cp + v;
         if (epi & EPI_GELU) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
@@ -267,6 +268,7 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ ws, int S, GemmAr
             v += a.beta * (f16out ? (float)static_cast<const _Float16*>(a.C)[c] : static_cast<const float*>(a.C)[c]);
         if (epi & EPI_BIAS) v += a.bias[j];
         if (epi & EPI_PREACT) a.preact[(int64_t)i * a.ldp + j] = v;
+        if (epi & EPI_RESID) v = static_cast<const float*>(a.C)[c] + v;
         if (epi & EPI_GELU) v = gelu_tanh(v);
         if (epi & EPI_GELU_BWD) v *= gelu_tanh_grad(a.preact[(int64_t)i * a.ldp + j]);
         if (f16out)
@@ -553,9 +555,15 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
         !(d->out_dtype == VEDIC_DT_F16 && (d->in_dtype == VEDIC_DT_F16 || amp)))
         return VEDIC_STATUS_BAD_DTYPE;
     if (!d->A || !d->B || (!d->C && !scatter)) return VEDIC_STATUS_NULL_POINTER;
-    if (d->epilogue < VEDIC_EPI_NONE || d->epilogue > VEDIC_EPI_GELU_BWD) return VEDIC_STATUS_BAD_EPILOGUE;
-    const bool want_bias = d->epilogue == VEDIC_EPI_BIAS || d->epilogue == VEDIC_EPI_BIAS_GELU;
+    if (d->epilogue < VEDIC_EPI_NONE || d->epilogue > VEDIC_EPI_BIAS_RESIDUAL) return VEDIC_STATUS_BAD_EPILOGUE;
+    const bool want_bias = d->epilogue == VEDIC_EPI_BIAS || d->epilogue == VEDIC_EPI_BIAS_GELU ||
+                           d->epilogue == VEDIC_EPI_BIAS_RESIDUAL;
     if (want_bias && !d->bias) return VEDIC_STATUS_BAD_EPILOGUE;
+    // the residual forms read C as the residual stream: fp32 C, no beta term,
+    // no column sums, no scattered heads
+    const bool resid = d->epilogue == VEDIC_EPI_RESIDUAL || d->epilogue == VEDIC_EPI_BIAS_RESIDUAL;
+    if (resid && (d->beta != 0.0f || d->out_dtype != VEDIC_DT_F32 || d->colsum || scatter))
+        return VEDIC_STATUS_BAD_EPILOGUE;
     // GELU backward reads the cached pre-activation through `preact`
     const bool gelu_bwd = d->epilogue == VEDIC_EPI_GELU_BWD;
     if (gelu_bwd && !d->preact) return VEDIC_STATUS_BAD_EPILOGUE;
@@ -596,6 +604,7 @@ static int gemm_impl(const vedic_gemm_desc_t* d, float* const* heads, int nheads
     if (d->alpha != 1.0f) a.epi |= EPI_ALPHA;
     if (d->out_dtype == VEDIC_DT_F16) a.epi |= EPI_F16OUT;
     if (d->colsum) a.epi |= EPI_COLSUM;
+    if (resid) a.epi |= EPI_RESID;
     a.group_m = 8;
 
     // 16-byte vector loads need aligned bases, leading dimensions that keep

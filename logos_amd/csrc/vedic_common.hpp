@@ -77,6 +77,7 @@ enum : int {
     EPI_F16OUT = 32,
     EPI_GELU_BWD = 64,  // C = t * gelu_tanh_grad(P), P read through `preact`
     EPI_COLSUM = 128,   // column sums of C into cs_part (per 32-row block)
+    EPI_RESID = 256,    // C = C_old + t (t after alpha and bias; P = t if preact)
 };
 
 constexpr int kMaxHeads = 64;  // scatter targets per GEMM

@@ -26,9 +26,11 @@ enum EpiKind : int {
     EK_GENERIC = 5,        // any flag combination (runtime flags)
     EK_GELU_BWD = 6,       // C = acc * gelu'(P)    (+ column sums if cs_part)
     EK_LINEAR_CS = 7,      // C = alpha acc (+ b), with column sums if cs_part
+    EK_RESIDUAL = 8,       // t = acc (+ b); P = t if preact; C = C_old + t
 };
 
 __host__ __device__ inline int epi_kind_of(int epi, float alpha, float beta) {
+    if (epi & EPI_RESID) return (epi & ~(EPI_RESID | EPI_BIAS | EPI_PREACT)) == 0 ? EK_RESIDUAL : EK_GENERIC;
     if ((epi & ~EPI_COLSUM) == EPI_GELU_BWD) return EK_GELU_BWD;
     if ((epi & EPI_COLSUM) && (epi & ~(EPI_COLSUM | EPI_ALPHA | EPI_BIAS)) == 0) return EK_LINEAR_CS;
     if (epi & EPI_COLSUM) return EK_GENERIC;
@@ -73,7 +75,7 @@ __device__ __forceinline__ float ld_f16(__amdgpu_buffer_rsrc_t rs, uint32_t voff
 template <int KIND>
 __device__ __forceinline__ bool epi_wants_bias(const GemmArgs& a) {
     return (KIND == EK_BIAS || KIND == EK_BIAS_GELU || KIND == EK_BIAS_GELU_PRE) ||
-           ((KIND == EK_GENERIC || KIND == EK_LINEAR_CS) && (a.epi & EPI_BIAS));
+           ((KIND == EK_GENERIC || KIND == EK_LINEAR_CS || KIND == EK_RESIDUAL) && (a.epi & EPI_BIAS));
 }
 
 // Writes a (32*MI) x (32*NI) wave tile whose top-left output is (row0, col0)
@@ -91,7 +93,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, void* Cp, const floa
     const char* cbase = static_cast<const char*>(Cp) + ((int64_t)row0 * a.ldc) * es;
     const __amdgpu_buffer_rsrc_t rc_tile = buffer_rsrc(cbase);
     __amdgpu_buffer_rsrc_t rp = rc_tile;
-    const bool pre = (KIND == EK_BIAS_GELU_PRE) || (KIND == EK_GENERIC && (a.epi & EPI_PREACT));
+    const bool pre = (KIND == EK_BIAS_GELU_PRE) || ((KIND == EK_GENERIC || KIND == EK_RESIDUAL) && (a.epi & EPI_PREACT));
     const bool gbwd = (KIND == EK_GELU_BWD) || (KIND == EK_GENERIC && (a.epi & EPI_GELU_BWD));
     if (pre || gbwd) rp = buffer_rsrc(a.preact + (int64_t)row0 * a.ldp);
     // column sums: per lane over its 16 rows of each 32-row block, then the
@@ -106,8 +108,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, void* Cp, const floa
     // a whole 32 x 32 block's values before they are needed: the next block's
     // loads go out before this block's stores, so the load latency is paid
     // about once per wave tile rather than once per element.
-    constexpr bool READS = KIND == EK_ACCUM || KIND == EK_GELU_BWD || KIND == EK_GENERIC;
-    const bool rd_c = KIND == EK_ACCUM || (KIND == EK_GENERIC && (a.epi & EPI_BETA));
+    constexpr bool READS = KIND == EK_ACCUM || KIND == EK_GELU_BWD || KIND == EK_GENERIC || KIND == EK_RESIDUAL;
+    const bool rd_c = KIND == EK_ACCUM || KIND == EK_RESIDUAL || (KIND == EK_GENERIC && (a.epi & (EPI_BETA | EPI_RESID)));
     const bool rd_p = gbwd;
     constexpr int NB = MI * NI;  // 32 x 32 blocks, in the order j-major, i-minor
 
@@ -194,6 +196,12 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, void* Cp, const floa
                     v *= gelu_tanh_grad(cur_p[e]);
                     st_f32(v, rc, oc, sc);
                     if (!CHECK || oc != kOob) csum += v;
+                } else if constexpr (KIND == EK_RESIDUAL) {
+                    // the bias is added to the product before the residual,
+                    // as the reference's GEMM + bias then residual_add_kernel
+                    const float t = want_bias ? v + bj : v;
+                    if (pre) st_f32(t, rp, op, sp);
+                    st_f32(cur_c[e] + t, rc, oc, sc);
                 } else if constexpr (KIND == EK_LINEAR_CS) {
                     v = __builtin_fmaf(v, a.alpha, bj);
                     st_f32(v, rc, oc, sc);
@@ -202,8 +210,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, void* Cp, const floa
                     const int epi = a.epi;
                     if (epi & EPI_ALPHA) v *= a.alpha;
                     if (epi & EPI_BETA) v += a.beta * cur_c[e];
-                    v += bj;
+                    if (!(epi & EPI_RESID) || (epi & EPI_BIAS)) v += bj;
                     if (epi & EPI_PREACT) st_f32(v, rp, op, sp);
+                    if (epi & EPI_RESID) v = cur_c[e] + v;
                     if (epi & EPI_GELU) v = gelu_tanh(v);
                     if (epi & EPI_GELU_BWD) v *= gelu_tanh_grad(cur_p[e]);
                     if (f16out)

@@ -706,7 +706,8 @@ int device_cu_count();
     VEDIC_F16_KERNEL(OP, Cfg, EK_ACCUM);          \
     VEDIC_F16_KERNEL(OP, Cfg, EK_GENERIC);        \
     VEDIC_F16_KERNEL(OP, Cfg, EK_GELU_BWD);       \
-    VEDIC_F16_KERNEL(OP, Cfg, EK_LINEAR_CS)
+    VEDIC_F16_KERNEL(OP, Cfg, EK_LINEAR_CS);      \
+    VEDIC_F16_KERNEL(OP, Cfg, EK_RESIDUAL)
 
 #ifndef VEDIC_F16_COLUMN_SPLIT
 #define VEDIC_F16_COLUMN_SPLIT 1
@@ -763,6 +764,7 @@ static hipError_t launch_f16_kind(const GemmArgs& a, hipStream_t s) {
         case EK_ACCUM: return launch_f16<OP, Cfg, EK_ACCUM>(a, s);
         case EK_GELU_BWD: return launch_f16<OP, Cfg, EK_GELU_BWD>(a, s);
         case EK_LINEAR_CS: return launch_f16<OP, Cfg, EK_LINEAR_CS>(a, s);
+        case EK_RESIDUAL: return launch_f16<OP, Cfg, EK_RESIDUAL>(a, s);
         default: return launch_f16<OP, Cfg, EK_GENERIC>(a, s);
     }
 }

@@ -434,6 +434,7 @@ static hipError_t launch_f32_kind(const GemmArgs& a, hipStream_t s) {
         case EK_ACCUM: return launch_f32<OP, EK_ACCUM, Cfg>(a, s);
         case EK_GELU_BWD: return launch_f32<OP, EK_GELU_BWD, Cfg>(a, s);
         case EK_LINEAR_CS: return launch_f32<OP, EK_LINEAR_CS, Cfg>(a, s);
+        case EK_RESIDUAL: return launch_f32<OP, EK_RESIDUAL, Cfg>(a, s);
         default: return launch_f32<OP, EK_GENERIC, Cfg>(a, s);
     }
 }

@@ -20,6 +20,7 @@ VEDIC_F32_INST(EK_ACCUM)
 VEDIC_F32_INST(EK_GENERIC)
 VEDIC_F32_INST(EK_GELU_BWD)
 VEDIC_F32_INST(EK_LINEAR_CS)
+VEDIC_F32_INST(EK_RESIDUAL)
 #undef VEDIC_F32_INST
 
 hipError_t launch_gemm_f32_direct_tn(const GemmArgs& a, hipStream_t s) { return launch_gemm_f32_direct_op<2>(a, s); }

@@ -27,11 +27,12 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from ._lib import (DT_F16, DT_F32, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU, EPI_GELU_BWD, EPI_NONE, OP_NN, OP_NT,
-                   OP_TN)
+from ._lib import (DT_F16, DT_F32, EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESIDUAL, EPI_GELU, EPI_GELU_BWD, EPI_NONE,
+                   EPI_RESIDUAL, OP_NN, OP_NT, OP_TN)
 
 __all__ = [
     "OP_NN", "OP_NT", "OP_TN", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU", "EPI_GELU", "EPI_GELU_BWD",
+    "EPI_RESIDUAL", "EPI_BIAS_RESIDUAL", "gemm_bias_residual",
     "gemm", "vedic_gemm", "vedic_gemm_bias", "gemm_fp16_fp32out", "gemm_fp16_fp16out",
     "gemm_bias_gelu", "amp_gemm", "gemm_nt", "gemm_tn", "gemm_nt_gelu_bwd", "bias_grad", "gemm_scatter",
     "cast_pack_fp16", "add_bias", "gelu_",
@@ -104,6 +105,11 @@ def gemm(op: int, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor | None = Non
         raise ValueError(f"unknown op {op}")
     if Kb != K:
         raise ValueError(f"VedicGEMM: inner dimensions differ (A gives K={K}, B gives K={Kb})")
+    if epilogue in (EPI_RESIDUAL, EPI_BIAS_RESIDUAL):
+        if C is None or C.dtype != torch.float32:
+            raise ValueError("the residual epilogues add to an existing float32 C (the residual stream)")
+        if beta != 0.0:
+            raise ValueError("the residual epilogues take beta = 0 (C is the residual)")
     if C is None:
         if beta != 0.0:
             raise ValueError("beta != 0 needs an existing C")
@@ -135,6 +141,18 @@ def gemm(op: int, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor | None = Non
     )
     _check(_lib.load().vedic_gemm(ctypes.byref(d)))
     return C
+
+
+def gemm_bias_residual(X: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None, residual: torch.Tensor,
+                       out_pre: torch.Tensor | None = None) -> torch.Tensor:
+    """residual += X . W (+ bias), in place, with the product (and bias)
+    rounded before the residual is added: the reference's FFN-down
+    amp_gemm_bias into a temporary followed by residual_add_kernel
+    (cuda/ModelGPU.cu:1044-1048), and its W_proj projection, saved and then
+    added (:1005-1012), with out_pre receiving the product.  X and W float32,
+    or float16, or float32 X with a float16 shadow W (AMP)."""
+    epi = EPI_BIAS_RESIDUAL if bias is not None else EPI_RESIDUAL
+    return gemm(OP_NN, X, W, residual, bias=bias, epilogue=epi, preact=out_pre)
 
 
 def vedic_gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:

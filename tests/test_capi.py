@@ -65,6 +65,10 @@ def _desc(**kw):
     (dict(ldc=2), _lib.STATUS_BAD_LD),
     (dict(epilogue=1), _lib.STATUS_BAD_EPILOGUE),  # bias missing
     (dict(epilogue=9), _lib.STATUS_BAD_EPILOGUE),
+    (dict(epilogue=7), _lib.STATUS_BAD_EPILOGUE),
+    (dict(epilogue=6), _lib.STATUS_BAD_EPILOGUE),  # residual with bias: bias missing
+    (dict(epilogue=5, beta=1.0), _lib.STATUS_BAD_EPILOGUE),  # the residual is C itself
+    (dict(epilogue=5, in_dtype=1, out_dtype=1), _lib.STATUS_BAD_EPILOGUE),  # fp32 residual stream only
 ])
 def test_gemm_validation(kw, status):
     d = _desc(**kw)
