@@ -272,6 +272,64 @@ inline void cuda_gemm_fp16_bias_gelu(const __half* X, int M, int K, const __half
     vedic_hip::check(vedic_gemm_bias_gelu_f16(X, W, bias, H, preact, M, K, N, stream), "cuda_gemm_fp16_bias_gelu");
 }
 
+// The projection added to the residual stream in one GEMM: X[M x N] +=
+// A[M x K] . W[K x N] (+ bias), with the product and bias rounded before the
+// residual is added, as the reference's amp_gemm / amp_gemm_bias into a
+// temporary followed by residual_add_kernel (cuda/ModelGPU.cu:1005-1012,
+// 1044-1048); out_pre (nullable) receives the product (the reference's saved
+// cache.attn_out).  Binary16 inputs, and the fp32 GPUTensor form below.
+inline void cuda_gemm_fp16_bias_residual(const __half* A, int M, int K, const __half* W, int N, const float* bias,
+                                         float* X, float* out_pre = nullptr, hipStream_t stream = nullptr) {
+    vedic_gemm_desc_t d{};
+    d.op = VEDIC_OP_NN;
+    d.in_dtype = VEDIC_DT_F16;
+    d.out_dtype = VEDIC_DT_F32;
+    d.M = M;
+    d.N = N;
+    d.K = K;
+    d.A = A;
+    d.lda = K;
+    d.B = W;
+    d.ldb = N;
+    d.C = X;
+    d.ldc = N;
+    d.alpha = 1.0f;
+    d.bias = bias;
+    d.epilogue = bias ? VEDIC_EPI_BIAS_RESIDUAL : VEDIC_EPI_RESIDUAL;
+    d.preact = out_pre;
+    d.ld_preact = out_pre ? N : 0;
+    d.stream = stream;
+    vedic_hip::check(vedic_gemm(&d), "cuda_gemm_fp16_bias_residual");
+}
+inline void cuda_vedic_gemm_bias_residual(const GPUTensor& A, const GPUTensor& W, const GPUTensor* bias, GPUTensor& X,
+                                          GPUTensor* out_pre = nullptr, hipStream_t stream = nullptr) {
+    vedic_hip::require(W.rows == A.cols, "cuda_vedic_gemm_bias_residual: A.cols != W.rows");
+    vedic_hip::require(X.rows == A.rows && X.cols == W.cols, "cuda_vedic_gemm_bias_residual: X shape");
+    vedic_hip::require(!bias || bias->size == W.cols, "cuda_vedic_gemm_bias_residual: bias size != W.cols");
+    vedic_hip::require(!out_pre || (out_pre->rows == X.rows && out_pre->cols == X.cols),
+                       "cuda_vedic_gemm_bias_residual: out_pre shape");
+    vedic_gemm_desc_t d{};
+    d.op = VEDIC_OP_NN;
+    d.in_dtype = VEDIC_DT_F32;
+    d.out_dtype = VEDIC_DT_F32;
+    d.M = A.rows;
+    d.N = W.cols;
+    d.K = A.cols;
+    d.A = A.data;
+    d.lda = A.cols;
+    d.B = W.data;
+    d.ldb = W.cols;
+    d.C = X.data;
+    d.ldc = X.cols;
+    d.alpha = 1.0f;
+    d.bias = bias ? bias->data : nullptr;
+    d.epilogue = bias ? VEDIC_EPI_BIAS_RESIDUAL : VEDIC_EPI_RESIDUAL;
+    d.preact = out_pre ? out_pre->data : nullptr;
+    d.ld_preact = out_pre ? out_pre->cols : 0;
+    d.stream = stream;
+    vedic_hip::check(vedic_gemm(&d), "cuda_vedic_gemm_bias_residual");
+}
+
 // dX[M x N] = dY[M x K] . W^T + beta dX, W stored [N x K], binary16 inputs.
 inline void cuda_gemm_fp16_nt(const __half* dY, int M, int K, const __half* W, int N, float* dX,
                               float beta = 0.f, hipStream_t stream = nullptr) {

@@ -332,6 +332,39 @@ static void test_fp16_path() {
     EXPECT(e <= 2e-3, "fp16 TN err %.3e", e);
 }
 
+// The residual forms against the reference's two steps: the bias GEMM into a
+// temporary, then X += temporary (residual_add_kernel, cuda/ModelGPU.cu:57-60),
+// bit for bit; the saved product equals the temporary.
+static void test_residual() {
+    Rng r(41);
+    const int M = 300, K = 264, N = 136;
+    auto A = rand_vec(r, (size_t)M * K), W = rand_vec(r, (size_t)K * N, 0.05), b = rand_vec(r, N, 0.1),
+         X = rand_vec(r, (size_t)M * N);
+    GPUTensor gA = upload(A, M, K), gW = upload(W, K, N), gb = upload(b, 1, N), gX = upload(X, M, N);
+    GPUTensor T = gpu_alloc(M, N), P = gpu_alloc(M, N);
+    cuda_vedic_gemm_bias(gA, gW, gb, T);
+    cuda_vedic_gemm_bias_residual(gA, gW, &gb, gX, &P);
+    auto t = download(T), x = download(gX), p = download(P);
+    bool same = true, pre = true;
+    for (size_t i = 0; i < x.size(); ++i) {
+        same = same && x[i] == X[i] + t[i];
+        pre = pre && p[i] == t[i];
+    }
+    EXPECT(same, "fp32 residual != X + (A.W + b)");
+    EXPECT(pre, "fp32 residual: saved product != bias GEMM");
+    // binary16 inputs, no bias
+    HalfTensor hA = half_alloc(M, K), hW = half_alloc(K, N);
+    cuda_cast_fp32_to_fp16(gA.data, hA.data, M * K);
+    cuda_cast_fp32_to_fp16(gW.data, hW.data, K * N);
+    GPUTensor gX2 = upload(X, M, N), T2 = gpu_alloc(M, N);
+    cuda_gemm_fp16_fp32out(hA.data, M, K, hW.data, N, T2.data);
+    cuda_gemm_fp16_bias_residual(hA.data, M, K, hW.data, N, nullptr, gX2.data);
+    auto t2 = download(T2), x2 = download(gX2);
+    same = true;
+    for (size_t i = 0; i < x2.size(); ++i) same = same && x2[i] == X[i] + t2[i];
+    EXPECT(same, "fp16 residual != X + A.W");
+}
+
 static void test_errors_and_verify() {
     GPUTensor A = gpu_alloc(2, 3), B = gpu_alloc(4, 2), C = gpu_alloc(2, 2);
     bool threw = false;
@@ -385,6 +418,8 @@ int main() {
         std::printf("backward fusion done\n");
         test_fp16_path();
         std::printf("fp16 path done\n");
+        test_residual();
+        std::printf("residual done\n");
         test_errors_and_verify();
         std::printf("errors and verify done\n");
     } catch (const std::exception& e) {
