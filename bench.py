@@ -129,6 +129,12 @@ COPY_WORKLOAD = "copy_256mib"  # calibration for the FETCH_SIZE / WRITE_SIZE cou
 # read, 256 MiB written) as a second calibration: its loads take the same path
 # as the GEMM kernels' operand loads.
 CAST_WORKLOAD = "cast_f16_f32_64mi"
+# The activation producer: layer normalisation of the 8192 x 1024 residual
+# stream (cuda_layernorm, cuda/ModelGPU.cu:772) writing the fp32 rows and their
+# binary16 copy in one pass, timed beside the two passes it replaces (the fp32
+# normalisation, then the cast the reference's amp_gemm runs per call,
+# cuda/ModelGPU.cu:825-827).  HBM-bound: 4 + 4 + 2 bytes per element.
+LN_WORKLOAD = "layernorm_fp16_copy_8192x1024"
 
 
 def parse():
@@ -139,7 +145,7 @@ def parse():
     # 75-77 us): the default warmup runs the kernel for ~40 ms first.
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=500)
-    ap.add_argument("--workload", default="ffn_up_fp16_bias_gelu", choices=sorted(WORKLOADS) + [COPY_WORKLOAD, CAST_WORKLOAD])
+    ap.add_argument("--workload", default="ffn_up_fp16_bias_gelu", choices=sorted(WORKLOADS) + [COPY_WORKLOAD, CAST_WORKLOAD, LN_WORKLOAD])
     ap.add_argument("--all", action="store_true", help="every workload, one JSON line each")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the cpu_baseline sample (default run)")
@@ -725,6 +731,42 @@ def run_cast(args, torch, dev):
             "bytes_read": 2 * n, "bytes_written": 4 * n}
 
 
+def run_layernorm(args, torch, dev):
+    from logos_amd import _lib
+
+    lib = _lib.load()
+    seq, d = 8192, 1024
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x4C4E)
+    X = torch.randn((seq, d), generator=gen, device=dev)
+    g = 1.0 + 0.1 * torch.randn(d, generator=gen, device=dev)
+    b = 0.1 * torch.randn(d, generator=gen, device=dev)
+    Y = torch.empty_like(X)
+    Y16 = torch.empty((seq, d), dtype=torch.float16, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+
+    def ok(rc):
+        if rc:
+            raise RuntimeError(_lib.status_string(rc))
+
+    def fused():
+        ok(lib.vedic_layernorm(X.data_ptr(), g.data_ptr(), b.data_ptr(), Y.data_ptr(), Y16.data_ptr(), seq, d,
+                               1e-5, s))
+
+    def two_pass():
+        ok(lib.vedic_layernorm(X.data_ptr(), g.data_ptr(), b.data_ptr(), Y.data_ptr(), None, seq, d, 1e-5, s))
+        ok(lib.vedic_cast_f32_to_f16(Y.data_ptr(), Y16.data_ptr(), seq * d, s))
+
+    ms, _ = time_steps(fused, args.steps, args.warmup, torch)
+    ms2, _ = time_steps(two_pass, args.steps, args.warmup, torch)
+    nbytes = seq * d * (4 + 4 + 2)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": LN_WORKLOAD, "ms_per_step": round(ms, 5), "GB/s": round(gbs, 1),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s",
+                         "frac": round(gbs / 8000.0, 4)},
+            "two_pass_ms": round(ms2, 5), "bytes_per_step": nbytes}
+
+
 def main():
     args = parse()
     if args.summarize_traffic:
@@ -743,6 +785,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.workload == COPY_WORKLOAD:
         print(json.dumps(run_copy(args, torch, dev)), flush=True)
+        return
+    if args.workload == LN_WORKLOAD:
+        print(json.dumps(run_layernorm(args, torch, dev)), flush=True)
         return
     if args.workload == CAST_WORKLOAD:
         print(json.dumps(run_cast(args, torch, dev)), flush=True)

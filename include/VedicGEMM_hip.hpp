@@ -493,6 +493,30 @@ inline void cuda_add_bias(float* C, const float* bias, int M, int N, hipStream_t
     vedic_hip::check(vedic_add_bias(C, bias, M, N, stream), "cuda_add_bias");
 }
 
+// Row layer normalisation, Y = gamma (X - mean) / sqrt(var + eps) + beta per
+// row (cuda/VedicGEMM.cuh:186, cuda/VedicGEMM.cu:157-193,699-705).
+inline void cuda_layernorm(const GPUTensor& X, const GPUTensor& gamma, const GPUTensor& beta, GPUTensor& Y,
+                           int seq_len, int d_model, float eps = 1e-5f, hipStream_t stream = nullptr) {
+    vedic_hip::require(X.size >= seq_len * d_model && Y.size >= seq_len * d_model, "cuda_layernorm: X / Y size");
+    vedic_hip::require(gamma.size == d_model && beta.size == d_model, "cuda_layernorm: gamma / beta size");
+    vedic_hip::check(vedic_layernorm(X.data, gamma.data, beta.data, Y.data, nullptr, seq_len, d_model, eps, stream),
+                     "cuda_layernorm");
+}
+// The same, also writing the binary16 copy of Y in the pass (the bits of
+// cuda_cast_fp32_to_fp16(Y)): the activation an fp16 GEMM takes without the
+// per-call cast of the reference's amp_gemm (cuda/ModelGPU.cu:825-827).  Y may
+// be null (binary16 only).
+inline void cuda_layernorm_fp16_copy(const float* X, const float* gamma, const float* beta, float* Y, __half* Y16,
+                                     int seq, int d, float eps = 1e-5f, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_layernorm(X, gamma, beta, Y, Y16, seq, d, eps, stream), "cuda_layernorm_fp16_copy");
+}
+// Binary16 rows in and out, fp32 statistics (cuda/VedicGEMM.cuh:253,
+// cuda/MixedPrecision.cuh:458-511).
+inline void cuda_layernorm_fp16(const __half* X, const float* gamma, const float* beta, __half* Y, int seq, int d,
+                                float eps = 1e-5f, hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_layernorm_f16(X, gamma, beta, Y, seq, d, eps, stream), "cuda_layernorm_fp16");
+}
+
 // In-place tanh-GELU (cuda/VedicGEMM.cu:707-711).
 inline void cuda_gelu(GPUTensor& data, hipStream_t stream = nullptr) {
     vedic_hip::check(vedic_gelu(data.data, data.size, stream), "cuda_gelu");

@@ -280,6 +280,24 @@ int vedic_bias_grad(const float* dY, float* db, int M, int N, float beta, void* 
  * Replaces add_bias_kernel (cuda/VedicGEMM.cuh:191, cuda/VedicGEMM.cu:96-102). */
 int vedic_add_bias(float* C, const float* bias, int M, int N, void* stream);
 
+/* Row layer normalisation: Y[i][j] = gamma[j] (X[i][j] - mean_i) /
+ * sqrt(var_i + eps) + beta[j], the mean and the biased variance of row i's d
+ * values accumulated in fp32 (in a fixed order).  Replaces cuda_layernorm
+ * (cuda/VedicGEMM.cuh:186, cuda/VedicGEMM.cu:157-193,699-705).  Y (fp32) and
+ * Y16 (binary16) are each optional, at least one: Y16 receives Y clamped to
+ * +-65504 and rounded to nearest even -- the bits vedic_cast_f32_to_f16(Y)
+ * would give -- in the same pass, so an fp16 GEMM takes the normalised
+ * activation without the per-call cast of the reference's amp_gemm
+ * (cuda/ModelGPU.cu:825-827).  New: the reference writes fp32 only. */
+int vedic_layernorm(const float* X, const float* gamma, const float* beta, float* Y, void* Y16, int seq, int d,
+                    float eps, void* stream);
+
+/* The same on binary16 rows, binary16 out (fp32 statistics; the output
+ * clamped to +-65504 before rounding).  Replaces cuda_layernorm_fp16
+ * (cuda/VedicGEMM.cuh:253, cuda/MixedPrecision.cuh:458-511). */
+int vedic_layernorm_f16(const void* X16, const float* gamma, const float* beta, void* Y16, int seq, int d, float eps,
+                        void* stream);
+
 /* In-place tanh-GELU over n floats.
  * Replaces cuda_gelu (cuda/VedicGEMM.cuh:187, cuda/VedicGEMM.cu:707-711). */
 int vedic_gelu(float* x, int64_t n, void* stream);

@@ -100,6 +100,8 @@ SIGNATURES = {
     "vedic_bias_grad": (c_int, [c_vp, c_vp, c_int, c_int, c_float, c_vp]),
     "vedic_add_bias": (c_int, [c_vp, c_vp, c_int, c_int, c_vp]),
     "vedic_gelu": (c_int, [c_vp, c_i64, c_vp]),
+    "vedic_layernorm": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_float, c_vp]),
+    "vedic_layernorm_f16": (c_int, [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_float, c_vp]),
     "vedic_cast_f32_to_f16": (c_int, [c_vp, c_vp, c_i64, c_vp]),
     "vedic_cast_f16_to_f32": (c_int, [c_vp, c_vp, c_i64, c_vp]),
     "vedic_verify": (

@@ -34,6 +34,7 @@ SOURCES = [
     "vedic_flash_attn.hip",
     "vedic_flash_attn_bwd.hip",
     "vedic_flash_probs.hip",
+    "vedic_layernorm.hip",
     "vedic_capi.hip",
 ]
 

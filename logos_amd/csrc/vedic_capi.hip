@@ -19,6 +19,10 @@
 #include "vedic_epilogue.hpp"
 
 namespace vedic {
+hipError_t launch_layernorm_f32(const float* X, const float* gamma, const float* beta, float* Y, void* Y16, int seq,
+                                int d, float eps, hipStream_t s);
+hipError_t launch_layernorm_f16(const void* X16, const float* gamma, const float* beta, void* Y16, int seq, int d,
+                                float eps, hipStream_t s);
 hipError_t launch_gemm_f16_generic(int op, const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f32(int op, bool vec, const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_nn(const GemmArgs& a, hipStream_t s);
@@ -1409,6 +1413,20 @@ extern "C" int vedic_add_bias(float* C, const float* bias, int M, int N, void* s
     hipLaunchKernelGGL(add_bias_kernel, dim3(ew_blocks((int64_t)M * N, 4)), dim3(kEwThreads), 0,
                        static_cast<hipStream_t>(stream), C, bias, M, N);
     return hip_status(hipGetLastError());
+}
+
+extern "C" int vedic_layernorm(const float* X, const float* gamma, const float* beta, float* Y, void* Y16, int seq,
+                               int d, float eps, void* stream) {
+    if (seq <= 0 || d <= 0) return VEDIC_STATUS_BAD_DIM;
+    if (!X || !gamma || !beta || (!Y && !Y16)) return VEDIC_STATUS_NULL_POINTER;
+    return hip_status(launch_layernorm_f32(X, gamma, beta, Y, Y16, seq, d, eps, static_cast<hipStream_t>(stream)));
+}
+
+extern "C" int vedic_layernorm_f16(const void* X16, const float* gamma, const float* beta, void* Y16, int seq, int d,
+                                   float eps, void* stream) {
+    if (seq <= 0 || d <= 0) return VEDIC_STATUS_BAD_DIM;
+    if (!X16 || !gamma || !beta || !Y16) return VEDIC_STATUS_NULL_POINTER;
+    return hip_status(launch_layernorm_f16(X16, gamma, beta, Y16, seq, d, eps, static_cast<hipStream_t>(stream)));
 }
 
 extern "C" int vedic_gelu(float* x, int64_t n, void* stream) {

@@ -1,0 +1,201 @@
+// vedic_layernorm.hip -- row layer normalisation, the producer of the GEMM
+// path's activations.
+//
+//   Y[i][j] = gamma[j] (X[i][j] - mean_i) / sqrt(var_i + eps) + beta[j]
+//
+// with the mean and the biased variance of row i's d values in fp32, as the
+// reference's layernorm_kernel (cuda/VedicGEMM.cu:157-193, launched by
+// cuda_layernorm, :699-705) and layernorm_fp16_kernel (binary16 in and out,
+// cuda/MixedPrecision.cuh:458-511, launched by cuda_layernorm_fp16,
+// cuda/VedicGEMM.cu:1200-1206).  The fp32 form can also write the binary16
+// copy of Y in the same pass (clamped to +-65504, rounded to nearest even:
+// the bits the cast kernel would give), so an fp16 GEMM consumes the
+// normalised activation with no cast pass of its own.
+//
+// One workgroup of 256 threads (four waves) per row.  A thread keeps its
+// values of the row in registers between the passes when the row fits
+// (d <= kLnHeld * 256); longer rows are read again (from cache).  fp32 rows
+// with d a multiple of 4 and aligned bases go four values per access.  Sums
+// are reduced in a fixed order (per thread, then across the 64 lanes of a
+// wave, then the four waves in order), so results do not depend on timing.
+#include <hip/hip_runtime.h>
+
+#include "vedic_common.hpp"
+
+namespace vedic {
+
+namespace {
+
+constexpr int kLnThreads = 256;
+constexpr int kLnHeld = 16;  // values per thread kept in registers
+
+// Sum over the workgroup: lanes by xor-shuffle (fixed pattern), then the four
+// wave sums in wave order; every thread gets the total.
+__device__ __forceinline__ float ln_block_sum(float v, float* red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    const float t = ((red[0] + red[1]) + red[2]) + red[3];
+    __syncthreads();  // red is reused by the next reduction
+    return t;
+}
+
+template <typename TIn>
+__device__ __forceinline__ float ln_load(const TIn* x, int j) {
+    return (float)x[j];
+}
+
+template <typename TIn, bool OUT32, bool OUT16>
+__global__ void __launch_bounds__(kLnThreads)
+    layernorm_rows_kernel(const TIn* __restrict__ X, const float* __restrict__ gamma,
+                          const float* __restrict__ beta, float* __restrict__ Y, _Float16* __restrict__ Y16,
+                          int d, float eps) {
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const TIn* x = X + row * d;
+    const int tid = threadIdx.x;
+    const bool held = d <= kLnHeld * kLnThreads;
+    float v[kLnHeld];
+    float s = 0.0f;
+    if (held) {
+#pragma unroll
+        for (int k = 0; k < kLnHeld; ++k) {
+            const int j = tid + k * kLnThreads;
+            v[k] = j < d ? ln_load(x, j) : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < kLnHeld; ++k) s += v[k];
+    } else {
+        for (int j = tid; j < d; j += kLnThreads) s += ln_load(x, j);
+    }
+    const float mean = ln_block_sum(s, red) / (float)d;
+    float q = 0.0f;
+    if (held) {
+#pragma unroll
+        for (int k = 0; k < kLnHeld; ++k) {
+            const int j = tid + k * kLnThreads;
+            const float df = v[k] - mean;
+            if (j < d) q += df * df;
+        }
+    } else {
+        for (int j = tid; j < d; j += kLnThreads) {
+            const float df = ln_load(x, j) - mean;
+            q += df * df;
+        }
+    }
+    const float inv = 1.0f / __builtin_sqrtf(ln_block_sum(q, red) / (float)d + eps);
+    auto emit = [&](int j, float xv) {
+        const float y = gamma[j] * (xv - mean) * inv + beta[j];
+        if constexpr (OUT32) Y[row * d + j] = y;
+        if constexpr (OUT16) Y16[row * d + j] = to_half_clamped(y);
+    };
+    if (held) {
+#pragma unroll
+        for (int k = 0; k < kLnHeld; ++k) {
+            const int j = tid + k * kLnThreads;
+            if (j < d) emit(j, v[k]);
+        }
+    } else {
+        for (int j = tid; j < d; j += kLnThreads) emit(j, ln_load(x, j));
+    }
+}
+
+// fp32 rows with d a multiple of 4 and 16-byte aligned rows, d <= 4096: four
+// consecutive values per thread and access (16-byte loads and stores, 8-byte
+// binary16 stores).
+template <bool OUT32, bool OUT16>
+__global__ void __launch_bounds__(kLnThreads)
+    layernorm_rows4_kernel(const float* __restrict__ X, const float* __restrict__ gamma,
+                           const float* __restrict__ beta, float* __restrict__ Y, _Float16* __restrict__ Y16, int d,
+                           float eps) {
+    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+    constexpr int H4 = kLnHeld / 4;  // float4 per thread
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const float4_t* x = reinterpret_cast<const float4_t*>(X + row * d);
+    const int tid = threadIdx.x, d4 = d / 4;
+    float4_t v[H4];
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < H4; ++k) {
+        const int j = tid + k * kLnThreads;
+        v[k] = j < d4 ? x[j] : float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int k = 0; k < H4; ++k) s += ((v[k][0] + v[k][1]) + v[k][2]) + v[k][3];
+    const float mean = ln_block_sum(s, red) / (float)d;
+    float q = 0.0f;
+#pragma unroll
+    for (int k = 0; k < H4; ++k) {
+        const int j = tid + k * kLnThreads;
+        if (j < d4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float df = v[k][e] - mean;
+                q += df * df;
+            }
+        }
+    }
+    const float inv = 1.0f / __builtin_sqrtf(ln_block_sum(q, red) / (float)d + eps);
+    const float4_t* g4 = reinterpret_cast<const float4_t*>(gamma);
+    const float4_t* b4 = reinterpret_cast<const float4_t*>(beta);
+#pragma unroll
+    for (int k = 0; k < H4; ++k) {
+        const int j = tid + k * kLnThreads;
+        if (j < d4) {
+            const float4_t gv = g4[j], bv = b4[j];
+            float4_t y;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = gv[e] * (v[k][e] - mean) * inv + bv[e];
+            if constexpr (OUT32) reinterpret_cast<float4_t*>(Y + row * d)[j] = y;
+            if constexpr (OUT16) {
+                half4_t h;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) h[e] = to_half_clamped(y[e]);
+                reinterpret_cast<half4_t*>(Y16 + row * d)[j] = h;
+            }
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_layernorm_f32(const float* X, const float* gamma, const float* beta, float* Y, void* Y16, int seq,
+                                int d, float eps, hipStream_t s) {
+    _Float16* y16 = static_cast<_Float16*>(Y16);
+    const dim3 grid((unsigned)seq), block(kLnThreads);
+    const uintptr_t al = reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(gamma) |
+                         reinterpret_cast<uintptr_t>(beta) | reinterpret_cast<uintptr_t>(Y);
+    if (d % 4 == 0 && d <= kLnHeld * kLnThreads && (al & 15) == 0 && (reinterpret_cast<uintptr_t>(Y16) & 7) == 0) {
+        if (Y && y16)
+            hipLaunchKernelGGL((layernorm_rows4_kernel<true, true>), grid, block, 0, s, X, gamma, beta, Y, y16, d, eps);
+        else if (Y)
+            hipLaunchKernelGGL((layernorm_rows4_kernel<true, false>), grid, block, 0, s, X, gamma, beta, Y, y16, d,
+                               eps);
+        else
+            hipLaunchKernelGGL((layernorm_rows4_kernel<false, true>), grid, block, 0, s, X, gamma, beta, Y, y16, d,
+                               eps);
+        return hipGetLastError();
+    }
+    if (Y && y16)
+        hipLaunchKernelGGL((layernorm_rows_kernel<float, true, true>), grid, block, 0, s, X, gamma, beta, Y, y16, d,
+                           eps);
+    else if (Y)
+        hipLaunchKernelGGL((layernorm_rows_kernel<float, true, false>), grid, block, 0, s, X, gamma, beta, Y, y16, d,
+                           eps);
+    else
+        hipLaunchKernelGGL((layernorm_rows_kernel<float, false, true>), grid, block, 0, s, X, gamma, beta, Y, y16, d,
+                           eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_layernorm_f16(const void* X16, const float* gamma, const float* beta, void* Y16, int seq, int d,
+                                float eps, hipStream_t s) {
+    hipLaunchKernelGGL((layernorm_rows_kernel<_Float16, false, true>), dim3((unsigned)seq), dim3(kLnThreads), 0, s,
+                       static_cast<const _Float16*>(X16), gamma, beta, nullptr, static_cast<_Float16*>(Y16), d, eps);
+    return hipGetLastError();
+}
+
+}  // namespace vedic

@@ -32,7 +32,7 @@ from ._lib import (DT_F16, DT_F32, EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESIDUAL, E
 
 __all__ = [
     "OP_NN", "OP_NT", "OP_TN", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU", "EPI_GELU", "EPI_GELU_BWD",
-    "EPI_RESIDUAL", "EPI_BIAS_RESIDUAL", "gemm_bias_residual",
+    "EPI_RESIDUAL", "EPI_BIAS_RESIDUAL", "gemm_bias_residual", "layernorm", "layernorm_fp16",
     "gemm", "vedic_gemm", "vedic_gemm_bias", "gemm_fp16_fp32out", "gemm_fp16_fp16out",
     "gemm_bias_gelu", "amp_gemm", "gemm_nt", "gemm_tn", "gemm_nt_gelu_bwd", "bias_grad", "gemm_scatter",
     "cast_pack_fp16", "add_bias", "gelu_",
@@ -311,6 +311,51 @@ def add_bias(C: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
         raise ValueError("bias size mismatch")
     _check(_lib.load().vedic_add_bias(C.data_ptr(), bias.contiguous().data_ptr(), M, N, _stream()))
     return C
+
+
+def _ln_args(X, gamma, beta, dtype):
+    if not X.is_cuda or X.dtype != dtype or X.dim() != 2 or not X.is_contiguous():
+        raise ValueError(f"X must be a contiguous 2-D {dtype} GPU tensor")
+    seq, d = X.shape
+    for name, t in (("gamma", gamma), ("beta", beta)):
+        if not t.is_cuda or t.dtype != torch.float32 or t.numel() != d or not t.is_contiguous():
+            raise ValueError(f"{name} must be {d} contiguous float32 values on the GPU")
+    return seq, d
+
+
+def layernorm(X: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, out: torch.Tensor | None = None,
+              out16: torch.Tensor | None = None, eps: float = 1e-5, fp32: bool = True,
+              fp16: bool = False) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+    """Row layer normalisation (cuda_layernorm): returns (Y fp32, Y16 binary16),
+    each written when asked for (fp32 / fp16, or out / out16 given); Y16 holds
+    the bits cast_fp32_to_fp16(Y) would give, written in the same pass."""
+    seq, d = _ln_args(X, gamma, beta, torch.float32)
+    if out is None and fp32:
+        out = torch.empty_like(X)
+    if out16 is None and fp16:
+        out16 = torch.empty(X.shape, dtype=torch.float16, device=X.device)
+    if out is None and out16 is None:
+        raise ValueError("ask for at least one output")
+    for t, dt in ((out, torch.float32), (out16, torch.float16)):
+        if t is not None and (t.shape != X.shape or t.dtype != dt or not t.is_contiguous()):
+            raise ValueError(f"outputs must be contiguous {seq}x{d} tensors")
+    _check(_lib.load().vedic_layernorm(X.data_ptr(), gamma.data_ptr(), beta.data_ptr(),
+                                       out.data_ptr() if out is not None else None,
+                                       out16.data_ptr() if out16 is not None else None, seq, d, eps, _stream()))
+    return out, out16
+
+
+def layernorm_fp16(X16: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, out16: torch.Tensor | None = None,
+                   eps: float = 1e-5) -> torch.Tensor:
+    """cuda_layernorm_fp16: binary16 rows in and out, fp32 statistics."""
+    seq, d = _ln_args(X16, gamma, beta, torch.float16)
+    if out16 is None:
+        out16 = torch.empty_like(X16)
+    if out16.shape != X16.shape or out16.dtype != torch.float16 or not out16.is_contiguous():
+        raise ValueError(f"out16 must be a contiguous float16 {seq}x{d} tensor")
+    _check(_lib.load().vedic_layernorm_f16(X16.data_ptr(), gamma.data_ptr(), beta.data_ptr(), out16.data_ptr(), seq,
+                                           d, eps, _stream()))
+    return out16
 
 
 def gelu_(x: torch.Tensor) -> torch.Tensor:

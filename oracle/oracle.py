@@ -294,6 +294,20 @@ def gelu_f64(x) -> np.ndarray:
     return 0.5 * x * (1.0 + np.tanh(_GELU_C * (x + _GELU_A * x ** 3)))
 
 
+def layernorm_f64(X, gamma, beta, eps=1e-5) -> np.ndarray:
+    """Row layer normalisation in float64: the closed form of the reference's
+    layernorm_kernel (cuda/VedicGEMM.cu:157-193) and layernorm_fp16_kernel
+    (cuda/MixedPrecision.cuh:458-511): mean and biased variance of each row,
+    y = gamma (x - mean) / sqrt(var + eps) + beta.  Pinned in
+    tests/test_oracle.py by hand-computed rows (constant, two-valued) and by
+    the properties the definition fixes (zero mean and var / (var + eps)
+    variance of the normalised row, invariance under x -> c x + s)."""
+    X = np.asarray(X, np.float64)
+    mean = X.mean(axis=1, keepdims=True)
+    var = ((X - mean) ** 2).mean(axis=1, keepdims=True)
+    return np.asarray(gamma, np.float64) * (X - mean) / np.sqrt(var + eps) + np.asarray(beta, np.float64)
+
+
 def gelu_grad_f64(x) -> np.ndarray:
     """d/dx of gelu_f64, closed form in float64:
     0.5 (1 + tanh u) + 0.5 x sech^2(u) c (1 + 3 a x^2), u = c (x + a x^3).

@@ -365,6 +365,34 @@ static void test_residual() {
     EXPECT(same, "fp16 residual != X + A.W");
 }
 
+// Layer normalisation: a constant row gives beta exactly; a two-valued row
+// [a, b] gives gamma (+-h) / sqrt(h^2 + eps) + beta, h = (a - b) / 2; the
+// binary16 copy equals the cast of the fp32 rows.
+static void test_layernorm() {
+    const int d = 4;
+    GPUTensor X = upload({2, 2, 2, 2, 5, 1, 5, 1}, 2, d), g = upload({1, 2, 3, 4}, 1, d),
+              b = upload({0.5f, -0.5f, 1, 0}, 1, d), Y = gpu_alloc(2, d);
+    cuda_layernorm(X, g, b, Y, 2, d, 0.25f);
+    auto y = download(Y);
+    const float bb[4] = {0.5f, -0.5f, 1, 0};
+    for (int j = 0; j < d; ++j) EXPECT(y[j] == bb[j], "constant row -> beta at %d: %g", j, y[j]);
+    const double h = 2.0, s = h / std::sqrt(h * h + 0.25);
+    for (int j = 0; j < d; ++j) {
+        const double want = (j + 1) * ((j % 2) ? -s : s) + bb[j];
+        EXPECT(std::fabs(y[d + j] - want) <= 1e-6 * (std::fabs(want) + 1), "two-valued row at %d: %g vs %g", j,
+               y[d + j], want);
+    }
+    HalfTensor Y16 = half_alloc(2, d), C16 = half_alloc(2, d);
+    cuda_layernorm_fp16_copy(X.data, g.data, b.data, nullptr, Y16.data, 2, d, 0.25f);
+    cuda_cast_fp32_to_fp16(Y.data, C16.data, 2 * d);
+    std::vector<__half> a(2 * d), c(2 * d);
+    HIP_CHECK(hipMemcpy(a.data(), Y16.data, 2 * d * sizeof(__half), hipMemcpyDeviceToHost));
+    HIP_CHECK(hipMemcpy(c.data(), C16.data, 2 * d * sizeof(__half), hipMemcpyDeviceToHost));
+    bool same = true;
+    for (int i = 0; i < 2 * d; ++i) same = same && __half2float(a[i]) == __half2float(c[i]);
+    EXPECT(same, "binary16 copy != cast of the fp32 rows");
+}
+
 static void test_errors_and_verify() {
     GPUTensor A = gpu_alloc(2, 3), B = gpu_alloc(4, 2), C = gpu_alloc(2, 2);
     bool threw = false;
@@ -420,6 +448,8 @@ int main() {
         std::printf("fp16 path done\n");
         test_residual();
         std::printf("residual done\n");
+        test_layernorm();
+        std::printf("layernorm done\n");
         test_errors_and_verify();
         std::printf("errors and verify done\n");
     } catch (const std::exception& e) {

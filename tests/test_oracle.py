@@ -543,3 +543,36 @@ def test_flash_probs_stale_maximum_is_kept():
     assert np.allclose(row[64:], soft[64:], rtol=1e-5)
     assert np.allclose(row[:64], soft[:64] * np.exp(3.0), rtol=1e-5)
     assert not np.allclose(row[:64], soft[:64], rtol=1e-2)
+
+
+# ----------------------------------------------------------- layer normalisation
+
+def test_layernorm_oracle_known_rows():
+    """Rows whose normalisation is fixed by hand: a constant row gives beta
+    exactly (x - mean = 0); the row [a, b] has mean (a + b) / 2 and biased
+    variance ((a - b) / 2)^2, so y = gamma (+-h) / sqrt(h^2 + eps) + beta with
+    h = (a - b) / 2 -- an unbiased variance (ddof = 1) or a missing eps fails."""
+    g = np.array([2.0, -0.5], np.float32)
+    b = np.array([0.25, 1.0], np.float32)
+    y = o.layernorm_f64(np.array([[3.0, 3.0]]), g, b, eps=1e-5)
+    assert np.array_equal(y, b.astype(np.float64)[None, :])
+    a, c, eps = 5.0, 1.0, 0.25
+    h = (a - c) / 2.0
+    want = np.array([[2.0 * h / np.sqrt(h * h + eps) + 0.25, -0.5 * (-h) / np.sqrt(h * h + eps) + 1.0]])
+    assert np.allclose(o.layernorm_f64(np.array([[a, c]]), g, b, eps=eps), want, rtol=1e-15, atol=0)
+
+
+def test_layernorm_oracle_properties():
+    """With gamma = 1, beta = 0 each normalised row has mean 0 and variance
+    var / (var + eps); the result does not change under x -> c x + s (c > 0)
+    once eps is scaled by c^2."""
+    rng = np.random.default_rng(3)
+    X = rng.standard_normal((6, 257)) * 3.0 + 1.5
+    eps = 1e-3
+    Y = o.layernorm_f64(X, np.ones(257), np.zeros(257), eps=eps)
+    var = X.var(axis=1)
+    assert np.allclose(Y.mean(axis=1), 0.0, atol=1e-12)
+    assert np.allclose(Y.var(axis=1), var / (var + eps), rtol=1e-12)
+    c, s = 4.0, -7.0
+    Y2 = o.layernorm_f64(c * X + s, np.ones(257), np.zeros(257), eps=eps * c * c)
+    assert np.allclose(Y, Y2, rtol=0, atol=1e-12)
