@@ -1768,7 +1768,7 @@ static int flash_launch(FlashArgs& a, int dh, Workspace& wsf) {
     const int full = a.nqg * kFaQ;
     if (a.chunk >= full) return hip_status(launch_flash_attn(a, dh, s));
     // Workspace: the chunk partials.  The split items go to a grid of
-    // resident workgroups (LDS allows three per CU at DH 64, one at DH 128)
+    // resident workgroups (LDS allows three per CU at DH 64, two at DH 128)
     // that take them largest first from the stream's work-queue counter.
     const size_t bytes = sizeof(float) * (size_t)flash_slot_floats(dh) * (size_t)a.items * a.nheads;
     char* ws = nullptr;
@@ -1780,7 +1780,10 @@ static int flash_launch(FlashArgs& a, int dh, Workspace& wsf) {
         (void)wsf.put(ws);
         return hip_status(e);
     }
-    a.queue_grid = (dh == 64 ? 3 : 1) * device_cu_count();
+#ifndef VEDIC_FA_WG128
+#define VEDIC_FA_WG128 2
+#endif
+    a.queue_grid = (dh == 64 ? 3 : VEDIC_FA_WG128) * device_cu_count();
     e = launch_flash_attn(a, dh, s);
     // a launch that failed may leave the counter off zero: the next call
     // allocates and clears a new one

@@ -42,6 +42,20 @@ constexpr int fa_stage_bytes() {
     return 2 * kFaKeys * DH * 4;  // one stage: a K block, then a V block
 }
 
+// DH 128: two 32 KB stages, so two workgroups fit a CU (two waves per SIMD):
+// 8 heads x seq 8192 1360 -> 1327 us against three stages and one workgroup.
+#ifndef VEDIC_FA_ST128
+#define VEDIC_FA_ST128 2
+#endif
+#ifndef VEDIC_FA_WPE128
+#define VEDIC_FA_WPE128 2
+#endif
+// LDS stages in flight
+template <int DH>
+constexpr int fa_stages() {
+    return DH == 128 ? VEDIC_FA_ST128 : kFaStages;
+}
+
 // One work item (`item` in decreasing size order) with the workgroup's three
 // LDS stages t0, t1, t2.
 template <int DH>
@@ -52,6 +66,7 @@ __device__ __forceinline__ void fa_item(const FlashArgs& a, int item, char* t0, 
     constexpr int CPR = DH / 4;           // 16-byte chunks per row
     constexpr int HALF = DH / 2;
     static_assert(DH == 64 || DH == 128, "head dimension 64 or 128");
+    constexpr int FST = fa_stages<DH>();
     char* const stg[3] = {t0, t1, t2};
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -175,18 +190,18 @@ __device__ __forceinline__ void fa_item(const FlashArgs& a, int item, char* t0, 
     };
 
 #pragma unroll
-    for (int st = 0; st < kFaStages - 1; ++st)
+    for (int st = 0; st < FST - 1; ++st)
         fa_issue<DH, NLD>(Kh, Vh, k_lo + st * kFaKeys, st < nkb ? a.seq - k_lo - st * kFaKeys : 0, stg[st], wave, loff, lrow, lisv);
-    for (int k0 = 0; k0 < nkb; k0 += kFaStages) {
+    for (int k0 = 0; k0 < nkb; k0 += FST) {
 #pragma unroll
-        for (int st = 0; st < kFaStages; ++st) {
+        for (int st = 0; st < FST; ++st) {
             const int kb = k0 + st;
-            wait_vmcnt<(kFaStages - 2) * NLD>();
+            wait_vmcnt<(FST - 2) * NLD>();
             stage_barrier();
             {
-                const int kn = kb + kFaStages - 1;  // past the range: zeros, no memory touched
+                const int kn = kb + FST - 1;  // past the range: zeros, no memory touched
                 fa_issue<DH, NLD>(Kh, Vh, k_lo + kn * kFaKeys, kn < nkb ? a.seq - k_lo - kn * kFaKeys : 0,
-                              stg[(st + kFaStages - 1) % kFaStages], wave, loff, lrow, lisv);
+                              stg[(st + FST - 1) % FST], wave, loff, lrow, lisv);
             }
             if (kb < nkb) compute(stg[st], kb);
         }
@@ -235,14 +250,14 @@ __device__ __forceinline__ void fa_item(const FlashArgs& a, int item, char* t0, 
 // that take items from a counter until none is left: items run largest first,
 // so the tail of the key-split one-head case stays balanced.
 // DH 64: registers held to three waves per SIMD, the occupancy its 48 KB of
-// LDS allows (three workgroups per CU).
+// LDS allows (three workgroups per CU); DH 128: two (two 64 KB workgroups).
 template <int DH, bool QUEUE>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DH == 64 ? 3 : 1)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DH == 64 ? 3 : VEDIC_FA_WPE128)))
 flash_attn_kernel(FlashArgs a) {
     constexpr int SB = fa_stage_bytes<DH>();
     __shared__ __attribute__((aligned(1024))) char t0[SB];
     __shared__ __attribute__((aligned(1024))) char t1[SB];
-    __shared__ __attribute__((aligned(1024))) char t2[SB];
+    __shared__ __attribute__((aligned(1024))) char t2[fa_stages<DH>() > 2 ? SB : 16];
     __shared__ int next;
     if constexpr (!QUEUE) {
         fa_item<DH>(a, blockIdx.x, t0, t1, t2);
