@@ -92,13 +92,30 @@ __device__ __forceinline__ bool fb_masked(const A& a, int key, int query) {
 
 // ------------------------------------------------------------------ dQ pass
 
+// DH 128: two stages instead of three.  The passes stay at one wave per SIMD
+// (370-453 registers), but the small spills of the dQ pass and the dK launch
+// go away: 8 heads x seq 8192 5636 -> 5459 us.  (Two waves per SIMD would cap
+// them at 256 registers: 280-650 bytes of scratch per lane.)
+#ifndef VEDIC_FB_ST128
+#define VEDIC_FB_ST128 2
+#endif
+#ifndef VEDIC_FB_WPE128
+#define VEDIC_FB_WPE128 1
+#endif
+// LDS stages in flight of the backward passes
 template <int DH>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DH == 64 ? 2 : 1)))
+constexpr int fb_stages() {
+    return DH == 128 ? VEDIC_FB_ST128 : kFaStages;
+}
+
+template <int DH>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DH == 64 ? 2 : VEDIC_FB_WPE128)))
 flash_bwd_dq_kernel(FlashBwdArgs a) {
     constexpr int KB = 32 * DH * 4, SB = 2 * KB, NLD = SB / 1024 / 4, HALF = DH / 2;
+    constexpr int FST = fb_stages<DH>();
     __shared__ __attribute__((aligned(1024))) char t0[SB];
     __shared__ __attribute__((aligned(1024))) char t1[SB];
-    __shared__ __attribute__((aligned(1024))) char t2[SB];
+    __shared__ __attribute__((aligned(1024))) char t2[FST > 2 ? SB : 16];
     char* const stg[3] = {t0, t1, t2};
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
@@ -185,19 +202,19 @@ flash_bwd_dq_kernel(FlashBwdArgs a) {
     };
 
 #pragma unroll
-    for (int st = 0; st < kFaStages - 1; ++st)
+    for (int st = 0; st < FST - 1; ++st)
         fb_issue_two<DH, NLD>(a.k[head], a.v[head], st * 32, st < nkb ? a.seq - st * 32 : 0, stg[st], wave, loff, lrow,
                               lsec);
-    for (int k0 = 0; k0 < nkb; k0 += kFaStages) {
+    for (int k0 = 0; k0 < nkb; k0 += FST) {
 #pragma unroll
-        for (int st = 0; st < kFaStages; ++st) {
+        for (int st = 0; st < FST; ++st) {
             const int kb = k0 + st;
-            wait_vmcnt<(kFaStages - 2) * NLD>();
+            wait_vmcnt<(FST - 2) * NLD>();
             stage_barrier();
             {
-                const int kn = kb + kFaStages - 1;
+                const int kn = kb + FST - 1;
                 fb_issue_two<DH, NLD>(a.k[head], a.v[head], kn * 32, kn < nkb ? a.seq - kn * 32 : 0,
-                                      stg[(st + kFaStages - 1) % kFaStages], wave, loff, lrow, lsec);
+                                      stg[(st + FST - 1) % FST], wave, loff, lrow, lsec);
             }
             if (kb < nkb) compute(stg[st], kb);
         }
@@ -223,14 +240,15 @@ flash_bwd_dq_kernel(FlashBwdArgs a) {
 // launches: PART 1 dV only (no V, no dP), PART 2 dK only; the second
 // recomputes S (five products per block instead of four) but nothing spills.
 template <int DH, int PART = 0>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DH == 64 ? 1 : VEDIC_FB_WPE128)))
 flash_bwd_dkdv_kernel(FlashBwdArgs a) {
     constexpr int KB = 32 * DH * 4, NLD = 2 * KB / 1024 / 4, HALF = DH / 2;
     constexpr bool DO_DV = PART != 2, DO_DK = PART != 1;
     constexpr int SB = 2 * KB + 1024;  // Q block, dO block, then (lse2, D) of the 32 queries
+    constexpr int FST = fb_stages<DH>();
     __shared__ __attribute__((aligned(1024))) char t0[SB];
     __shared__ __attribute__((aligned(1024))) char t1[SB];
-    __shared__ __attribute__((aligned(1024))) char t2[SB];
+    __shared__ __attribute__((aligned(1024))) char t2[FST > 2 ? SB : 16];
     char* const stg[3] = {t0, t1, t2};
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
@@ -341,14 +359,14 @@ flash_bwd_dkdv_kernel(FlashBwdArgs a) {
                        8 * wave + (lane >> 1) < rows_ ? soff : kOob);                                           \
     } while (0)
 #pragma unroll
-    for (int st = 0; st < kFaStages - 1; ++st) VEDIC_FB_ISSUE(st, stg[st]);
-    for (int b0 = 0; b0 < nqb; b0 += kFaStages) {
+    for (int st = 0; st < FST - 1; ++st) VEDIC_FB_ISSUE(st, stg[st]);
+    for (int b0 = 0; b0 < nqb; b0 += FST) {
 #pragma unroll
-        for (int st = 0; st < kFaStages; ++st) {
+        for (int st = 0; st < FST; ++st) {
             const int qb = b0 + st;
-            wait_vmcnt<(kFaStages - 2) * (NLD + 1)>();
+            wait_vmcnt<(FST - 2) * (NLD + 1)>();
             stage_barrier();
-            VEDIC_FB_ISSUE(qb + kFaStages - 1, stg[(st + kFaStages - 1) % kFaStages]);
+            VEDIC_FB_ISSUE(qb + FST - 1, stg[(st + FST - 1) % FST]);
             if (qb < nqb) compute(stg[st], qb);
         }
     }
