@@ -761,7 +761,8 @@ def run_layernorm(args, torch, dev):
     ms2, _ = time_steps(two_pass, args.steps, args.warmup, torch)
     nbytes = seq * d * (4 + 4 + 2)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"workload": LN_WORKLOAD, "ms_per_step": round(ms, 5), "GB/s": round(gbs, 1),
+    return {"workload": LN_WORKLOAD, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+            "value": round(gbs, 1), "unit": "GB/s", "GB/s": round(gbs, 1),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s",
                          "frac": round(gbs / 8000.0, 4)},
             "two_pass_ms": round(ms2, 5), "bytes_per_step": nbytes}
