@@ -12,12 +12,14 @@
 // the bits the cast kernel would give), so an fp16 GEMM consumes the
 // normalised activation with no cast pass of its own.
 //
-// One workgroup of 256 threads (four waves) per row.  A thread keeps its
-// values of the row in registers between the passes when the row fits
-// (d <= kLnHeld * 256); longer rows are read again (from cache).  fp32 rows
-// with d a multiple of 4 and aligned bases go four values per access.  Sums
-// are reduced in a fixed order (per thread, then across the 64 lanes of a
-// wave, then the four waves in order), so results do not depend on timing.
+// fp32 rows with d a multiple of 4, aligned bases and d <= 4096 go one wave
+// per row (four rows per workgroup), up to sixteen 16-byte loads in flight per
+// lane and the sums reduced across the wave alone.  Other rows take one
+// workgroup of 256 threads (four waves) per row: a thread keeps its values of
+// the row in registers between the passes when the row fits (d <= kLnHeld *
+// 256); longer rows are read again (from cache).  Sums are reduced in a fixed
+// order (per thread, then across the 64 lanes of a wave by a fixed xor
+// pattern, then the four waves in order), so results do not depend on timing.
 #include <hip/hip_runtime.h>
 
 #include "vedic_common.hpp"
@@ -28,6 +30,7 @@ namespace {
 
 constexpr int kLnThreads = 256;
 constexpr int kLnHeld = 16;  // values per thread kept in registers
+constexpr int kLnWaveMax = 4096;  // aligned fp32 rows up to this length: one wave per row
 
 // Sum over the workgroup: lanes by xor-shuffle (fixed pattern), then the four
 // wave sums in wave order; every thread gets the total.
@@ -102,35 +105,42 @@ __global__ void __launch_bounds__(kLnThreads)
     }
 }
 
-// fp32 rows with d a multiple of 4 and 16-byte aligned rows, d <= 4096: four
-// consecutive values per thread and access (16-byte loads and stores, 8-byte
-// binary16 stores).
-template <bool OUT32, bool OUT16>
+// Sum over one wave's 64 lanes (fixed xor pattern); every lane gets the total.
+__device__ __forceinline__ float ln_wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// fp32 rows with d a multiple of 4, d <= 256 * H4, aligned: one wave per row,
+// four rows per workgroup, H4 float4 per lane (H4 loads in flight per lane),
+// the sums reduced across the wave with no barrier.  The outputs are written
+// with non-temporal stores (nothing reads them back in this kernel): 11.6 us
+// instead of 13.5 us for 8192 x 1024 with the binary16 copy.
+template <int H4, bool OUT32, bool OUT16>
 __global__ void __launch_bounds__(kLnThreads)
-    layernorm_rows4_kernel(const float* __restrict__ X, const float* __restrict__ gamma,
-                           const float* __restrict__ beta, float* __restrict__ Y, _Float16* __restrict__ Y16, int d,
-                           float eps) {
+    layernorm_wave_rows_kernel(const float* __restrict__ X, const float* __restrict__ gamma,
+                               const float* __restrict__ beta, float* __restrict__ Y, _Float16* __restrict__ Y16,
+                               int seq, int d, float eps) {
     typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-    constexpr int H4 = kLnHeld / 4;  // float4 per thread
-    __shared__ float red[4];
-    const int64_t row = blockIdx.x;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= seq) return;  // whole waves leave; no barrier below
+    const int lane = threadIdx.x & 63, d4 = d / 4;
     const float4_t* x = reinterpret_cast<const float4_t*>(X + row * d);
-    const int tid = threadIdx.x, d4 = d / 4;
     float4_t v[H4];
-    float s = 0.0f;
 #pragma unroll
     for (int k = 0; k < H4; ++k) {
-        const int j = tid + k * kLnThreads;
+        const int j = lane + k * 64;
         v[k] = j < d4 ? x[j] : float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
+    float s = 0.0f;
 #pragma unroll
     for (int k = 0; k < H4; ++k) s += ((v[k][0] + v[k][1]) + v[k][2]) + v[k][3];
-    const float mean = ln_block_sum(s, red) / (float)d;
+    const float mean = ln_wave_sum(s) / (float)d;
     float q = 0.0f;
 #pragma unroll
     for (int k = 0; k < H4; ++k) {
-        const int j = tid + k * kLnThreads;
-        if (j < d4) {
+        if (lane + k * 64 < d4) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float df = v[k][e] - mean;
@@ -138,26 +148,41 @@ __global__ void __launch_bounds__(kLnThreads)
             }
         }
     }
-    const float inv = 1.0f / __builtin_sqrtf(ln_block_sum(q, red) / (float)d + eps);
+    const float inv = 1.0f / __builtin_sqrtf(ln_wave_sum(q) / (float)d + eps);
     const float4_t* g4 = reinterpret_cast<const float4_t*>(gamma);
     const float4_t* b4 = reinterpret_cast<const float4_t*>(beta);
 #pragma unroll
     for (int k = 0; k < H4; ++k) {
-        const int j = tid + k * kLnThreads;
+        const int j = lane + k * 64;
         if (j < d4) {
             const float4_t gv = g4[j], bv = b4[j];
             float4_t y;
 #pragma unroll
             for (int e = 0; e < 4; ++e) y[e] = gv[e] * (v[k][e] - mean) * inv + bv[e];
-            if constexpr (OUT32) reinterpret_cast<float4_t*>(Y + row * d)[j] = y;
+            if constexpr (OUT32) __builtin_nontemporal_store(y, reinterpret_cast<float4_t*>(Y + row * d) + j);
             if constexpr (OUT16) {
                 half4_t h;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) h[e] = to_half_clamped(y[e]);
-                reinterpret_cast<half4_t*>(Y16 + row * d)[j] = h;
+                __builtin_nontemporal_store(h, reinterpret_cast<half4_t*>(Y16 + row * d) + j);
             }
         }
     }
+}
+
+template <int H4>
+void launch_wave_rows(const float* X, const float* gamma, const float* beta, float* Y, _Float16* y16, int seq, int d,
+                      float eps, hipStream_t s) {
+    const dim3 grid((unsigned)((seq + 3) / 4)), block(kLnThreads);
+    if (Y && y16)
+        hipLaunchKernelGGL((layernorm_wave_rows_kernel<H4, true, true>), grid, block, 0, s, X, gamma, beta, Y, y16,
+                           seq, d, eps);
+    else if (Y)
+        hipLaunchKernelGGL((layernorm_wave_rows_kernel<H4, true, false>), grid, block, 0, s, X, gamma, beta, Y, y16,
+                           seq, d, eps);
+    else
+        hipLaunchKernelGGL((layernorm_wave_rows_kernel<H4, false, true>), grid, block, 0, s, X, gamma, beta, Y, y16,
+                           seq, d, eps);
 }
 
 }  // namespace
@@ -165,20 +190,18 @@ __global__ void __launch_bounds__(kLnThreads)
 hipError_t launch_layernorm_f32(const float* X, const float* gamma, const float* beta, float* Y, void* Y16, int seq,
                                 int d, float eps, hipStream_t s) {
     _Float16* y16 = static_cast<_Float16*>(Y16);
-    const dim3 grid((unsigned)seq), block(kLnThreads);
     const uintptr_t al = reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(gamma) |
                          reinterpret_cast<uintptr_t>(beta) | reinterpret_cast<uintptr_t>(Y);
-    if (d % 4 == 0 && d <= kLnHeld * kLnThreads && (al & 15) == 0 && (reinterpret_cast<uintptr_t>(Y16) & 7) == 0) {
-        if (Y && y16)
-            hipLaunchKernelGGL((layernorm_rows4_kernel<true, true>), grid, block, 0, s, X, gamma, beta, Y, y16, d, eps);
-        else if (Y)
-            hipLaunchKernelGGL((layernorm_rows4_kernel<true, false>), grid, block, 0, s, X, gamma, beta, Y, y16, d,
-                               eps);
+    if (d % 4 == 0 && d <= kLnWaveMax && (al & 15) == 0 && (reinterpret_cast<uintptr_t>(Y16) & 7) == 0) {
+        if (d <= 1024)
+            launch_wave_rows<4>(X, gamma, beta, Y, y16, seq, d, eps, s);
+        else if (d <= 2048)
+            launch_wave_rows<8>(X, gamma, beta, Y, y16, seq, d, eps, s);
         else
-            hipLaunchKernelGGL((layernorm_rows4_kernel<false, true>), grid, block, 0, s, X, gamma, beta, Y, y16, d,
-                               eps);
+            launch_wave_rows<16>(X, gamma, beta, Y, y16, seq, d, eps, s);
         return hipGetLastError();
     }
+    const dim3 grid((unsigned)seq), block(kLnThreads);
     if (Y && y16)
         hipLaunchKernelGGL((layernorm_rows_kernel<float, true, true>), grid, block, 0, s, X, gamma, beta, Y, y16, d,
                            eps);

@@ -11,8 +11,11 @@ Checks:
     (the same clamp and rounding), alone or beside the fp32 output;
   - binary16 in and out: within one binary16 unit of the float64 result on
     the rounded inputs;
-  - rows held in registers (d <= 4096) and rows read again (d > 4096),
-    ragged d, one-element rows, constant rows (variance 0: y = beta);
+  - one wave per row (d <= 4096, multiples of 4; row counts not a multiple
+    of the four rows per workgroup), a workgroup per row with the row held in
+    registers (d <= 4096, d not a multiple of 4) or read again (d > 4096),
+    ragged d, one-element rows, constant rows
+    (variance 0: y = beta);
   - repeatability, and an fp16 GEMM on the binary16 copy equals the fp16 GEMM
     on the cast of the fp32 rows and the AMP GEMM on the fp32 rows.
 """
@@ -33,7 +36,8 @@ def V():
     return vedic
 
 
-SHAPES = [(8192, 1024), (1, 1), (3, 7), (300, 64), (33, 4097), (7, 5000), (64, 4096), (5, 12288)]
+SHAPES = [(8192, 1024), (1, 1), (3, 7), (300, 64), (10, 1500), (257, 2048), (6, 1028), (9, 3000), (33, 4097), (7, 5000),
+          (64, 4096), (5, 12288)]
 
 
 def _inputs(rng, seq, d):
@@ -128,3 +132,22 @@ def test_layernorm_rejections():
         vedic.layernorm(x, g, g, fp32=False, fp16=False)
     with pytest.raises(ValueError):
         vedic.layernorm_fp16(x, g, g)  # binary16 input expected
+
+
+@pytest.mark.parametrize("d", [1024, 3000])
+def test_layernorm_rows_off_16_byte_alignment(d):
+    """Rows whose base is 4 bytes off 16-byte alignment take the workgroup-per-
+    row kernel; the result stays within the same bound and the binary16 copy
+    is still the cast of the fp32 rows."""
+    vedic = V()
+    rng = np.random.default_rng(d)
+    seq = 37
+    X, g, b = _inputs(rng, seq, d)
+    flat = torch.empty(seq * d + 1, device="cuda")
+    x = flat[1:].view(seq, d)
+    x.copy_(dev(X))
+    assert x.data_ptr() % 16 == 4
+    Y, Y16 = vedic.layernorm(x, dev(g), dev(b), fp16=True)
+    want = o.layernorm_f64(X, g, b, 1e-5)
+    assert np.all(np.abs(host(Y) - want) <= _bound(X, g, b, 1e-5))
+    assert torch.equal(Y16, vedic.cast_fp32_to_fp16(Y))
