@@ -115,8 +115,9 @@ __device__ __forceinline__ float ln_wave_sum(float v) {
 // fp32 rows with d a multiple of 4, d <= 256 * H4, aligned: one wave per row,
 // four rows per workgroup, H4 float4 per lane (H4 loads in flight per lane),
 // the sums reduced across the wave with no barrier.  The outputs are written
-// with non-temporal stores (nothing reads them back in this kernel): 11.6 us
-// instead of 13.5 us for 8192 x 1024 with the binary16 copy.
+// with ordinary stores: non-temporal ones make this kernel faster alone (11.5
+// against 13.5 us at 8192 x 1024) but the GEMM that reads the binary16 copy
+// next slower by more (2-4 us), as its operand no longer comes from cache.
 template <int H4, bool OUT32, bool OUT16>
 __global__ void __launch_bounds__(kLnThreads)
     layernorm_wave_rows_kernel(const float* __restrict__ X, const float* __restrict__ gamma,
@@ -159,12 +160,12 @@ __global__ void __launch_bounds__(kLnThreads)
             float4_t y;
 #pragma unroll
             for (int e = 0; e < 4; ++e) y[e] = gv[e] * (v[k][e] - mean) * inv + bv[e];
-            if constexpr (OUT32) __builtin_nontemporal_store(y, reinterpret_cast<float4_t*>(Y + row * d) + j);
+            if constexpr (OUT32) reinterpret_cast<float4_t*>(Y + row * d)[j] = y;
             if constexpr (OUT16) {
                 half4_t h;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) h[e] = to_half_clamped(y[e]);
-                __builtin_nontemporal_store(h, reinterpret_cast<half4_t*>(Y16 + row * d) + j);
+                reinterpret_cast<half4_t*>(Y16 + row * d)[j] = h;
             }
         }
     }
