@@ -174,7 +174,7 @@ __global__ void __launch_bounds__(kLnThreads)
 template <int H4>
 void launch_wave_rows(const float* X, const float* gamma, const float* beta, float* Y, _Float16* y16, int seq, int d,
                       float eps, hipStream_t s) {
-    const dim3 grid((unsigned)((seq + 3) / 4)), block(kLnThreads);
+    const dim3 grid((unsigned)(((int64_t)seq + 3) / 4)), block(kLnThreads);
     if (Y && y16)
         hipLaunchKernelGGL((layernorm_wave_rows_kernel<H4, true, true>), grid, block, 0, s, X, gamma, beta, Y, y16,
                            seq, d, eps);
