@@ -12,9 +12,10 @@
 // the bits the cast kernel would give), so an fp16 GEMM consumes the
 // normalised activation with no cast pass of its own.
 //
-// fp32 rows with d a multiple of 4, aligned bases and d <= 4096 go one wave
-// per row (four rows per workgroup), up to sixteen 16-byte loads in flight per
-// lane and the sums reduced across the wave alone.  Other rows take one
+// Rows with d a multiple of 4, aligned bases and d <= 4096 (fp32 or binary16
+// input) go one wave per row (four rows per workgroup), up to sixteen loads
+// of four values in flight per lane and the sums reduced across the wave
+// alone.  Other rows take one
 // workgroup of 256 threads (four waves) per row: a thread keeps its values of
 // the row in registers between the passes when the row fits (d <= kLnHeld *
 // 256); longer rows are read again (from cache).  Sums are reduced in a fixed
@@ -30,7 +31,7 @@ namespace {
 
 constexpr int kLnThreads = 256;
 constexpr int kLnHeld = 16;  // values per thread kept in registers
-constexpr int kLnWaveMax = 4096;  // aligned fp32 rows up to this length: one wave per row
+constexpr int kLnWaveMax = 4096;  // aligned rows up to this length: one wave per row
 
 // Sum over the workgroup: lanes by xor-shuffle (fixed pattern), then the four
 // wave sums in wave order; every thread gets the total.
@@ -112,27 +113,47 @@ __device__ __forceinline__ float ln_wave_sum(float v) {
     return v;
 }
 
-// fp32 rows with d a multiple of 4, d <= 256 * H4, aligned: one wave per row,
-// four rows per workgroup, H4 float4 per lane (H4 loads in flight per lane),
-// the sums reduced across the wave with no barrier.  The outputs are written
+template <typename TIn>
+struct Vec4;
+template <>
+struct Vec4<float> {
+    typedef float4_t type;  // 16-byte loads
+};
+template <>
+struct Vec4<_Float16> {
+    typedef _Float16 type __attribute__((ext_vector_type(4)));  // 8-byte loads
+};
+
+// Rows (fp32 or binary16) with d a multiple of 4, d <= 256 * H4, aligned: one
+// wave per row, four rows per workgroup, H4 groups of four values per lane (H4
+// loads in flight per lane), the sums reduced across the wave with no
+// barrier, the statistics and outputs in fp32 as in the workgroup-per-row
+// kernel.  The outputs are written
 // with ordinary stores: non-temporal ones make this kernel faster alone (11.5
 // against 13.5 us at 8192 x 1024) but the GEMM that reads the binary16 copy
 // next slower by more (2-4 us), as its operand no longer comes from cache.
-template <int H4, bool OUT32, bool OUT16>
+template <int H4, typename TIn, bool OUT32, bool OUT16>
 __global__ void __launch_bounds__(kLnThreads)
-    layernorm_wave_rows_kernel(const float* __restrict__ X, const float* __restrict__ gamma,
+    layernorm_wave_rows_kernel(const TIn* __restrict__ X, const float* __restrict__ gamma,
                                const float* __restrict__ beta, float* __restrict__ Y, _Float16* __restrict__ Y16,
                                int seq, int d, float eps) {
     typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= seq) return;  // whole waves leave; no barrier below
     const int lane = threadIdx.x & 63, d4 = d / 4;
-    const float4_t* x = reinterpret_cast<const float4_t*>(X + row * d);
+    typedef typename Vec4<TIn>::type in4_t;
+    const in4_t* x = reinterpret_cast<const in4_t*>(X + row * d);
     float4_t v[H4];
 #pragma unroll
     for (int k = 0; k < H4; ++k) {
         const int j = lane + k * 64;
-        v[k] = j < d4 ? x[j] : float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        if (j < d4) {
+            const in4_t t = x[j];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[k][e] = (float)t[e];
+        } else {
+            v[k] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
     }
     float s = 0.0f;
 #pragma unroll
@@ -171,19 +192,40 @@ __global__ void __launch_bounds__(kLnThreads)
     }
 }
 
-template <int H4>
-void launch_wave_rows(const float* X, const float* gamma, const float* beta, float* Y, _Float16* y16, int seq, int d,
+template <int H4, typename TIn>
+void launch_wave_rows(const TIn* X, const float* gamma, const float* beta, float* Y, _Float16* y16, int seq, int d,
                       float eps, hipStream_t s) {
     const dim3 grid((unsigned)(((int64_t)seq + 3) / 4)), block(kLnThreads);
     if (Y && y16)
-        hipLaunchKernelGGL((layernorm_wave_rows_kernel<H4, true, true>), grid, block, 0, s, X, gamma, beta, Y, y16,
-                           seq, d, eps);
+        hipLaunchKernelGGL((layernorm_wave_rows_kernel<H4, TIn, true, true>), grid, block, 0, s, X, gamma, beta, Y,
+                           y16, seq, d, eps);
     else if (Y)
-        hipLaunchKernelGGL((layernorm_wave_rows_kernel<H4, true, false>), grid, block, 0, s, X, gamma, beta, Y, y16,
-                           seq, d, eps);
+        hipLaunchKernelGGL((layernorm_wave_rows_kernel<H4, TIn, true, false>), grid, block, 0, s, X, gamma, beta, Y,
+                           y16, seq, d, eps);
     else
-        hipLaunchKernelGGL((layernorm_wave_rows_kernel<H4, false, true>), grid, block, 0, s, X, gamma, beta, Y, y16,
-                           seq, d, eps);
+        hipLaunchKernelGGL((layernorm_wave_rows_kernel<H4, TIn, false, true>), grid, block, 0, s, X, gamma, beta, Y,
+                           y16, seq, d, eps);
+}
+
+// One wave per row when d is a multiple of 4 up to kLnWaveMax and the bases
+// allow the vector accesses (X: four values; gamma, beta, Y: 16 bytes; Y16:
+// 8 bytes); false otherwise.
+template <typename TIn>
+bool try_wave_rows(const TIn* X, const float* gamma, const float* beta, float* Y, _Float16* y16, int seq, int d,
+                   float eps, hipStream_t s) {
+    const uintptr_t al16 = reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta) |
+                           reinterpret_cast<uintptr_t>(Y);
+    const uintptr_t x = reinterpret_cast<uintptr_t>(X);
+    if (d % 4 != 0 || d > kLnWaveMax || (al16 & 15) != 0 || (x & (4 * sizeof(TIn) - 1)) != 0 ||
+        (reinterpret_cast<uintptr_t>(y16) & 7) != 0)
+        return false;
+    if (d <= 1024)
+        launch_wave_rows<4>(X, gamma, beta, Y, y16, seq, d, eps, s);
+    else if (d <= 2048)
+        launch_wave_rows<8>(X, gamma, beta, Y, y16, seq, d, eps, s);
+    else
+        launch_wave_rows<16>(X, gamma, beta, Y, y16, seq, d, eps, s);
+    return true;
 }
 
 }  // namespace
@@ -191,17 +233,7 @@ void launch_wave_rows(const float* X, const float* gamma, const float* beta, flo
 hipError_t launch_layernorm_f32(const float* X, const float* gamma, const float* beta, float* Y, void* Y16, int seq,
                                 int d, float eps, hipStream_t s) {
     _Float16* y16 = static_cast<_Float16*>(Y16);
-    const uintptr_t al = reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(gamma) |
-                         reinterpret_cast<uintptr_t>(beta) | reinterpret_cast<uintptr_t>(Y);
-    if (d % 4 == 0 && d <= kLnWaveMax && (al & 15) == 0 && (reinterpret_cast<uintptr_t>(Y16) & 7) == 0) {
-        if (d <= 1024)
-            launch_wave_rows<4>(X, gamma, beta, Y, y16, seq, d, eps, s);
-        else if (d <= 2048)
-            launch_wave_rows<8>(X, gamma, beta, Y, y16, seq, d, eps, s);
-        else
-            launch_wave_rows<16>(X, gamma, beta, Y, y16, seq, d, eps, s);
-        return hipGetLastError();
-    }
+    if (try_wave_rows(X, gamma, beta, Y, y16, seq, d, eps, s)) return hipGetLastError();
     const dim3 grid((unsigned)seq), block(kLnThreads);
     if (Y && y16)
         hipLaunchKernelGGL((layernorm_rows_kernel<float, true, true>), grid, block, 0, s, X, gamma, beta, Y, y16, d,
@@ -217,8 +249,11 @@ hipError_t launch_layernorm_f32(const float* X, const float* gamma, const float*
 
 hipError_t launch_layernorm_f16(const void* X16, const float* gamma, const float* beta, void* Y16, int seq, int d,
                                 float eps, hipStream_t s) {
+    const _Float16* x16 = static_cast<const _Float16*>(X16);
+    _Float16* y16 = static_cast<_Float16*>(Y16);
+    if (try_wave_rows(x16, gamma, beta, nullptr, y16, seq, d, eps, s)) return hipGetLastError();
     hipLaunchKernelGGL((layernorm_rows_kernel<_Float16, false, true>), dim3((unsigned)seq), dim3(kLnThreads), 0, s,
-                       static_cast<const _Float16*>(X16), gamma, beta, nullptr, static_cast<_Float16*>(Y16), d, eps);
+                       x16, gamma, beta, nullptr, y16, d, eps);
     return hipGetLastError();
 }
 

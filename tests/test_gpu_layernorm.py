@@ -10,7 +10,8 @@ Checks:
   - the binary16 copy equals, bit for bit, the library's cast of the fp32 rows
     (the same clamp and rounding), alone or beside the fp32 output;
   - binary16 in and out: within one binary16 unit of the float64 result on
-    the rounded inputs;
+    the rounded inputs (one wave per row for d a multiple of 4 up to 4096, a
+    workgroup per row otherwise);
   - one wave per row (d <= 4096, multiples of 4; row counts not a multiple
     of the four rows per workgroup), a workgroup per row with the row held in
     registers (d <= 4096, d not a multiple of 4) or read again (d > 4096),
@@ -91,7 +92,7 @@ def test_layernorm_constant_rows_and_eps():
         assert np.all(np.abs(y - want) <= _bound(X, g, b, eps)), f"eps {eps}"
 
 
-@pytest.mark.parametrize("seq,d", [(8192, 1024), (300, 520), (9, 4100), (1, 3)], ids=lambda x: str(x))
+@pytest.mark.parametrize("seq,d", [(8192, 1024), (300, 520), (7, 3000), (9, 4100), (1, 3), (5, 6)], ids=lambda x: str(x))
 def test_layernorm_fp16_in_and_out(seq, d):
     vedic = V()
     rng = np.random.default_rng(d + 5 * seq)
@@ -151,3 +152,20 @@ def test_layernorm_rows_off_16_byte_alignment(d):
     want = o.layernorm_f64(X, g, b, 1e-5)
     assert np.all(np.abs(host(Y) - want) <= _bound(X, g, b, 1e-5))
     assert torch.equal(Y16, vedic.cast_fp32_to_fp16(Y))
+
+
+def test_layernorm_fp16_rows_off_8_byte_alignment():
+    """binary16 rows whose base is 2 bytes off 8-byte alignment take the
+    workgroup-per-row kernel and stay within the binary16 bound."""
+    vedic = V()
+    rng = np.random.default_rng(77)
+    seq, d = 21, 1024
+    X, g, b = _inputs(rng, seq, d)
+    flat = torch.empty(seq * d + 1, dtype=torch.float16, device="cuda")
+    x16 = flat[1:].view(seq, d)
+    x16.copy_(vedic.cast_fp32_to_fp16(dev(X)))
+    assert x16.data_ptr() % 8 == 2
+    got = host(vedic.layernorm_fp16(x16, dev(g), dev(b)))
+    want = o.layernorm_f64(o.f16_round(X), g, b, 1e-5)
+    ulp16 = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(got - want) <= ulp16 + _bound(o.f16_round(X), g, b, 1e-5))
