@@ -288,13 +288,21 @@ int vedic_add_bias(float* C, const float* bias, int M, int N, void* stream);
  * +-65504 and rounded to nearest even -- the bits vedic_cast_f32_to_f16(Y)
  * would give -- in the same pass, so an fp16 GEMM takes the normalised
  * activation without the per-call cast of the reference's amp_gemm
- * (cuda/ModelGPU.cu:825-827).  New: the reference writes fp32 only. */
+ * (cuda/ModelGPU.cu:825-827).  New: the reference writes fp32 only.
+ * The summation order is fixed for a given d and operand alignment (rows with
+ * d a multiple of 4 up to 4096 and 16-byte aligned X, gamma, beta, Y and
+ * 8-byte aligned Y16 are reduced one wave per row, others one workgroup per
+ * row), so repeated calls give the same bits; the same rows at another
+ * alignment may differ in the last bits. */
 int vedic_layernorm(const float* X, const float* gamma, const float* beta, float* Y, void* Y16, int seq, int d,
                     float eps, void* stream);
 
 /* The same on binary16 rows, binary16 out (fp32 statistics; the output
  * clamped to +-65504 before rounding).  Replaces cuda_layernorm_fp16
- * (cuda/VedicGEMM.cuh:253, cuda/MixedPrecision.cuh:458-511). */
+ * (cuda/VedicGEMM.cuh:253, cuda/MixedPrecision.cuh:458-511).  One wave per
+ * row when d is a multiple of 4 up to 4096 and X16 and Y16 are 8-byte
+ * aligned (gamma and beta 16-byte), one workgroup per row otherwise; as
+ * above, the bits are repeatable for a given alignment. */
 int vedic_layernorm_f16(const void* X16, const float* gamma, const float* beta, void* Y16, int seq, int d, float eps,
                         void* stream);
 
