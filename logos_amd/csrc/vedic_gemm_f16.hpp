@@ -67,10 +67,17 @@ __device__ __forceinline__ int swz_kc(int r) {
 // MC slot swizzle.  Rows of 16 or more slots (BM / BN >= 128): slots XOR
 // 4 (k mod 4).  Rows of 4 slots (32 columns, 64 bytes) need none: the four
 // k rows a 16-lane transpose read touches already fill a 256-byte bank window.
+//
+// Rows of 24 slots (192 columns, 384 bytes) alternate between the two halves
+// of the 256-byte bank window by themselves (row k starts at 128 (k mod 2)
+// bytes into it); XOR 4 (bit 1 of k) moves rows 2 and 3 of every four by 64
+// bytes, so the four k rows of a transpose read again cover the window once.
+// (XOR 4 flips bit 2 of the slot index, which keeps it below 24.)
 template <int R>
 __device__ __forceinline__ int swz_mc(int k) {
-    static_assert(R == 32 || R >= 128, "MC layouts of 32 or >= 128 columns");
-    return R >= 128 ? 4 * (k & 3) : 0;
+    static_assert(R == 32 || R == 192 || (R >= 128 && (R & (R - 1)) == 0), "MC layouts of 32, 192 or 2^n >= 128 columns");
+    if constexpr (R == 192) return 4 * ((k >> 1) & 1);
+    else return R >= 128 ? 4 * (k & 3) : 0;
 }
 
 // vmcnt(N), expcnt and lgkmcnt left at their maxima (gfx9 encoding).
@@ -658,6 +665,10 @@ struct CfgSmallK {
 #ifndef VEDIC_F16_MID_ST
 #define VEDIC_F16_MID_ST 3
 #endif
+struct CfgWide {  // 256 x 192, eight waves of 64 x 96 (3072-column products: whole rounds of tiles)
+    static constexpr int BM = 256, BN = 192, BK = 64, ST = 2, WGM = 4, WGN = 2, WGK = 1;
+    static constexpr int PER_CU = 1;
+};
 struct CfgMid {  // 256 x 128, eight waves of 64 x 64
     static constexpr int BM = 256, BN = 128, BK = 64, ST = VEDIC_F16_MID_ST, WGM = 4, WGN = 2, WGK = 1;
     static constexpr int PER_CU = 1;
@@ -712,26 +723,44 @@ int device_cu_count();
 #ifndef VEDIC_F16_COLUMN_SPLIT
 #define VEDIC_F16_COLUMN_SPLIT 1
 #endif
+#ifndef VEDIC_F16_WIDE_EFF
+#define VEDIC_F16_WIDE_EFF 100
+#endif
+
+// The tile configurations the cost model chooses among: tile shape,
+// workgroups per CU and relative efficiency (percent, measured).
+// 0: 256 x 256, 1: 256 x 128, 2: 128 x 128, 3: 256 x 192.
+struct F16TileCost {
+    int bm, bn, per_cu, eff;
+};
+constexpr int kF16Configs = 4;
+constexpr F16TileCost kF16Cost[kF16Configs] = {{256, 256, 1, 100},
+                                               {256, 128, 1, VEDIC_F16_MID_EFF},
+                                               {128, 128, VEDIC_F16_SMALL_PER_CU, VEDIC_F16_SMALL_EFF},
+                                               {256, 192, 1, VEDIC_F16_WIDE_EFF}};
+
+// Estimated time of configuration c: rounds of resident tiles x the work one
+// CU does per round / the configuration's relative efficiency.
+inline double f16_tile_estimate(int M, int N, int cus, int c) {
+    const F16TileCost& t = kF16Cost[c];
+    const int64_t tiles = (int64_t)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+    const int64_t slots = (int64_t)cus * t.per_cu;
+    const int64_t rounds = (tiles + slots - 1) / slots;
+    // a round's per-CU work: min(per_cu, tiles resident per CU) tiles
+    const int64_t per_cu = tiles < slots ? (tiles + cus - 1) / cus : t.per_cu;
+    return (double)rounds * per_cu * t.bm * t.bn * 100.0 / t.eff;
+}
 
 // Tile configuration for an M x N product on `cus` CUs: the one with the
-// least estimated time, rounds of resident tiles x the work one CU does per
-// round / the configuration's relative efficiency (in percent, measured).
-// 0: 256 x 256, 1: 256 x 128, 2: 128 x 128.
+// least estimated time (the first of equal ones).
 inline int f16_tile_config(int M, int N, int cus) {
-    struct C { int bm, bn, per_cu, eff; };
-    const C cfgs[3] = {{256, 256, 1, 100}, {256, 128, 1, VEDIC_F16_MID_EFF}, {128, 128, VEDIC_F16_SMALL_PER_CU, VEDIC_F16_SMALL_EFF}};
     int best = 0;
-    double best_t = 0.0;
-    for (int i = 0; i < 3; ++i) {
-        const int64_t tiles = (int64_t)((M + cfgs[i].bm - 1) / cfgs[i].bm) * ((N + cfgs[i].bn - 1) / cfgs[i].bn);
-        const int64_t slots = (int64_t)cus * cfgs[i].per_cu;
-        const int64_t rounds = (tiles + slots - 1) / slots;
-        // a round's per-CU work: min(per_cu, tiles resident per CU) tiles
-        const int64_t per_cu = tiles < slots ? (tiles + cus - 1) / cus : cfgs[i].per_cu;
-        const double t_est = (double)rounds * per_cu * cfgs[i].bm * cfgs[i].bn * 100.0 / cfgs[i].eff;
-        if (i == 0 || t_est < best_t) {
+    double best_t = f16_tile_estimate(M, N, cus, 0);
+    for (int i = 1; i < kF16Configs; ++i) {
+        const double t = f16_tile_estimate(M, N, cus, i);
+        if (t < best_t) {
             best = i;
-            best_t = t_est;
+            best_t = t;
         }
     }
     return best;
@@ -787,17 +816,7 @@ inline int f16_column_split(int M, int N, int cus) {
     if (mid_tiles > cus) return 0;
     const double t_split = (double)(n1 / cols_round) * 256 * 256 + 256.0 * 128 * 100.0 / VEDIC_F16_MID_EFF;
     // the best single configuration's estimate
-    struct C { int bm, bn, per_cu, eff; };
-    const C cfgs[3] = {{256, 256, 1, 100}, {256, 128, 1, VEDIC_F16_MID_EFF}, {128, 128, VEDIC_F16_SMALL_PER_CU, VEDIC_F16_SMALL_EFF}};
-    double best = 0.0;
-    for (int i = 0; i < 3; ++i) {
-        const int64_t tiles = (int64_t)((M + cfgs[i].bm - 1) / cfgs[i].bm) * ((N + cfgs[i].bn - 1) / cfgs[i].bn);
-        const int64_t slots = (int64_t)cus * cfgs[i].per_cu;
-        const int64_t rounds = (tiles + slots - 1) / slots;
-        const int64_t per_cu = tiles < slots ? (tiles + cus - 1) / cus : cfgs[i].per_cu;
-        const double t = (double)rounds * per_cu * cfgs[i].bm * cfgs[i].bn * 100.0 / cfgs[i].eff;
-        if (i == 0 || t < best) best = t;
-    }
+    const double best = f16_tile_estimate(M, N, cus, f16_tile_config(M, N, cus));
     return t_split < best ? n1 : 0;
 }
 
@@ -827,10 +846,10 @@ hipError_t launch_gemm_f16_direct_op(const GemmArgs& a, hipStream_t s) {
             return launch_f16_kind<OP, CfgNarrow>(a, s);
     }
     if constexpr (OP == 3) {
-        // fp32 A: no 256 x 256 tiles (its staging registers do not fit beside
-        // their accumulators); 256 x 128 where the cost model picks 256 x 256
-        // or 256 x 128, else 128 x 128
-        if (a.ksplit <= 1 && f16_tile_config(a.M, a.N, device_cu_count()) <= 1)
+        // fp32 A: no 256 x 256 or 256 x 192 tiles (its staging registers do
+        // not fit beside their accumulators); 256 x 128 where the cost model
+        // picks one of those three, else 128 x 128
+        if (a.ksplit <= 1 && f16_tile_config(a.M, a.N, device_cu_count()) != 2)
             return launch_f16_kind<OP, CfgMid>(a, s);
         return launch_f16_kind<OP, CfgSmall>(a, s);
     } else {
@@ -845,6 +864,7 @@ hipError_t launch_gemm_f16_direct_op(const GemmArgs& a, hipStream_t s) {
         switch (a.ksplit > 1 ? 2 : f16_tile_config(a.M, a.N, device_cu_count())) {
             case 0: return launch_f16_kind<OP, CfgLarge>(a, s);
             case 1: return launch_f16_kind<OP, CfgMid>(a, s);
+            case 3: return launch_f16_kind<OP, CfgWide>(a, s);
             default:
                 // (TN only: the NN and NT products keep the order of the
                 // AMP path's 128 x 128 tiles, so the two agree bit for bit)

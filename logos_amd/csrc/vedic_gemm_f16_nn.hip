@@ -8,6 +8,7 @@ namespace vedic {
 VEDIC_F16_INSTANTIATE(0, CfgLarge);
 VEDIC_F16_INSTANTIATE(0, CfgSmall);
 VEDIC_F16_INSTANTIATE(0, CfgMid);
+VEDIC_F16_INSTANTIATE(0, CfgWide);
 VEDIC_F16_INSTANTIATE(0, CfgNarrow);
 
 hipError_t launch_gemm_f16_direct_nn(const GemmArgs& a, hipStream_t s) {

@@ -8,6 +8,7 @@ namespace vedic {
 VEDIC_F16_INSTANTIATE(1, CfgLarge);
 VEDIC_F16_INSTANTIATE(1, CfgSmall);
 VEDIC_F16_INSTANTIATE(1, CfgMid);
+VEDIC_F16_INSTANTIATE(1, CfgWide);
 VEDIC_F16_INSTANTIATE(1, CfgNarrow);
 
 hipError_t launch_gemm_f16_direct_nt(const GemmArgs& a, hipStream_t s) {

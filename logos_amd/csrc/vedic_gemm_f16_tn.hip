@@ -9,6 +9,7 @@ VEDIC_F16_INSTANTIATE(2, CfgLarge);
 VEDIC_F16_INSTANTIATE(2, CfgSmall);
 VEDIC_F16_INSTANTIATE(2, CfgSmallK);
 VEDIC_F16_INSTANTIATE(2, CfgMid);
+VEDIC_F16_INSTANTIATE(2, CfgWide);
 VEDIC_F16_INSTANTIATE(2, CfgNarrowT);
 
 hipError_t launch_gemm_f16_direct_tn(const GemmArgs& a, hipStream_t s) {

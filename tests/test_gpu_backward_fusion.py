@@ -285,8 +285,9 @@ def test_gemm_scatter_heads(dtype, M):
     the matching columns of the unscattered product (bit for bit where both run
     the same kernel; the unscattered fp32 product at M = 300 has few tiles and
     is split over K, which scattered output never is), and the per-head product
-    X . W_h of the fp64 oracle within tolerance.  M = 8192 takes the 256 x 256
-    tiles, 300 the 128 x 128 tiles, 7 the decode kernel."""
+    X . W_h of the fp64 oracle within tolerance.  M = 8192 takes the 256 x 192
+    tiles (three heads per tile), 300 the 128 x 128 tiles, 7 the decode
+    kernel."""
     vedic = V()
     H, DH, K = 16, 64, 1024
     rng = np.random.default_rng(zlib.crc32(f"scatter-{dtype}-{M}".encode()))
@@ -315,6 +316,27 @@ def test_gemm_scatter_heads(dtype, M):
             want, _ = o.gemm_f64(o.NN, np.ascontiguousarray(X[rows]), np.ascontiguousarray(Wp[:, h * DH:(h + 1) * DH]),
                                  bias=bias[h * DH:(h + 1) * DH])
             assert o.inf_rel_err(got[rows], want) <= tol
+
+
+def test_gemm_scatter_heads_column_split():
+    """40 heads of 64 columns at M = 16384: the library runs the first 2048
+    columns on 256 x 256 tiles and the last 512 on 256 x 128 tiles (two
+    launches, the second with its heads shifted by 32); every head equals
+    the unscattered product's columns bit for bit."""
+    vedic = V()
+    M, K, NH, DH = 16384, 256, 40, 64
+    rng = np.random.default_rng(4040)
+    x, X = dev_f16(normal(rng, (M, K)))
+    w, Wp = dev_f16(normal(rng, (K, NH * DH), std=0.05))
+    bias = normal(rng, (NH * DH,), std=0.01)
+    heads = [torch.full((M, DH), 9.0, device="cuda") for _ in range(NH)]
+    vedic.gemm_scatter(x, w, heads, bias=dev(bias))
+    full = host(vedic.gemm(vedic.OP_NN, x, w, bias=dev(bias), epilogue=vedic.EPI_BIAS))
+    for h in range(NH):
+        assert np.array_equal(host(heads[h]), full[:, h * DH:(h + 1) * DH]), f"head {h}"
+    rows = np.array([0, 5000, M - 1])
+    want, _ = o.gemm_f64(o.NN, np.ascontiguousarray(X[rows]), Wp, bias=bias)
+    assert o.inf_rel_err(full[rows], want) <= FP16_TOL
 
 
 def test_gemm_scatter_rejections():

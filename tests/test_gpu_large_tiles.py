@@ -1,6 +1,7 @@
-"""The 256 x 256 fp16 tile (plain, bias and bias + GELU epilogues) on shapes
-large enough for the library to pick that tile, edges included, and the
-column split that runs part of a product on 256 x 128 tiles.
+"""The 256 x 256 and 256 x 192 fp16 tiles (plain, bias and bias + GELU
+epilogues) on shapes large enough for the library to pick them, edges
+included, and the column split that runs part of a product on 256 x 128
+tiles.
 
 Every output is compared over the whole matrix with the same product through
 the epilogue that also writes the pre-activation (another instantiation of
@@ -24,12 +25,13 @@ from tests.test_gpu_configs import rows_of, sampled_check  # noqa: E402
 pytestmark = pytest.mark.gpu
 
 OPS = {"NN": o.NN, "NT": o.NT, "TN": o.TN}
-# (M, N, K): edges in M, N and K; interior tiles with an odd stage count;
-# K below one 64-deep stage; edge and interior tiles with whole stages; and
-# two products the library splits by columns (2048 columns of 256 x 256
-# tiles, the rest on 256 x 128 tiles), the second with an edge in N
+# (M, N, K), 256 x 256 tiles: edges in M, N and K; interior tiles with an odd
+# stage count; K below one 64-deep stage; edge and interior tiles with whole
+# stages.  256 x 192 tiles (two whole rounds): the packed Q/K/V shape, the
+# same with an edge in N, and edges in M, N and K.  The column split (4096
+# columns of 256 x 256 tiles, 520 on 256 x 128 tiles).
 SHAPES = [(7000, 3464, 1000), (7936, 3840, 960), (7000, 3464, 40), (7000, 3464, 1024), (8192, 3072, 1024),
-          (8192, 3000, 200)]
+          (8192, 3000, 200), (7000, 2900, 1000), (8192, 4616, 136)]
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -89,15 +91,16 @@ def test_large_tile_leaves_outside_rows_alone():
     assert np.all(h[0] == 7.0) and np.all(h[M + 1] == 7.0)
 
 
+@pytest.mark.parametrize("shape", [(8192, 3072, 256), (8192, 4616, 136)], ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("opname", list(OPS))
-def test_column_split_fp16_output(opname):
-    """fp16 C through the column split: the second part's C starts 2048
-    two-byte elements in."""
+def test_column_split_fp16_output(opname, shape):
+    """fp16 C on the 256 x 192 tile and through the column split (the second
+    part's C starts 4096 two-byte elements in)."""
     from logos_amd import vedic
 
     layout = OPS[opname]
-    M, N, K = 8192, 3072, 256
-    rng = np.random.default_rng(zlib.crc32(f"split16-{opname}".encode()))
+    M, N, K = shape
+    rng = np.random.default_rng(zlib.crc32(f"split16-{opname}-{shape}".encode()))
     A, B = _operands(rng, layout, M, N, K)
     a, Ar = dev_f16(A)
     b, Br = dev_f16(B)
@@ -108,13 +111,15 @@ def test_column_split_fp16_output(opname):
     assert err <= FP16_TOL, f"{opname} fp16 out: {err:.3e}"
 
 
-@pytest.mark.parametrize("shape", [(4096, 4096, 512), (8192, 3072, 256)], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("shape", [(4096, 4096, 512), (8192, 3072, 256), (8192, 4616, 136)],
+                         ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("opname", list(OPS))
 def test_large_tile_padded_leading_dimensions(opname, shape):
     """A, B and C as views into wider buffers (row pitch > the used extent) on
-    the 256 x 256 tile and through the column split (whose second part starts
-    B 2048 columns -- for NT 2048 rows of pitch ldb -- in): the same bits as
-    the contiguous product, and the padding columns of C untouched."""
+    the 256 x 256 and 256 x 192 tiles and through the column split (whose
+    second part starts B 4096 columns -- for NT 4096 rows of pitch ldb -- in):
+    the same bits as the contiguous product, and the padding columns of C
+    untouched."""
     from logos_amd import vedic
 
     layout = OPS[opname]
