@@ -388,9 +388,11 @@ inline void cuda_cast_pack_fp16(const float* const* src, int nsrc, int rows, int
 // --------------------------------------------------- attention
 
 // cuda_flash_attention_fwd (cuda/VedicGEMM.cuh:236, cuda/VedicGEMM.cu:1065-1104):
-// out = softmax(scale Q K^T + mask) V for one head, fp32 [seq x DH].  As in the
-// reference, DH > 128 throws std::runtime_error; this build also needs DH 64
-// or 128 and attn_ptr == nullptr (std::invalid_argument otherwise).
+// out = softmax(scale Q K^T + mask) V for one head, fp32 [seq x DH], any DH
+// from 1 to 128.  As in the reference, DH > 128 throws std::runtime_error;
+// DH < 1 or a bad mask stride throws std::invalid_argument.  attn_ptr (null,
+// or [seq x seq]) receives the reference's probability copy: the values of
+// its 16-key walk with a running row maximum, normalised by the row sum.
 inline void cuda_flash_attention_fwd(const float* Q, const float* K, const float* V, float* out, float* attn_ptr,
                                      int seq, int DH, float scale, bool causal, bool shunyam, int window, int stride,
                                      hipStream_t stream = nullptr) {

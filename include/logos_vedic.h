@@ -361,8 +361,9 @@ int vedic_gemm_checked(const vedic_gemm_desc_t* desc, float tolerance, vedic_ver
  * Replaces cuda_flash_attention_fwd (cuda/VedicGEMM.cuh:236, cuda/VedicGEMM.cu:1065-1104;
  * kernel :898-1063), called per head at cuda/ModelGPU.cu:959-968.
  * attn (NULL, or [seq x seq]): the reference's optional probability copy,
- * with the reference's values (its flash kernel walks the keys in tiles of 32
- * with a running row maximum): an allowed key k gets expf(s_k - m_t) / l,
+ * with the reference's values (its flash kernel walks the keys in tiles of 16,
+ * FA_TILE at cuda/VedicGEMM.cu:898, with a running row maximum): an allowed
+ * key k gets expf(s_k - m_t) / l,
  * m_t the running maximum after the tile holding k and l the row sum; a
  * masked key keeps its previous content times 1 / l (the reference's final
  * pass scales the whole row; 0 for a row with l <= 1e-9).  Computed by a

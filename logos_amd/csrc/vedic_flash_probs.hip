@@ -3,8 +3,9 @@
 // 1056-1060): attn[q][k] for one head, [seq x seq] fp32.
 //
 // The reference fills it inside its flash kernel, which walks the keys in
-// tiles of 32 with a running row maximum, and its values are those of that
-// walk, not plain softmax probabilities:
+// tiles of 16 (FA_TILE, cuda/VedicGEMM.cu:898, loop :952-1043) with a running
+// row maximum, and its values are those of that walk, not plain softmax
+// probabilities:
 //   * an allowed key k of tile t gets expf(s_k - M_t) / l, where s_k is the
 //     scaled score, M_t the running maximum after tile t (the maximum over
 //     the allowed scores of tiles 0..t, -1e30 before the first), and l the
@@ -22,10 +23,11 @@
 // the running maximum (the same operations, so the same M_t) and writes the
 // row.  Scores are dot products in ascending d, as in the reference.
 //
-// Workgroup: 256 threads, 32 query rows; per 32-key tile the K rows go
+// Workgroup: 256 threads, 32 query rows; per 32-key LDS block the K rows go
 // through LDS, thread t computes the scores of query t / 8 against keys
 // 4 (t % 8) .. + 3 (its query row in registers), and thread r < 32 updates row
-// r's running state over the tile's 32 scores in key order.
+// r's running state over the block's two 16-key tiles in key order, one
+// maximum update per tile as in the reference.
 #include <hip/hip_runtime.h>
 
 #include "vedic_flash_device.hpp"
@@ -35,7 +37,8 @@ namespace vedic {
 namespace {
 
 constexpr int kPrQ = 32;     // query rows per workgroup
-constexpr int kPrKeys = 32;  // keys per tile, the reference's FA_TILE
+constexpr int kPrKeys = 32;  // keys per LDS block: two of the walk's tiles
+constexpr int kPrTile = 16;  // keys per tile of the walk, the reference's FA_TILE
 
 template <int DHP>
 struct ProbsTile {
@@ -96,27 +99,29 @@ __global__ void __launch_bounds__(256) flash_probs_kernel(FlashArgs a, int dh, f
         score_tile(key0);
         __syncthreads();
         if (tid < kPrQ) {
-            float tmax = -1e30f;
-            for (int j = 0; j < kPrKeys; ++j) tmax = fmaxf(tmax, tl.s[tid][j]);
-            const float mn = fmaxf(m, tmax);
-            float ln = l * expf(m - mn);
-            for (int j = 0; j < kPrKeys; ++j) {
-                const float s = tl.s[tid][j];
-                if (s <= -1e29f) continue;
-                ln += expf(s - mn);
+#pragma unroll
+            for (int h = 0; h < kPrKeys; h += kPrTile) {
+                float tmax = -1e30f;
+                for (int j = h; j < h + kPrTile; ++j) tmax = fmaxf(tmax, tl.s[tid][j]);
+                const float mn = fmaxf(m, tmax);
+                float ln = l * expf(m - mn);
+                for (int j = h; j < h + kPrTile; ++j) {
+                    const float s = tl.s[tid][j];
+                    if (s <= -1e29f) continue;
+                    ln += expf(s - mn);
+                }
+                m = mn;
+                l = ln;
             }
-            m = mn;
-            l = ln;
         }
     }
     const float inv_l = l > 1e-9f ? 1.0f / l : 0.0f;
     // pass 2: the same walk, writing the row; each thread writes its four
     // keys of its query (allowed: expf(s - M_t) / l; masked: old value / l)
-    __shared__ float row_m[kPrQ], row_inv[kPrQ];
-    if (tid < kPrQ) {
-        row_inv[tid] = inv_l;
-        row_m[tid] = -1e30f;
-    }
+    // row_m[r][h]: row r's running maximum after the block's tile h
+    __shared__ float row_m[kPrQ][kPrKeys / kPrTile], row_inv[kPrQ];
+    if (tid < kPrQ) row_inv[tid] = inv_l;
+    float run_m = -1e30f;  // row tid's running maximum (threads 0..31)
     for (int t = 0; t < ntiles; ++t) {
         const int key0 = t * kPrKeys;
         __syncthreads();
@@ -125,14 +130,18 @@ __global__ void __launch_bounds__(256) flash_probs_kernel(FlashArgs a, int dh, f
         score_tile(key0);
         __syncthreads();
         if (tid < kPrQ) {
-            float tmax = -1e30f;
-            for (int j = 0; j < kPrKeys; ++j) tmax = fmaxf(tmax, tl.s[tid][j]);
-            row_m[tid] = fmaxf(row_m[tid], tmax);
+#pragma unroll
+            for (int h = 0; h < kPrKeys / kPrTile; ++h) {
+                float tmax = -1e30f;
+                for (int j = h * kPrTile; j < (h + 1) * kPrTile; ++j) tmax = fmaxf(tmax, tl.s[tid][j]);
+                run_m = fmaxf(run_m, tmax);
+                row_m[tid][h] = run_m;
+            }
         }
         __syncthreads();
         if (my_q < a.seq) {
-            const int r = tid / 8, kc = 4 * (tid % 8);
-            const float mt = row_m[r], il = row_inv[r];
+            const int r = tid / 8, kc = 4 * (tid % 8);  // kc .. kc + 3 lie in one tile
+            const float mt = row_m[r][kc / kPrTile], il = row_inv[r];
             float* out = attn + (int64_t)my_q * a.seq + key0 + kc;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {

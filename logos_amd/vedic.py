@@ -475,7 +475,8 @@ def flash_attention_fwd(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, out: 
     stride.  attn (optional contiguous float32 [seq x seq] GPU tensor)
     receives the reference's probability copy, with the reference's values:
     allowed entries expf(s - m_t) / l (m_t the running maximum after the
-    32-key tile holding the key), masked entries their previous content / l.
+    16-key tile holding the key: the reference's FA_TILE,
+    cuda/VedicGEMM.cu:898), masked entries their previous content / l.
     lse (optional float32 [seq] GPU tensor, not together with attn) receives
     each row's log-sum-exp ln(sum over allowed keys of e^(scale q.k)), for
     flash_attention_bwd."""

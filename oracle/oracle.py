@@ -468,17 +468,23 @@ def flash_attention_f64(Q, K, V, scale, causal=True, shunyam=False, window=0, st
     return np.where(den > 0, (P @ V) / np.where(den > 0, den, 1.0), 0.0)
 
 
+FA_TILE = 16  # keys per tile of the reference's flash walk (cuda/VedicGEMM.cu:898)
+
+
 def flash_attention_probs(Q, K, scale, causal=True, shunyam=False, window=0, stride=1, prior=None,
-                          rows=None) -> np.ndarray:
+                          rows=None, tile=FA_TILE) -> np.ndarray:
     """The reference's optional probability copy `Aptr` (cuda/VedicGEMM.cu:906,
-    1033-1037, 1056-1060) restated in fp32: keys walked in tiles of 32
-    (FA_TILE) with the running row maximum m (-1e30 before any allowed key);
-    an allowed key of tile t is written expf(s - m_t), m_t the maximum after
-    tile t; the row sum l accumulates with the online rescaling; finally the
-    whole row, masked entries included (never written, so they keep `prior`),
-    is multiplied by 1/l (0 if l <= 1e-9).  prior: the buffer's previous
-    content (zeros if None).  rows: optional query subset (rows are
-    independent); the result then has one row per entry."""
+    952-1059) restated in fp32: keys walked in tiles of
+    FA_TILE = 16 (`#define FA_TILE 16`, cuda/VedicGEMM.cu:898; the loop over
+    kv tiles at :952) with the running row maximum m (-1e30 before any allowed
+    key); an allowed key of tile t is written expf(s - m_t), m_t the maximum
+    after tile t (:1009, :1036); the row sum l accumulates with the online
+    rescaling (:1015-1024); finally the whole row, masked entries included
+    (never written, so they keep `prior`), is multiplied by 1/l, 0 if
+    l <= 1e-9 (:1049-1059).  prior: the buffer's previous content (zeros if
+    None).  rows: optional query subset (rows are independent); the result
+    then has one row per entry.  tile: the walk's width; only the tests pass
+    another value, to show that a different walk gives different values."""
     Q, K = _f32(Q), _f32(K)
     seq = K.shape[0]
     idx = np.arange(seq) if rows is None else np.asarray(rows)
@@ -490,15 +496,15 @@ def flash_attention_probs(Q, K, scale, causal=True, shunyam=False, window=0, str
     out = np.zeros((n, seq), dtype=f) if prior is None else np.array(prior, dtype=f, copy=True)
     m = np.full(n, -1e30, dtype=f)
     l = np.zeros(n, dtype=f)
-    for k0 in range(0, seq, 32):
-        blk = S[:, k0:k0 + 32]
-        ok = allowed[:, k0:k0 + 32]
+    for k0 in range(0, seq, tile):
+        blk = S[:, k0:k0 + tile]
+        ok = allowed[:, k0:k0 + tile]
         mn = np.maximum(m, blk.max(axis=1))
         ln = l * np.exp(m - mn)
         e = np.exp(blk - mn[:, None]).astype(f)
         for j in range(blk.shape[1]):  # the reference's order of additions
             ln = np.where(ok[:, j], ln + e[:, j], ln).astype(f)
-        out[:, k0:k0 + 32] = np.where(ok, e, out[:, k0:k0 + 32])
+        out[:, k0:k0 + tile] = np.where(ok, e, out[:, k0:k0 + tile])
         m, l = mn, ln
     inv = np.where(l > f(1e-9), f(1) / np.where(l > 0, l, f(1)), f(0)).astype(f)
     return (out * inv[:, None]).astype(f)

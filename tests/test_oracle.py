@@ -487,18 +487,22 @@ def test_componentwise_ratio_definition():
 
 # ------------------------------------------- attention probability copy (Aptr)
 
-def _probs_closed_form(Q, K, scale, mask, prior):
+REF_FA_TILE = 16  # `#define FA_TILE 16`, /root/reference/cuda/VedicGEMM.cu:898
+
+
+def _probs_closed_form(Q, K, scale, mask, prior, tile=REF_FA_TILE):
     """float64 closed form of the reference's Aptr values: an allowed key of
-    32-key tile t gets exp(s - M_t) / l with M_t = max of the allowed scores
+    16-key tile t gets exp(s - M_t) / l with M_t = max of the allowed scores
     of tiles 0..t and l = sum over allowed keys of exp(s - M_row); a masked key
-    prior / l.  (Derived from the kernel's walk: m only grows, and the online
-    rescaling makes l the plain sum at the final maximum.)"""
+    prior / l.  (Derived from the kernel's walk, cuda/VedicGEMM.cu:952-1059:
+    m only grows, and the online rescaling makes l the plain sum at the final
+    maximum.)"""
     S = scale * (np.asarray(Q, np.float64) @ np.asarray(K, np.float64).T)
     seq = S.shape[0]
     Sm = np.where(mask, S, -np.inf)
-    tile_max = np.stack([Sm[:, k0:k0 + 32].max(axis=1) for k0 in range(0, seq, 32)], axis=1)
+    tile_max = np.stack([Sm[:, k0:k0 + tile].max(axis=1) for k0 in range(0, seq, tile)], axis=1)
     run = np.maximum.accumulate(tile_max, axis=1)
-    Mt = np.repeat(run, 32, axis=1)[:, :seq]
+    Mt = np.repeat(run, tile, axis=1)[:, :seq]
     Mrow = run[:, -1:]
     l = np.where(mask, np.exp(S - Mrow), 0.0).sum(axis=1, keepdims=True)
     inv = np.where(l > 1e-9, 1.0 / np.where(l > 0, l, 1.0), 0.0)
@@ -506,7 +510,8 @@ def _probs_closed_form(Q, K, scale, mask, prior):
 
 
 @pytest.mark.parametrize("seq,causal,shunyam,window,stride", [
-    (20, 1, 0, 0, 1), (32, 0, 0, 0, 1), (31, 1, 1, 4, 5),   # one tile: plain softmax
+    (12, 1, 0, 0, 1), (16, 0, 0, 0, 1), (15, 1, 1, 4, 5),   # one tile: plain softmax
+    (20, 1, 0, 0, 1), (32, 0, 0, 0, 1), (31, 1, 1, 4, 5),
     (100, 1, 0, 0, 1), (100, 0, 0, 0, 1), (97, 1, 1, 8, 7), (130, 0, 1, 3, 10)])
 def test_flash_probs_restatement_against_closed_form(seq, causal, shunyam, window, stride):
     rng = np.random.default_rng(seq + 3 * window)
@@ -517,11 +522,22 @@ def test_flash_probs_restatement_against_closed_form(seq, causal, shunyam, windo
     got = o.flash_attention_probs(Q, K, 0.5, causal, shunyam, window, stride, prior)
     want = _probs_closed_form(Q, K, 0.5, mask, prior)
     assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-3)) < 2e-5
-    if seq <= 32:  # a single tile: the allowed entries are the softmax probabilities
+    if seq <= REF_FA_TILE:  # a single tile: the allowed entries are the softmax probabilities
         S = 0.5 * (Q.astype(np.float64) @ K.T.astype(np.float64))
         P = np.where(mask, np.exp(S - np.where(mask, S, -np.inf).max(1, keepdims=True)), 0.0)
         P /= P.sum(1, keepdims=True)
         assert np.max(np.abs(np.where(mask, got, 0.0) - P)) < 1e-6
+
+
+def _stale_max_case(seq, kmax):
+    """Q = e0, all keys 0 except key kmax = 3 e0: every score is 0 but s[kmax] = 3."""
+    Q = np.zeros((seq, 2), np.float32)
+    K = np.zeros((seq, 2), np.float32)
+    Q[:, 0] = 1.0
+    K[kmax, 0] = 3.0
+    S = np.zeros(seq)
+    S[kmax] = 3.0
+    return Q, K, S
 
 
 def test_flash_probs_stale_maximum_is_kept():
@@ -530,19 +546,33 @@ def test_flash_probs_stale_maximum_is_kept():
     reference's values, which a plain softmax would miss -- while the tile
     holding the maximum and later ones are the softmax."""
     seq = 96
-    Q = np.zeros((seq, 2), np.float32)
-    K = np.zeros((seq, 2), np.float32)
-    Q[:, 0] = 1.0
-    K[:, 0] = 0.0
-    K[70, 0] = 3.0  # the row maximum: key 70, tile 2
+    Q, K, S = _stale_max_case(seq, 70)  # the row maximum: key 70, in the tile of keys 64..79
     got = o.flash_attention_probs(Q, K, 1.0, causal=False)
-    S = np.zeros(seq)
-    S[70] = 3.0
     soft = np.exp(S - 3.0) / np.exp(S - 3.0).sum()
     row = got[80].astype(np.float64)
     assert np.allclose(row[64:], soft[64:], rtol=1e-5)
     assert np.allclose(row[:64], soft[:64] * np.exp(3.0), rtol=1e-5)
     assert not np.allclose(row[:64], soft[:64], rtol=1e-2)
+
+
+def test_flash_probs_walk_is_sixteen_keys_wide():
+    """The row maximum at key 50, in the second half of a 32-key block: the
+    reference's 16-key walk has seen it when it writes keys 48..63 but not
+    when it writes keys 32..47, so keys 32..47 hold exp(s - max(s_0..s_47)) / l
+    = exp(0) / l and keys 48.. the softmax probability.  A 32-key walk writes
+    keys 32..47 after seeing key 50 and gives exp(-3) / l there: it fails."""
+    seq = 96
+    Q, K, S = _stale_max_case(seq, 50)
+    l = np.exp(S - 3.0).sum()  # the final sum at the row maximum
+    got = o.flash_attention_probs(Q, K, 1.0, causal=False).astype(np.float64)
+    for r in (0, 33, 95):
+        assert np.allclose(got[r, :48], 1.0 / l, rtol=1e-5)          # stale maxima 0
+        assert np.allclose(got[r, 48:], np.exp(S[48:] - 3.0) / l, rtol=1e-5)
+    mask = np.ones((seq, seq), dtype=bool)
+    assert np.allclose(got, _probs_closed_form(Q, K, 1.0, mask, np.zeros((seq, seq))), rtol=1e-5)
+    wide = o.flash_attention_probs(Q, K, 1.0, causal=False, tile=32).astype(np.float64)
+    assert not np.allclose(wide[:, 32:48], got[:, 32:48], rtol=1e-2)
+    assert np.allclose(wide[0, 32:48], np.exp(-3.0) / l, rtol=1e-5)
 
 
 # ----------------------------------------------------------- layer normalisation
