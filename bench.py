@@ -50,9 +50,12 @@ HBM_PEAK_GBS = 8000.0                   # MI355X HBM3E, GB/s (published)
 #   dtype "amp": A fp32, converted to binary16 inside the GEMM (the AMP path from
 #   an fp32 activation); cast_a: an fp32 A cast into a binary16 buffer by a
 #   separate launch before the fp16 GEMM, every step (the reference's amp_gemm).
-def _g(M, K, N, op="NN", dtype="fp16", epi="none", beta=0.0, checked=False, heads=0, alpha=1.0, cast_a=False):
+#   gather: A read from that many [M x K / gather] head matrices, accumulated
+#   head by head (vedic_gemm_gather).
+def _g(M, K, N, op="NN", dtype="fp16", epi="none", beta=0.0, checked=False, heads=0, alpha=1.0, cast_a=False,
+       gather=0):
     return dict(M=M, K=K, N=N, op=op, dtype=dtype, epi=epi, beta=beta, checked=checked, heads=heads, alpha=alpha,
-                cast_a=cast_a)
+                cast_a=cast_a, gather=gather)
 
 
 # BASELINE.json configs; each workload is a list of GEMMs run back to back per step.
@@ -75,6 +78,15 @@ WORKLOADS = {
     # the same activation X with each head's own [1024 x 64] weight
     "qkv_per_head_fp16": dict(cfg=5, share_a=True, gemms=[_g(8192, 1024, 64) for _ in range(48)]),
     "qkv_packed_scatter_fp16": dict(cfg=5, gemms=[_g(8192, 1024, 3072, heads=48)]),
+    # the attention-output projection of one layer: the reference's 16 per-head
+    # amp_gemm(hc.head_out, W_O[h]) calls, each added into the zeroed concat by
+    # residual_add_kernel (cuda/ModelGPU.cu:976-986; here beta = 1 into the one
+    # shared concat, no temporary), against one launch that gathers the 16 fp32
+    # head outputs and multiplies the row-stacked W_O, added head by head (the
+    # same bits)
+    "attn_out_per_head_amp": dict(cfg=5, share_c=True,
+                                  gemms=[_g(8192, 64, 1024, dtype="amp", beta=1.0) for _ in range(16)]),
+    "attn_out_stacked_amp": dict(cfg=5, gemms=[_g(8192, 1024, 1024, dtype="amp", gather=16)]),
     # the FFN-down with its bias and the residual add in the epilogue: the
     # reference's amp_gemm_bias into a temporary, then residual_add_kernel
     # (cuda/ModelGPU.cu:1044-1048); C holds the residual stream X
@@ -453,6 +465,7 @@ def make_step(w: dict, dev, torch):
     keep = []
     items = []
     shared_a = None  # share_a: every GEMM reads the first one's A (one activation, several weights)
+    shared_c = None  # share_c: every GEMM accumulates into the first one's C
     for g in w["gemms"]:
         M, K, N, op = g["M"], g["K"], g["N"], g["op"]
         a_shape = (K, M) if op == "TN" else (M, K)
@@ -478,6 +491,22 @@ def make_step(w: dict, dev, torch):
         resid = g["epi"] == "bias_residual"
         C = (torch.randn((M, N), generator=gen, device=dev) * (1.0 if resid else 1e-3) if g["beta"] or resid
              else torch.empty((M, N), device=dev))
+        if w.get("share_c"):
+            if shared_c is None:
+                shared_c = C
+            else:
+                C = shared_c
+        aheads = None
+        if g["gather"]:
+            hc = K // g["gather"]
+            hts = [torch.randn((M, hc), generator=gen, device=dev) for _ in range(g["gather"])]
+            if g["dtype"] == "fp16":
+                hts = [t.half() for t in hts]
+            keep += hts
+            A = hts[0]
+            aheads = (ctypes.c_void_p * g["gather"])(*[t.data_ptr() for t in hts])
+            keep.append(aheads)
+        g["_aheads"] = aheads
         keep += [A, B, bias, C]
         epi = {"none": _lib.EPI_NONE, "bias": _lib.EPI_BIAS, "bias_gelu": _lib.EPI_BIAS_GELU,
                "gelu_bwd": _lib.EPI_GELU_BWD, "bias_residual": _lib.EPI_BIAS_RESIDUAL}[g["epi"]]
@@ -530,6 +559,8 @@ def make_step(w: dict, dev, torch):
                     raise RuntimeError(f"vedic_cast_f32_to_f16 failed: {_lib.status_string(rc)}")
             if g["heads"]:
                 rc = lib.vedic_gemm_scatter(p, g["_heads"], g["heads"], g["N"] // g["heads"])
+            elif g["gather"]:
+                rc = lib.vedic_gemm_gather(p, g["_aheads"], g["gather"], g["K"] // g["gather"])
             else:
                 rc = lib.vedic_gemm_checked(p, 0.05, ctypes.byref(vres)) if checked else gemm(p)
             if rc:

@@ -385,6 +385,62 @@ inline void cuda_cast_pack_fp16(const float* const* src, int nsrc, int rows, int
                      "cuda_cast_pack_fp16");
 }
 
+// Stacked attention-output projection: concat[seq x D] = sum over heads, in
+// head order, of head_out[h][seq x DH] . W_O[h][DH x D] onto a zeroed concat,
+// bit for bit the reference's per-head amp_gemm + residual_add_kernel loop
+// (cuda/ModelGPU.cu:976-986) in one launch.  head_out fp32 (rounded to
+// binary16 as read, as amp_gemm casts it); Wo the binary16 row stack of the
+// W_O[h] (cuda_cast_stack_fp16).
+inline void cuda_amp_gemm_heads(const float* const* head_out, int nheads, int seq, int DH, const __half* Wo, int D,
+                                float* concat, hipStream_t stream = nullptr) {
+    vedic_gemm_desc_t d{};
+    d.op = VEDIC_OP_NN;
+    d.in_dtype = VEDIC_DT_F32_F16;
+    d.out_dtype = VEDIC_DT_F32;
+    d.M = seq;
+    d.N = D;
+    d.K = nheads * DH;
+    d.lda = DH;
+    d.B = Wo;
+    d.ldb = D;
+    d.C = concat;
+    d.ldc = D;
+    d.alpha = 1.0f;
+    d.stream = stream;
+    vedic_hip::check(vedic_gemm_gather(&d, reinterpret_cast<const void* const*>(head_out), nheads, DH),
+                     "cuda_amp_gemm_heads");
+}
+
+// The same with binary16 head outputs.
+inline void cuda_gemm_fp16_heads(const __half* const* head_out, int nheads, int seq, int DH, const __half* Wo, int D,
+                                 float* concat, hipStream_t stream = nullptr) {
+    vedic_gemm_desc_t d{};
+    d.op = VEDIC_OP_NN;
+    d.in_dtype = VEDIC_DT_F16;
+    d.out_dtype = VEDIC_DT_F32;
+    d.M = seq;
+    d.N = D;
+    d.K = nheads * DH;
+    d.lda = DH;
+    d.B = Wo;
+    d.ldb = D;
+    d.C = concat;
+    d.ldc = D;
+    d.alpha = 1.0f;
+    d.stream = stream;
+    vedic_hip::check(vedic_gemm_gather(&d, reinterpret_cast<const void* const*>(head_out), nheads, DH),
+                     "cuda_gemm_fp16_heads");
+}
+
+// Shadow-weight cast of several fp32 [rows x cols] matrices stacked by rows
+// into one binary16 matrix (cuda/train_gpu.cu:1542-1547 per parameter, here
+// W_O[0..H) of a layer into [H DH x D]).
+inline void cuda_cast_stack_fp16(const float* const* src, int nsrc, int rows, int cols, __half* dst,
+                                 hipStream_t stream = nullptr) {
+    vedic_hip::check(vedic_cast_stack_f16(src, nsrc, rows, cols, dst, (int64_t)cols, stream),
+                     "cuda_cast_stack_fp16");
+}
+
 // --------------------------------------------------- attention
 
 // cuda_flash_attention_fwd (cuda/VedicGEMM.cuh:236, cuda/VedicGEMM.cu:1065-1104):

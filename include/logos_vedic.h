@@ -146,8 +146,12 @@ int vedic_gemm(const vedic_gemm_desc_t* desc);
  * vedic_noalloc_scratch_bytes() bytes (32 MiB) compiled into the library and
  * held until the process ends.  A call that needs more returns
  * VEDIC_STATUS_TOO_LARGE before launching anything that writes C.  Every call
- * on one GPU shares that region: calls that overlap on one GPU (two streams,
- * two host threads) race, so serialise them. */
+ * on one GPU shares that region, so calls whose kernels can be in flight at
+ * the same time race: calls from two host threads, and also calls made one
+ * after another by one thread on two different streams (the second call's
+ * kernels may start before the first call's have finished).  Order such
+ * calls on the GPU: issue them on one stream, or make the second stream wait
+ * for an event recorded after the first call. */
 int vedic_gemm_noalloc(const vedic_gemm_desc_t* desc);
 
 /* Size of the region vedic_gemm_noalloc draws from (per GPU). */
@@ -159,7 +163,10 @@ size_t vedic_noalloc_scratch_bytes(void);
  * before destroying a stream the library has used: blocks are keyed by the
  * stream handle, and a stream created later with the same handle would
  * otherwise inherit the block while work of the destroyed stream may still be
- * using it.  New: the reference allocates per call and keeps nothing. */
+ * using it.  hipStreamPerThread names a different stream in every host
+ * thread; its blocks are kept per thread, and a thread that used it releases
+ * its own (pass hipStreamPerThread) before it exits.  New: the reference
+ * allocates per call and keeps nothing. */
 int vedic_workspace_release(void* stream);
 
 /* ---- reference-compatible entry points ------------------------------- */
@@ -257,6 +264,31 @@ int vedic_gemm_scatter(const vedic_gemm_desc_t* desc, float* const* heads, int n
 int vedic_gemm_f16_scatter(const void* X, int M, int K, const void* W, int N, float* const* heads, int nheads,
                            int head_cols, void* stream);
 
+/* The mirror of vedic_gemm_scatter on the A side, for the attention-output
+ * projection: A is gathered from separate matrices and the contraction is
+ * accumulated head by head,
+ *     C[MxN] = sum over h in 0..nheads-1, in that order, of
+ *              heads[h][M x head_cols] . B[h head_cols .. (h+1) head_cols)[KxN],
+ * each head's product taken from zero in fp32 and added to the running sum
+ * (round to nearest), starting from a zeroed C: bit for bit the result of
+ * zeroing C and calling vedic_gemm once per head with beta = 1.  Replaces the
+ * reference's per-head loop amp_gemm(hc.head_out, W_O[h]) + residual_add_kernel
+ * into `concat` (cuda/ModelGPU.cu:976-986; residual_add_kernel :57-60), 16
+ * launches of K = 64 and 16 passes over the 32 MB concat per layer, with one
+ * launch over the row-stacked W_O (vedic_cast_stack_f16).
+ * desc: op NN; in_dtype VEDIC_DT_F16 (binary16 heads) or VEDIC_DT_F32_F16
+ * (fp32 heads, the reference's head_out, rounded to binary16 as they are
+ * read, as the AMP entry points do); B binary16 [K x N], K = nheads *
+ * head_cols; out_dtype F32; epilogue NONE, alpha 1, beta 0, no colsum or
+ * preact (VEDIC_STATUS_BAD_EPILOGUE otherwise); desc->A unused; desc->lda is
+ * the heads' leading dimension (>= head_cols).  nheads <= 64.
+ * One launch when head_cols is a multiple of 64, N > 64 and every head, B and
+ * the leading dimensions are aligned as for the 16-byte-load path; otherwise
+ * the per-head calls themselves (same result).  With fp32 heads and N > 1024
+ * the heads are first cast into an M x K binary16 block of the stream's
+ * workspace. */
+int vedic_gemm_gather(const vedic_gemm_desc_t* desc, const void* const* heads, int nheads, int head_cols);
+
 /* FFN backward through the activation, fused:
  *     dH[MxN] = (dY[MxK] . W^T) * gelu_tanh'(H),   W stored [NxK],
  *     db[j]  += sum_i dH[i][j]                     (db nullable),
@@ -322,6 +354,14 @@ int vedic_cast_f32_to_f16(const float* src, void* dst, int64_t n, void* stream);
  * vedic_gemm_f16_scatter. */
 int vedic_cast_pack_f16(const float* const* src, int nsrc, int rows, int cols, void* dst, int64_t ld_dst,
                         void* stream);
+
+/* The same cast with the matrices stacked by rows: dst[i * rows + r][c] =
+ * src[i][r][c], dst row-major with leading dimension ld_dst >= cols; nsrc <=
+ * 64.  The shadow-weight cast of cuda/train_gpu.cu:1542-1547 applied to a
+ * layer's per-head W_O[h] [DH x D] blocks, stacked into the [H DH x D] B
+ * operand of vedic_gemm_gather. */
+int vedic_cast_stack_f16(const float* const* src, int nsrc, int rows, int cols, void* dst, int64_t ld_dst,
+                         void* stream);
 
 /* dst = float(src).  Replaces cuda_cast_fp16_to_fp32 (cuda/MixedPrecision.cuh:164-172,192-196). */
 int vedic_cast_f16_to_f32(const void* src, float* dst, int64_t n, void* stream);

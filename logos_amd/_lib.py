@@ -95,6 +95,8 @@ SIGNATURES = {
     "vedic_gemm_scatter": (c_int, [ctypes.POINTER(GemmDesc), ctypes.POINTER(c_vp), c_int, c_int]),
     "vedic_gemm_f16_scatter": (c_int, [c_vp, c_int, c_int, c_vp, c_int, ctypes.POINTER(c_vp), c_int, c_int, c_vp]),
     "vedic_cast_pack_f16": (c_int, [ctypes.POINTER(c_vp), c_int, c_int, c_int, c_vp, c_i64, c_vp]),
+    "vedic_gemm_gather": (c_int, [ctypes.POINTER(GemmDesc), ctypes.POINTER(c_vp), c_int, c_int]),
+    "vedic_cast_stack_f16": (c_int, [ctypes.POINTER(c_vp), c_int, c_int, c_int, c_vp, c_i64, c_vp]),
     "vedic_gemm_nt_gelu_bwd_f16": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     "vedic_gemm_nt_gelu_bwd_f32": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     "vedic_bias_grad": (c_int, [c_vp, c_vp, c_int, c_int, c_float, c_vp]),

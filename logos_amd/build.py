@@ -26,6 +26,7 @@ SOURCES = [
     "vedic_gemm_f16_nt.hip",
     "vedic_gemm_f16_tn.hip",
     "vedic_gemm_f16_amp.hip",
+    "vedic_gemm_f16_gather.hip",
     "vedic_gemm_f32_nn.hip",
     "vedic_gemm_f32_nt.hip",
     "vedic_gemm_f32_tn.hip",
@@ -83,8 +84,21 @@ def build_library(jobs: int = 6) -> str:
             f.result()
     tmp = LIB + ".tmp"
     _run([cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp, *objs])
+    check_wide_stores(tmp)
     os.replace(tmp, LIB)
     return LIB
+
+
+def check_wide_stores(lib: str) -> None:
+    """Fails the build if a 12- or 16-byte store's data registers are
+    rewritten within isa_check.WINDOW wait states on any path (isa_check)."""
+    from logos_amd import isa_check
+
+    total, found = isa_check.scan(lib)
+    if found:
+        lines = [f"{f}: {st} ; {u} after {ws} wait states" for f, st, u, ws in found[:20]]
+        raise RuntimeError(f"{len(found)} of {total} wide stores have a data register rewritten within "
+                           f"{isa_check.WINDOW} wait states:\n" + "\n".join(lines))
 
 
 CPP_DIR = os.path.join(ROOT, "tests", "cpp")

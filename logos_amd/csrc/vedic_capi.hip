@@ -11,6 +11,7 @@
 #include <chrono>
 #include <map>
 #include <mutex>
+#include <tuple>
 #include <utility>
 
 #include "../../include/logos_vedic.h"
@@ -29,6 +30,7 @@ hipError_t launch_gemm_f16_direct_nn(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_nt(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_tn(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f16_direct_amp(const GemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_f16_gather(const GemmArgs& a, bool amp, hipStream_t s);
 hipError_t launch_gemm_f16_skinny(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f32_skinny(const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_f32_direct_nn(const GemmArgs& a, hipStream_t s);
@@ -86,14 +88,26 @@ struct StreamArena {
     size_t cap = 0, used = 0, want = 0;
 };
 
-static std::mutex g_arenas_mu;
-static std::map<std::pair<int, hipStream_t>, StreamArena*> g_arenas;  // entries live until the process ends
+// Arenas and work-queue counters are kept per (device, stream handle, owner).
+// The owner is null except for hipStreamPerThread, which names a different
+// stream in every host thread: its memory is kept per thread (the address of
+// a thread-local tag), so threads that pass that handle never share it.
+typedef std::tuple<int, hipStream_t, const void*> StreamKey;
 
-static StreamArena* arena_of(hipStream_t s) {
+static StreamKey stream_key(hipStream_t s) {
+    static thread_local char tag;
     int dev = 0;
     (void)hipGetDevice(&dev);
+    return StreamKey(dev, s, s == hipStreamPerThread ? static_cast<const void*>(&tag) : nullptr);
+}
+
+static std::mutex g_arenas_mu;
+static std::map<StreamKey, StreamArena*> g_arenas;  // entries live until the process ends
+
+static StreamArena* arena_of(hipStream_t s) {
+    const StreamKey key = stream_key(s);
     std::lock_guard<std::mutex> lk(g_arenas_mu);
-    StreamArena*& a = g_arenas[std::make_pair(dev, s)];
+    StreamArena*& a = g_arenas[key];
     if (!a) a = new StreamArena();
     return a;
 }
@@ -104,13 +118,12 @@ static StreamArena* arena_of(hipStream_t s) {
 // merge kernel that ends every launch that uses it, so a call needs no reset
 // launch of its own.  Freed by vedic_workspace_release.
 static std::mutex g_fq_mu;
-static std::map<std::pair<int, hipStream_t>, int*> g_flash_queues;
+static std::map<StreamKey, int*> g_flash_queues;
 
 static int* flash_queue_of(hipStream_t s, hipError_t& e) {
-    int dev = 0;
-    (void)hipGetDevice(&dev);
+    const StreamKey key = stream_key(s);
     std::lock_guard<std::mutex> lk(g_fq_mu);
-    int*& q = g_flash_queues[std::make_pair(dev, s)];
+    int*& q = g_flash_queues[key];
     e = hipSuccess;
     if (!q) {
         int* p = nullptr;
@@ -126,10 +139,9 @@ static int* flash_queue_of(hipStream_t s, hipError_t& e) {
 }
 
 static hipError_t flash_queue_release(hipStream_t s) {
-    int dev = 0;
-    (void)hipGetDevice(&dev);
+    const StreamKey key = stream_key(s);
     std::lock_guard<std::mutex> lk(g_fq_mu);
-    auto it = g_flash_queues.find(std::make_pair(dev, s));
+    auto it = g_flash_queues.find(key);
     if (it == g_flash_queues.end()) return hipSuccess;
     const hipError_t e = hipFreeAsync(it->second, s);
     g_flash_queues.erase(it);
@@ -1055,24 +1067,50 @@ __global__ void cast_f32_f16_kernel(const float* __restrict__ src, _Float16* __r
     }
 }
 
-// Several fp32 [rows x cols] matrices cast to binary16 (same clamp and
-// rounding as the plain cast) and packed side by side: dst[r][i cols + c] =
-// src_i[r][c].  One thread per destination element, consecutive threads on
-// consecutive destination columns.
+// Several fp32 [rows x cols] matrices (rows lds elements apart) cast to
+// binary16 (same clamp and rounding as the plain cast) and packed side by
+// side: dst[r][i cols + c] = src_i[r][c].  One thread per destination
+// element, consecutive threads on consecutive destination columns.
 constexpr int kMaxPack = 64;
 struct PackSources {
     const float* p[kMaxPack];
 };
 
-__global__ void cast_pack_f16_kernel(PackSources src, int nsrc, int rows, int cols, _Float16* __restrict__ dst,
-                                     int64_t ld) {
+__global__ void cast_pack_f16_kernel(PackSources src, int nsrc, int rows, int cols, int64_t lds,
+                                     _Float16* __restrict__ dst, int64_t ld) {
     const int64_t width = (int64_t)nsrc * cols;
     const int64_t total = width * rows;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += (int64_t)gridDim.x * blockDim.x) {
         const int64_t r = e / width, w = e - r * width;
         const int i = (int)(w / cols), c = (int)(w - (int64_t)i * cols);
-        dst[r * ld + w] = to_half_clamped(src.p[i][r * cols + c]);
+        dst[r * ld + w] = to_half_clamped(src.p[i][r * lds + c]);
+    }
+}
+
+// The same matrices stacked by rows instead: dst[i rows + r][c] = src_i[r][c]
+// (the per-head W_O blocks of a layer as one [H DH x D] matrix).
+__global__ void cast_stack_f16_kernel(PackSources src, int nsrc, int rows, int cols, _Float16* __restrict__ dst,
+                                      int64_t ld) {
+    const int64_t per = (int64_t)rows * cols;
+    const int64_t total = per * nsrc;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int i = (int)(e / per);
+        const int64_t q = e - (int64_t)i * per;
+        const int64_t r = q / cols, c = q - r * cols;
+        dst[((int64_t)i * rows + r) * ld + c] = to_half_clamped(src.p[i][q]);
+    }
+}
+
+// C[r][c] = 0 over an M x N fp32 matrix (a kernel, not a memset, so that it
+// can be recorded in a graph).
+__global__ void zero_rows_kernel(float* __restrict__ C, int64_t ldc, int M, int N) {
+    const int64_t total = (int64_t)M * N;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = e / N;
+        C[r * ldc + (e - r * N)] = 0.0f;
     }
 }
 
@@ -1459,8 +1497,120 @@ extern "C" int vedic_cast_pack_f16(const float* const* src, int nsrc, int rows, 
     }
     const int64_t n = (int64_t)nsrc * cols * rows;
     hipLaunchKernelGGL(cast_pack_f16_kernel, dim3(ew_blocks(n, 4)), dim3(kEwThreads), 0,
+                       static_cast<hipStream_t>(stream), ps, nsrc, rows, cols, (int64_t)cols,
+                       static_cast<_Float16*>(dst), ld_dst);
+    return hip_status(hipGetLastError());
+}
+
+extern "C" int vedic_cast_stack_f16(const float* const* src, int nsrc, int rows, int cols, void* dst,
+                                    int64_t ld_dst, void* stream) {
+    if (nsrc <= 0 || rows <= 0 || cols <= 0) return VEDIC_STATUS_BAD_DIM;
+    if (nsrc > kMaxPack) return VEDIC_STATUS_TOO_LARGE;
+    if (!src || !dst) return VEDIC_STATUS_NULL_POINTER;
+    if (ld_dst < cols) return VEDIC_STATUS_BAD_LD;
+    PackSources ps{};
+    for (int i = 0; i < nsrc; ++i) {
+        if (!src[i]) return VEDIC_STATUS_NULL_POINTER;
+        ps.p[i] = src[i];
+    }
+    const int64_t n = (int64_t)nsrc * cols * rows;
+    hipLaunchKernelGGL(cast_stack_f16_kernel, dim3(ew_blocks(n, 4)), dim3(kEwThreads), 0,
                        static_cast<hipStream_t>(stream), ps, nsrc, rows, cols, static_cast<_Float16*>(dst), ld_dst);
     return hip_status(hipGetLastError());
+}
+
+// ------------------------------------------- gathered A, head-ordered sum
+
+// C = sum over heads h of A_h . B[h hc .. (h + 1) hc), added in head order
+// onto a zeroed C (each head's product from zero, fp32).  One launch of the
+// HO kernels where the operands allow it; otherwise literally the per-head
+// products with beta = 1 after zeroing C, which is what the one launch
+// reproduces bit for bit.
+extern "C" int vedic_gemm_gather(const vedic_gemm_desc_t* d, const void* const* a_heads, int nheads, int head_cols) {
+    if (!d || !a_heads) return VEDIC_STATUS_NULL_POINTER;
+    if (nheads <= 0 || head_cols <= 0 || d->M <= 0 || d->N <= 0) return VEDIC_STATUS_BAD_DIM;
+    if (nheads > kMaxHeads) return VEDIC_STATUS_TOO_LARGE;
+    if ((int64_t)nheads * head_cols != d->K) return VEDIC_STATUS_BAD_DIM;
+    if (d->op != VEDIC_OP_NN) return VEDIC_STATUS_BAD_LAYOUT;
+    if (d->in_dtype != VEDIC_DT_F16 && d->in_dtype != VEDIC_DT_F32_F16) return VEDIC_STATUS_BAD_DTYPE;
+    if (d->out_dtype != VEDIC_DT_F32) return VEDIC_STATUS_BAD_DTYPE;
+    if (!d->B || !d->C) return VEDIC_STATUS_NULL_POINTER;
+    if (d->epilogue != VEDIC_EPI_NONE || d->alpha != 1.0f || d->beta != 0.0f || d->colsum || d->preact)
+        return VEDIC_STATUS_BAD_EPILOGUE;
+    if (d->lda < head_cols || d->ldb < d->N || d->ldc < d->N) return VEDIC_STATUS_BAD_LD;
+    if (d->ldc >= kMaxLd) return VEDIC_STATUS_TOO_LARGE;
+    for (int h = 0; h < nheads; ++h)
+        if (!a_heads[h]) return VEDIC_STATUS_NULL_POINTER;
+    const bool amp = d->in_dtype == VEDIC_DT_F32_F16;
+    hipStream_t s = static_cast<hipStream_t>(d->stream);
+
+    bool heads_ok = head_cols % 64 == 0 && d->lda % (amp ? 4 : 8) == 0 && d->lda < (amp ? kMaxLd / 2 : kMaxLd);
+    for (int h = 0; h < nheads && heads_ok; ++h) heads_ok = aligned16(a_heads[h]);
+    const bool b_ok = aligned16(d->B) && d->ldb % 8 == 0 && d->N % 8 == 0 && d->ldb < kMaxLd;
+    if (!heads_ok || !b_ok || d->N <= 64) {
+        // the per-head products themselves
+        const int64_t n = (int64_t)d->M * d->N;
+        hipLaunchKernelGGL(zero_rows_kernel, dim3(ew_blocks(n, 4)), dim3(kEwThreads), 0, s, static_cast<float*>(d->C), d->ldc, d->M, d->N);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return hip_status(e);
+        for (int h = 0; h < nheads; ++h) {
+            vedic_gemm_desc_t g = *d;
+            g.A = a_heads[h];
+            g.K = head_cols;
+            g.B = static_cast<const char*>(d->B) + (int64_t)h * head_cols * d->ldb * 2;
+            g.beta = 1.0f;
+            const int st = gemm_impl(&g, nullptr, 0, 0);
+            if (st != VEDIC_STATUS_OK) return st;
+        }
+        return VEDIC_STATUS_OK;
+    }
+
+    GemmArgs a{};
+    a.B = d->B;
+    a.C = d->C;
+    a.ldb = d->ldb;
+    a.ldc = d->ldc;
+    a.M = d->M;
+    a.N = d->N;
+    a.K = d->K;
+    a.alpha = 1.0f;
+    a.beta = 0.0f;
+    a.epi = 0;
+    a.epi_kind = EK_PLAIN;
+    a.group_m = 8;
+    a.a_head_cols = head_cols;
+    Workspace ws;
+    ws.s = s;
+    _Float16* a16 = nullptr;
+    bool in_kernel_amp = amp;
+    if (amp && d->N > kAmpInKernelMaxN) {
+        // long rows of C: the heads cast once into a packed binary16 A (the
+        // per-head products also cast first at this width)
+        hipError_t e = ws.get(&a16, sizeof(_Float16) * (size_t)d->M * d->K);
+        if (e != hipSuccess) return ws.overflow ? VEDIC_STATUS_TOO_LARGE : hip_status(e);
+        PackSources ps{};
+        for (int h = 0; h < nheads; ++h) ps.p[h] = static_cast<const float*>(a_heads[h]);
+        const int64_t n = (int64_t)d->M * d->K;
+        hipLaunchKernelGGL(cast_pack_f16_kernel, dim3(ew_blocks(n, 4)), dim3(kEwThreads), 0, s, ps, nheads, d->M,
+                           head_cols, d->lda, a16, (int64_t)d->K);
+        e = hipGetLastError();
+        if (e != hipSuccess) return hip_status(e);
+        for (int h = 0; h < nheads; ++h) a.heads[h] = reinterpret_cast<float*>(a16 + (int64_t)h * head_cols);
+        a.lda = d->K;
+        in_kernel_amp = false;
+    } else {
+        for (int h = 0; h < nheads; ++h) a.heads[h] = const_cast<float*>(static_cast<const float*>(a_heads[h]));
+        a.lda = d->lda;
+    }
+    a.A = a.heads[0];
+    a.ksplit = 1;
+    a.kslice = d->K;
+    hipError_t e = launch_gemm_f16_gather(a, in_kernel_amp, s);
+    if (a16) {
+        const hipError_t f = ws.put(a16);
+        if (e == hipSuccess) e = f;
+    }
+    return hip_status(e);
 }
 
 extern "C" int vedic_cast_f16_to_f32(const void* src, float* dst, int64_t n, void* stream) {

@@ -60,6 +60,18 @@ __device__ __forceinline__ float gelu_tanh_grad(float x) {
     return __builtin_fmaf(2.0f * c * t, __builtin_fmaf(k3, x2, 1.0f), sg);
 }
 
+// A 16-byte store whose data registers are left unchanged for four wait
+// states after it issues.  A store of more than 8 bytes reads its data
+// registers after issue, and the gfx940 family needs two wait states before
+// a VALU instruction may overwrite them; the asm statement reads the value
+// after an s_nop 3, so the compiler cannot reuse those registers sooner: twice
+// the minimum.  logos_amd/isa_check.py checks every wide store of the
+// library against that margin at build time.
+__device__ __forceinline__ void store16_hold(float* p, float4_t v) {
+    *reinterpret_cast<float4_t*>(p) = v;
+    asm volatile("s_nop 3" ::"v"(v) : "memory");
+}
+
 // binary16(clamp(v, -65504, 65504)), round to nearest even: the AMP cast of
 // cast_fp32_to_fp16_kernel (cuda/MixedPrecision.cuh:149-161).  fminf/fmaxf
 // return the non-NaN operand, so NaN becomes 65504 as there.
@@ -127,6 +139,13 @@ struct GemmArgs {
     // of C go to heads[h], a row-major [M x head_cols] matrix; head_cols is a
     // multiple of 32, so every 32 x 32 block lies in one head.  fp32 C.
     int head_cols;
+    // Gathered A with head-ordered accumulation (a_head_cols > 0, kernels
+    // instantiated with HO > 0; never together with a scattered C): the
+    // contraction columns [h * a_head_cols, (h + 1) * a_head_cols) of A are
+    // columns 0 .. a_head_cols - 1 of heads[h] (binary16, or fp32 on the AMP
+    // path), rows lda elements apart; each head's product starts from zero
+    // and is added to the running sum in head order.
+    int a_head_cols;
     float* heads[kMaxHeads];
 };
 

@@ -224,7 +224,7 @@ __device__ __forceinline__ void fa_item(const FlashArgs& a, int item, char* t0, 
                 float4_t v;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) v[r] = o[d][4 * gg + r] * inv;
-                *reinterpret_cast<float4_t*>(orow + 32 * d + 8 * gg + 4 * h) = v;
+                store16_hold(orow + 32 * d + 8 * gg + 4 * h, v);
             }
     } else {
         // partial slot: [kFaQ][DH] unnormalised O, then the row maxima and sums
@@ -237,7 +237,7 @@ __device__ __forceinline__ void fa_item(const FlashArgs& a, int item, char* t0, 
                 float4_t v;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) v[r] = o[d][4 * gg + r];
-                *reinterpret_cast<float4_t*>(orow + 32 * d + 8 * gg + 4 * h) = v;
+                store16_hold(orow + 32 * d + 8 * gg + 4 * h, v);
             }
         if (h == 0) {
             slot[kFaQ * DH + 32 * wave + l32] = m_run;
@@ -320,7 +320,7 @@ __global__ void __launch_bounds__(256) flash_merge_kernel(FlashArgs a) {
         M = Mn;
     }
     const float inv = L > 1e-9f ? 1.0f / L : 0.0f;
-    *reinterpret_cast<float4_t*>(a.o[head] + (int64_t)query * DH + 4 * d4) = acc * inv;
+    store16_hold(a.o[head] + (int64_t)query * DH + 4 * d4, acc * inv);
     if (a.lse[head] != nullptr && d4 == 0) a.lse[head][query] = fa_lse(M, L);
 }
 

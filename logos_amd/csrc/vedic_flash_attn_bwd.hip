@@ -229,7 +229,7 @@ flash_bwd_dq_kernel(FlashBwdArgs a) {
             float4_t v;
 #pragma unroll
             for (int r = 0; r < 4; ++r) v[r] = dq[d][4 * gg + r] * a.scale;
-            *reinterpret_cast<float4_t*>(row + 32 * d + 8 * gg + 4 * h) = v;
+            store16_hold(row + 32 * d + 8 * gg + 4 * h, v);
         }
 }
 
@@ -385,8 +385,8 @@ flash_bwd_dkdv_kernel(FlashBwdArgs a) {
                 v[r] = dv[d][4 * gg + r];
                 w[r] = dk[d][4 * gg + r] * a.scale;
             }
-            if constexpr (DO_DV) *reinterpret_cast<float4_t*>(vrow + 32 * d + 8 * gg + 4 * h) = v;
-            if constexpr (DO_DK) *reinterpret_cast<float4_t*>(krow + 32 * d + 8 * gg + 4 * h) = w;
+            if constexpr (DO_DV) store16_hold(vrow + 32 * d + 8 * gg + 4 * h, v);
+            if constexpr (DO_DK) store16_hold(krow + 32 * d + 8 * gg + 4 * h, w);
         }
 }
 

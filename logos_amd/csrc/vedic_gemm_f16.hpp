@@ -262,7 +262,10 @@ constexpr int kSgMfma = 0x008, kSgVmem = 0x010, kSgDsRead = 0x100;
 // no wave blocks on a full texture-address queue while its MFMAs wait.
 // KN < BK / 16: the wave takes only the KN k steps from kk0 on (the
 // contraction of a stage split among a workgroup's waves).
-template <bool A_KC, bool B_KC, int BM, int BN, int BK, int MI, int NI, int NV = 0, int EVERY = 1, int KN = BK / 16>
+// ZF: the stage's first k step starts each accumulator from zero (the
+// previous contents are dropped), as a product whose contraction begins here.
+template <bool A_KC, bool B_KC, int BM, int BN, int BK, int MI, int NI, int NV = 0, int EVERY = 1, int KN = BK / 16,
+          bool ZF = false>
 __device__ __forceinline__ void mfma_stage(const char* la, const char* lb, int ar0, int bc0, int lane,
                                            float16_t (&acc)[MI][NI], int kk0 = 0) {
     constexpr int KS = KN;
@@ -288,7 +291,8 @@ __device__ __forceinline__ void mfma_stage(const char* la, const char* lb, int a
         for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int j = 0; j < NI; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[c][i], bf[c][j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[c][i], bf[c][j],
+                                                                   ZF && kk == 0 ? float16_t{} : acc[i][j], 0, 0, 0);
     }
     if constexpr (NV == 0) {
         __builtin_amdgcn_sched_group_barrier(kSgDsRead, NR, 0);
@@ -351,9 +355,19 @@ __device__ __forceinline__ WorkItem work_of(const GemmArgs& a, int w, int ntiles
     return it;
 }
 
-#define VEDIC_A_TILE(k) \
-    (A_KC ? A + (int64_t)m0 * args.lda + ((k) < K ? (k) : 0) : A + (int64_t)((k) < K ? (k) : 0) * args.lda + m0)
-#define VEDIC_A32_TILE(k) (A32f + (int64_t)m0 * args.lda + ((k) < K ? (k) : 0))
+// A gathered from per-head matrices: the tile of head (k / a_head_cols) at
+// column k mod a_head_cols (k past the range: head 0, column 0).
+template <typename T>
+__device__ __forceinline__ const T* gathered_tile(const GemmArgs& a, int m0, int k) {
+    const int kk = k < a.K ? k : 0;
+    const int h = kk / a.a_head_cols;
+    return reinterpret_cast<const T*>(a.heads[h]) + (int64_t)m0 * a.lda + (kk - h * a.a_head_cols);
+}
+
+#define VEDIC_A_TILE(k)                                                                                      \
+    (HO ? gathered_tile<_Float16>(args, m0, k)                                                               \
+        : A_KC ? A + (int64_t)m0 * args.lda + ((k) < K ? (k) : 0) : A + (int64_t)((k) < K ? (k) : 0) * args.lda + m0)
+#define VEDIC_A32_TILE(k) (HO ? gathered_tile<float>(args, m0, k) : A32f + (int64_t)m0 * args.lda + ((k) < K ? (k) : 0))
 #define VEDIC_B_TILE(k) \
     (B_KC ? B + (int64_t)n0 * args.ldb + ((k) < K ? (k) : 0) : B + (int64_t)((k) < K ? (k) : 0) * args.ldb + n0)
 // The loads of stage kt: A into (la) (an fp32 A into registers, committed
@@ -390,7 +404,13 @@ __device__ __forceinline__ WorkItem work_of(const GemmArgs& a, int w, int ntiles
 // [g KN, (g + 1) KN) of every stage (KN = BK / 16 / WGK), and after the
 // contraction groups 1.. leave their accumulators in the stage buffers for
 // group 0, which adds them in group order and runs the epilogue.
-template <int OP, int BM, int BN, int BK, int ST, int WGM, int WGN, int KIND, int WGK = 1>
+// HO > 0: A gathered from per-head matrices (args.heads, args.a_head_cols, a
+// multiple of BK), and the contraction accumulated head by head: each head's
+// partial product starts from zero and is added to the running sum (fp32,
+// round to nearest) in head order, the bits of one product per head added
+// into a zeroed C one after another.  HO = 1: one stage per head
+// (a_head_cols = BK); HO = 2: a_head_cols / BK stages per head.
+template <int OP, int BM, int BN, int BK, int ST, int WGM, int WGN, int KIND, int WGK = 1, int HO = 0>
 __global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f16_kernel(GemmArgs args) {
     constexpr int WMN = WGM * WGN, NW = WMN * WGK, WM = BM / WGM, WN = BN / WGN, MI = WM / 32, NI = WN / 32;
     constexpr int KN = BK / 16 / WGK;
@@ -405,7 +425,8 @@ __global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f16_kernel(GemmArgs 
     // 256 x 256 tiles: the stage's direct loads are spread one per MFMA instead
     // of issued together (2-3 % faster: fewer waves held at a full
     // texture-address queue); 128 x 128 tiles measured slower that way.
-    constexpr bool kInterleave = BM * BN >= 256 * 256 && WGK == 1;
+    constexpr bool kInterleave = BM * BN >= 256 * 256 && WGK == 1 && HO == 0;
+    static_assert(HO == 0 || (WGK == 1 && (OP == 0 || OP == 3)), "gathered A: NN or AMP, one k group");
 
     // One LDS object per stage (A then B): reads of one stage provably do not
     // alias the direct loads into another.  The compiler follows only a few
@@ -454,12 +475,25 @@ __global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f16_kernel(GemmArgs 
     // epilogue.
     const bool pre_bias = epi_wants_bias<KIND>(args);  // (split-K slices run the plain kind)
     float bias_pre[NI];
+    // stages per head of a gathered A (HO = 2)
+    const int seg = HO == 2 ? args.a_head_cols / BK : 1;
     while (true) {
         float16_t acc[MI][NI];
+        float16_t tot[MI][NI];  // HO: the sum of the finished heads
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
-            for (int j = 0; j < NI; ++j) acc[i][j] = float16_t{};
+            for (int j = 0; j < NI; ++j) {
+                acc[i][j] = float16_t{};
+                tot[i][j] = float16_t{};
+            }
+        // HO: after a head's last stage its partial joins the running sum
+        auto head_done = [&]() {
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NI; ++j) tot[i][j] += acc[i][j];
+        };
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
             const int col = n0 + wn * WN + 32 * j + lane % 32;
@@ -493,9 +527,23 @@ __global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f16_kernel(GemmArgs 
                     // register loads, then the MFMAs, then the conversion into
                     // stage kt - 1's buffer, free since the barrier above
                     VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
-                    if (kt < nk)
-                        mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI, 0, 1, KN>(As[s], Bs[s], wm * WM, wn * WN, lane, acc,
-                                                                            wk * KN);
+                    if (kt < nk) {
+                        if constexpr (HO == 1) {
+                            mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI, 0, 1, KN, true>(As[s], Bs[s], wm * WM, wn * WN,
+                                                                                      lane, acc);
+                            head_done();
+                        } else {
+                            mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI, 0, 1, KN>(As[s], Bs[s], wm * WM, wn * WN, lane,
+                                                                                acc, wk * KN);
+                            if (HO == 2 && (kt + 1) % seg == 0) {
+                                head_done();
+#pragma unroll
+                                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                                    for (int j = 0; j < NI; ++j) acc[i][j] = float16_t{};
+                            }
+                        }
+                    }
                     wait_vmcnt<SB::NLD>();
                     sa.commit(As[sl], wave, lane);
                 } else if constexpr (kInterleave) {
@@ -508,9 +556,23 @@ __global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f16_kernel(GemmArgs 
                     }
                 } else {
                     VEDIC_ISSUE(kt + ST - 1, As[sl], Bs[sl]);
-                    if (kt < nk)
-                        mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI, 0, 1, KN>(As[s], Bs[s], wm * WM, wn * WN, lane, acc,
-                                                                            wk * KN);
+                    if (kt < nk) {
+                        if constexpr (HO == 1) {
+                            mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI, 0, 1, KN, true>(As[s], Bs[s], wm * WM, wn * WN,
+                                                                                      lane, acc);
+                            head_done();
+                        } else {
+                            mfma_stage<A_KC, B_KC, BM, BN, BK, MI, NI, 0, 1, KN>(As[s], Bs[s], wm * WM, wn * WN, lane,
+                                                                                acc, wk * KN);
+                            if (HO == 2 && (kt + 1) % seg == 0) {
+                                head_done();
+#pragma unroll
+                                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                                    for (int j = 0; j < NI; ++j) acc[i][j] = float16_t{};
+                            }
+                        }
+                    }
                 }
             }
         }
@@ -557,6 +619,12 @@ __global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f16_kernel(GemmArgs 
             }
             // (the barrier before the next work item's first loads orders
             // these reads before the buffers are written again)
+        }
+        if constexpr (HO > 0) {
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NI; ++j) acc[i][j] = tot[i][j];
         }
         const int row0 = m0 + wm * WM, col0 = n0 + wn * WN;
         // split-K: this slice's raw partial goes to its own slab of the workspace
@@ -709,6 +777,10 @@ int device_cu_count();
 // host stub).
 #define VEDIC_F16_KERNEL(OP, Cfg, KIND) \
     template __global__ void gemm_f16_kernel<OP, Cfg::BM, Cfg::BN, Cfg::BK, Cfg::ST, Cfg::WGM, Cfg::WGN, KIND, Cfg::WGK>(GemmArgs)
+// The gathered-A, head-ordered kernels (plain epilogue).
+#define VEDIC_F16_KERNEL_HO(OP, Cfg, HO)                                                                        \
+    template __global__ void gemm_f16_kernel<OP, Cfg::BM, Cfg::BN, Cfg::BK, Cfg::ST, Cfg::WGM, Cfg::WGN, EK_PLAIN, \
+                                             Cfg::WGK, HO>(GemmArgs)
 #define VEDIC_F16_INSTANTIATE(OP, Cfg)            \
     VEDIC_F16_KERNEL(OP, Cfg, EK_PLAIN);          \
     VEDIC_F16_KERNEL(OP, Cfg, EK_BIAS);           \
@@ -766,7 +838,7 @@ inline int f16_tile_config(int M, int N, int cus) {
     return best;
 }
 
-template <int OP, class Cfg, int KIND>
+template <int OP, class Cfg, int KIND, int HO = 0>
 static hipError_t launch_f16(GemmArgs a, hipStream_t s) {
     a.tiles_m = (a.M + Cfg::BM - 1) / Cfg::BM;
     a.tiles_n = (a.N + Cfg::BN - 1) / Cfg::BN;
@@ -778,7 +850,7 @@ static hipError_t launch_f16(GemmArgs a, hipStream_t s) {
     const int nwork = a.tiles_m * a.tiles_n * a.ksplit;
     const int slots = device_cu_count() * Cfg::PER_CU;
     const int grid = nwork < slots ? nwork : slots;
-    hipLaunchKernelGGL((gemm_f16_kernel<OP, Cfg::BM, Cfg::BN, Cfg::BK, Cfg::ST, Cfg::WGM, Cfg::WGN, KIND, Cfg::WGK>),
+    hipLaunchKernelGGL((gemm_f16_kernel<OP, Cfg::BM, Cfg::BN, Cfg::BK, Cfg::ST, Cfg::WGM, Cfg::WGN, KIND, Cfg::WGK, HO>),
                        dim3(grid), dim3(Cfg::WGM * Cfg::WGN * Cfg::WGK * 64), 0, s, a);
     return hipGetLastError();
 }

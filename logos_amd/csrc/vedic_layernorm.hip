@@ -181,7 +181,7 @@ __global__ void __launch_bounds__(kLnThreads)
             float4_t y;
 #pragma unroll
             for (int e = 0; e < 4; ++e) y[e] = gv[e] * (v[k][e] - mean) * inv + bv[e];
-            if constexpr (OUT32) reinterpret_cast<float4_t*>(Y + row * d)[j] = y;
+            if constexpr (OUT32) store16_hold(Y + row * d + 4 * j, y);
             if constexpr (OUT16) {
                 half4_t h;
 #pragma unroll

@@ -34,7 +34,7 @@ __all__ = [
     "OP_NN", "OP_NT", "OP_TN", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU", "EPI_GELU", "EPI_GELU_BWD",
     "EPI_RESIDUAL", "EPI_BIAS_RESIDUAL", "gemm_bias_residual", "layernorm", "layernorm_fp16",
     "gemm", "vedic_gemm", "vedic_gemm_bias", "gemm_fp16_fp32out", "gemm_fp16_fp16out",
-    "gemm_bias_gelu", "amp_gemm", "gemm_nt", "gemm_tn", "gemm_nt_gelu_bwd", "bias_grad", "gemm_scatter",
+    "gemm_bias_gelu", "amp_gemm", "gemm_nt", "gemm_tn", "gemm_nt_gelu_bwd", "bias_grad", "gemm_scatter", "gemm_gather", "cast_stack_fp16",
     "cast_pack_fp16", "add_bias", "gelu_",
     "cast_fp32_to_fp16",
     "cast_fp16_to_fp32", "verify", "gemm_checked", "VerifyResult", "uses_vendor_blas", "backend_name",
@@ -299,6 +299,64 @@ def cast_pack_fp16(srcs: list[torch.Tensor], out: torch.Tensor | None = None) ->
         raise ValueError("out must be float16 [rows x nsrc*cols]")
     ptrs = (ctypes.c_void_p * len(srcs))(*[t.data_ptr() for t in srcs])
     _check(_lib.load().vedic_cast_pack_f16(ptrs, len(srcs), rows, cols, out.data_ptr(), ld, _stream()))
+    return out
+
+
+def cast_stack_fp16(srcs: list[torch.Tensor], out: torch.Tensor | None = None) -> torch.Tensor:
+    """binary16 copy of fp32 [rows x cols] matrices stacked by rows
+    (out[i*rows:(i+1)*rows] = srcs[i]), with the reference cast's clamp: a
+    layer's per-head W_O blocks as the B operand of gemm_gather."""
+    if not srcs:
+        raise ValueError("no sources")
+    rows, cols = srcs[0].shape
+    for t in srcs:
+        if tuple(t.shape) != (rows, cols) or t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda:
+            raise ValueError(f"every source must be a contiguous float32 [{rows} x {cols}] GPU matrix")
+    if out is None:
+        out = torch.empty((len(srcs) * rows, cols), dtype=torch.float16, device=srcs[0].device)
+    r, c, ld = _mat(out, "out")
+    if r != len(srcs) * rows or c != cols or out.dtype != torch.float16:
+        raise ValueError("out must be float16 [nsrc*rows x cols]")
+    ptrs = (ctypes.c_void_p * len(srcs))(*[t.data_ptr() for t in srcs])
+    _check(_lib.load().vedic_cast_stack_f16(ptrs, len(srcs), rows, cols, out.data_ptr(), ld, _stream()))
+    return out
+
+
+def gemm_gather(heads: list[torch.Tensor], W: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """C = sum over h, in head order, of heads[h] . W[h*hc:(h+1)*hc] onto a
+    zeroed C (each head's product from zero in fp32): the reference's
+    per-head amp_gemm(head_out, W_O[h]) + residual_add_kernel loop
+    (cuda/ModelGPU.cu:976-986) in one launch, bit for bit.  heads: equal
+    [M x hc] float16 or float32 GPU matrices (float32: rounded to binary16 as
+    they are read, the AMP path); W: float16 [nheads*hc x N] (cast_stack_fp16);
+    out: float32 [M x N]."""
+    if not heads:
+        raise ValueError("no heads")
+    dt = heads[0].dtype
+    if dt not in (torch.float16, torch.float32):
+        raise ValueError("heads must be float16 or float32")
+    M, hc, lda = _mat(heads[0], "heads[0]")
+    for t in heads:
+        if tuple(t.shape) != (M, hc) or t.dtype != dt or t.stride() != heads[0].stride() or not t.is_cuda:
+            raise ValueError(f"every head must be a {dt} [{M} x {hc}] GPU matrix with the same strides")
+    K, N, ldb = _mat(W, "W")
+    if W.dtype != torch.float16:
+        raise ValueError("W must be float16")
+    if K != len(heads) * hc:
+        raise ValueError(f"VedicGEMM: W has {K} rows, the heads {len(heads)} x {hc} columns")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=W.device)
+    Mo, No, ldc = _mat(out, "out")
+    if (Mo, No) != (M, N) or out.dtype != torch.float32:
+        raise ValueError(f"out must be float32 [{M} x {N}]")
+    d = _lib.GemmDesc(
+        op=OP_NN, in_dtype=DT_F16 if dt == torch.float16 else _lib.DT_F32_F16, out_dtype=DT_F32, M=M, N=N, K=K,
+        A=None, lda=lda, B=W.data_ptr(), ldb=ldb, C=out.data_ptr(), ldc=ldc,
+        alpha=1.0, beta=0.0, bias=None, epilogue=EPI_NONE, preact=None, ld_preact=0, stream=_stream(),
+        colsum=None, colsum_beta=0.0,
+    )
+    ptrs = (ctypes.c_void_p * len(heads))(*[t.data_ptr() for t in heads])
+    _check(_lib.load().vedic_gemm_gather(ctypes.byref(d), ptrs, len(heads), hc))
     return out
 
 

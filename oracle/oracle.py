@@ -173,6 +173,26 @@ def f32_to_f16_bits(x) -> np.ndarray:
     return out
 
 
+def gemm_heads_ordered(heads, W, order=None) -> np.ndarray:
+    """The reference's attention-output projection in fp32: concat zeroed
+    (cudaMemset, cuda/ModelGPU.cu:889-890), then for each head h in order
+    concat += head_out[h] . W_O[h] (amp_gemm then residual_add_kernel,
+    :976-986 and :57-60), each head's product computed on its own -- here by
+    the restated CPU vedic_gemm (include/VedicGEMM.hpp:25-54) -- and added
+    with one fp32 rounding.  heads: [M x hc] matrices; W: [len(heads) hc x N],
+    head h's rows h hc .. (h + 1) hc - 1.  order: the heads' order of
+    addition (default ascending; only the tests pass another, to show that
+    the order shows in the bits)."""
+    heads = [_f32(h) for h in heads]
+    W = _f32(W)
+    hc = heads[0].shape[1]
+    M, N = heads[0].shape[0], W.shape[1]
+    C = np.zeros((M, N), dtype=np.float32)
+    for h in (range(len(heads)) if order is None else order):
+        C = (C + vedic_gemm(heads[h], W[h * hc:(h + 1) * hc])).astype(np.float32)
+    return C
+
+
 def f16_round(x) -> np.ndarray:
     """fp32 values rounded through binary16 (clamp + RNE) and widened back."""
     bits = f32_to_f16_bits(x)

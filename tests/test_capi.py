@@ -142,3 +142,43 @@ def test_flash_attention_refusals():
     # the sparse mask needs a stride, and a null operand is refused
     assert f(p, p, p, p, p, 256, 96, 0.125, 1, 1, 8, 0, None) == _lib.STATUS_BAD_DIM
     assert f(p, None, p, p, p, 256, 96, 0.125, 1, 0, 0, 1, None) == _lib.STATUS_NULL_POINTER
+
+
+@pytest.mark.parametrize("kw,nheads,hc,status", [
+    (dict(K=8), 2, 4, _lib.STATUS_OK),          # accepted shape (not run: checked below with a bad head)
+    (dict(K=8), 2, 3, _lib.STATUS_BAD_DIM),     # nheads * head_cols != K
+    (dict(K=8), 0, 4, _lib.STATUS_BAD_DIM),
+    (dict(K=8), 2, 0, _lib.STATUS_BAD_DIM),
+    (dict(K=8 * 65), 65, 8, _lib.STATUS_TOO_LARGE),
+    (dict(K=8, op=1), 2, 4, _lib.STATUS_BAD_LAYOUT),
+    (dict(K=8, in_dtype=0), 2, 4, _lib.STATUS_BAD_DTYPE),   # binary16 or fp32 heads with a binary16 B
+    (dict(K=8, in_dtype=1, out_dtype=1), 2, 4, _lib.STATUS_BAD_DTYPE),
+    (dict(K=8, beta=1.0), 2, 4, _lib.STATUS_BAD_EPILOGUE),  # C is defined from zero
+    (dict(K=8, alpha=2.0), 2, 4, _lib.STATUS_BAD_EPILOGUE),
+    (dict(K=8, epilogue=1, bias=16), 2, 4, _lib.STATUS_BAD_EPILOGUE),
+    (dict(K=8, lda=3), 2, 4, _lib.STATUS_BAD_LD),           # heads' leading dimension < head_cols
+    (dict(K=8, ldc=3), 2, 4, _lib.STATUS_BAD_LD),
+    (dict(K=8, C=None), 2, 4, _lib.STATUS_NULL_POINTER),
+    (dict(K=8, B=None), 2, 4, _lib.STATUS_NULL_POINTER),
+])
+def test_gather_validation(kw, nheads, hc, status):
+    """vedic_gemm_gather's argument checks, before any launch (a null head is
+    refused last, so the accepted case returns NULL_POINTER without running)."""
+    kw = dict(dict(in_dtype=1), **kw)
+    d = _desc(**kw)
+    n = max(nheads, 1)
+    heads = (ctypes.c_void_p * n)(*([16] * (n - 1) + [None]))
+    want = _lib.STATUS_NULL_POINTER if status == _lib.STATUS_OK else status
+    assert _lib.load().vedic_gemm_gather(ctypes.byref(d), heads, nheads, hc) == want
+    assert _lib.load().vedic_gemm_gather(None, heads, nheads, hc) == _lib.STATUS_NULL_POINTER
+
+
+def test_cast_stack_validation():
+    lib = _lib.load()
+    srcs = (ctypes.c_void_p * 2)(16, 16)
+    assert lib.vedic_cast_stack_f16(srcs, 0, 4, 4, 16, 4, None) == _lib.STATUS_BAD_DIM
+    assert lib.vedic_cast_stack_f16(srcs, 65, 4, 4, 16, 4, None) == _lib.STATUS_TOO_LARGE
+    assert lib.vedic_cast_stack_f16(srcs, 2, 4, 4, None, 4, None) == _lib.STATUS_NULL_POINTER
+    assert lib.vedic_cast_stack_f16(srcs, 2, 4, 4, 16, 3, None) == _lib.STATUS_BAD_LD
+    nul = (ctypes.c_void_p * 2)(16, None)
+    assert lib.vedic_cast_stack_f16(nul, 2, 4, 4, 16, 4, None) == _lib.STATUS_NULL_POINTER

@@ -128,6 +128,53 @@ def test_threads_sharing_a_stream():
             assert torch.equal(g, r)
 
 
+HIP_STREAM_PER_THREAD = 2  # hipStreamPerThread ((hipStream_t)2, hip_runtime_api.h)
+
+
+def test_threads_on_their_per_thread_streams():
+    """Host threads passing the hipStreamPerThread handle each run on their
+    own stream; the library keeps their workspace blocks apart (one handle
+    value, several streams), so the split products, whose slices live in
+    the block, match the single-stream results bit for bit.  Each thread
+    releases its block before it ends."""
+    vedic = V()
+    lib = _lib.load()
+    rng = np.random.default_rng(4)
+    M, N, K = 256, 256, 4096
+    cases = [split_case(rng, M, N, K) for _ in range(4)]
+    refs = [run_split(vedic, *c) for c in cases]
+    outs = [[torch.empty((M, N), device="cuda") for _ in range(8)] for _ in cases]
+    torch.cuda.synchronize()
+    errors = []
+    barrier = threading.Barrier(len(cases))
+
+    def work(t):
+        a, b = cases[t]
+        barrier.wait()
+        for rep in range(8):
+            d = _lib.GemmDesc(op=0, in_dtype=1, out_dtype=0, M=M, N=N, K=K, A=a.data_ptr(), lda=K, B=b.data_ptr(),
+                              ldb=N, C=outs[t][rep].data_ptr(), ldc=N, alpha=1.0, beta=0.0,
+                              stream=HIP_STREAM_PER_THREAD)
+            st = lib.vedic_gemm(ctypes.byref(d))
+            if st != 0:
+                errors.append(st)
+        torch.cuda.synchronize()
+        st = lib.vedic_workspace_release(HIP_STREAM_PER_THREAD)
+        if st != 0:
+            errors.append(st)
+
+    threads = [threading.Thread(target=work, args=(t,)) for t in range(len(cases))]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    torch.cuda.synchronize()
+    assert not errors, [_lib.status_string(e) for e in errors]
+    for t, r in enumerate(refs):
+        for g in outs[t]:
+            assert torch.equal(g, r)
+
+
 def test_checked_gemm_with_work_queued_ahead_and_threads():
     """vedic_gemm_checked returns once its last kernel has published the
     result in host memory (polled, with a stream synchronisation as the

@@ -606,3 +606,43 @@ def test_layernorm_oracle_properties():
     c, s = 4.0, -7.0
     Y2 = o.layernorm_f64(c * X + s, np.ones(257), np.zeros(257), eps=eps * c * c)
     assert np.allclose(Y, Y2, rtol=0, atol=1e-12)
+
+
+# ------------------------------------------- head-ordered attention-output sum
+
+def test_heads_ordered_one_head_is_vedic_gemm():
+    rng = np.random.default_rng(5)
+    A = rng.standard_normal((37, 64), dtype=np.float32)
+    W = rng.standard_normal((64, 50), dtype=np.float32)
+    assert np.array_equal(o.gemm_heads_ordered([A], W), o.vedic_gemm(A, W))
+
+
+def test_heads_ordered_small_integers_exact():
+    """Integer products whose sums stay below 2^24: every rounding is exact,
+    so the ordered sum equals the integer product of the concatenated heads."""
+    rng = np.random.default_rng(6)
+    heads = [rng.integers(-8, 9, size=(19, 16)).astype(np.float32) for _ in range(5)]
+    W = rng.integers(-8, 9, size=(80, 23)).astype(np.float32)
+    want = np.concatenate(heads, axis=1).astype(np.int64) @ W.astype(np.int64)
+    assert np.array_equal(o.gemm_heads_ordered(heads, W), want.astype(np.float32))
+
+
+def test_heads_ordered_rounds_each_head_in_order():
+    """Head products 1, 2^-24, 2^-24: added in head order onto zero, each add
+    rounds to nearest even back to 1 (1 + 2^-24 is a tie between 1 and
+    1 + 2^-23); the last two first would give 1 + 2^-23.  The order of
+    addition is visible in the bits, and the restatement takes the heads'."""
+    one = np.ones((1, 1), np.float32)
+    heads = [one, one, one]
+    W = np.array([[1.0], [2.0 ** -24], [2.0 ** -24]], np.float32)
+    assert o.gemm_heads_ordered(heads, W)[0, 0] == np.float32(1.0)
+    assert o.gemm_heads_ordered(heads, W, order=[2, 1, 0])[0, 0] == np.float32(1.0 + 2.0 ** -23)
+
+
+def test_heads_ordered_within_fp32_bound():
+    rng = np.random.default_rng(7)
+    heads = [rng.standard_normal((33, 64), dtype=np.float32) for _ in range(4)]
+    W = (rng.standard_normal((256, 40), dtype=np.float32) * np.float32(0.02))
+    got = o.gemm_heads_ordered(heads, W)
+    want, absdot = o.gemm_f64(o.NN, np.concatenate(heads, axis=1), W)
+    assert o.componentwise_ratio(got, want, absdot) <= 256 * o.U32

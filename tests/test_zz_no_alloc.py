@@ -99,3 +99,34 @@ def test_noalloc_refuses_what_does_not_fit():
     (c1, _), (c2, _) = _pair(lib, "splitk_tn_f16", 1024, 1024, 8192, seed=5)
     assert torch.equal(c1, c2)
     assert lib.vedic_gemm_noalloc(None) == _lib.STATUS_NULL_POINTER
+
+
+def test_noalloc_two_streams_ordered_by_an_event():
+    """Calls on two streams share the region; ordered on the GPU by an event
+    (the second stream waits for the first call), both match vedic_gemm."""
+    lib = _lib.load()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(77)
+    cases = []
+    for (M, N, K) in ((1024, 1024, 8192), (512, 256, 4096)):  # both split over K into the region
+        A = torch.randn(K, M, generator=g, device="cuda").half()
+        B = (torch.randn(K, N, generator=g, device="cuda") * 1e-2).half()
+        cases.append((M, N, K, A, B, torch.zeros(M, N, device="cuda"), torch.zeros(M, N, device="cuda")))
+    torch.cuda.synchronize()
+    ev = torch.cuda.Event()
+    for i, (stream, (M, N, K, A, B, C, _)) in enumerate(zip((s1, s2), cases)):
+        print(f"noalloc stream {i} {M}x{N}x{K}", flush=True)
+        with torch.cuda.stream(stream):
+            if i == 1:
+                stream.wait_event(ev)
+            rc = _run(lib.vedic_gemm_noalloc, _lib.OP_TN, _lib.DT_F16, M, N, K, A, B, C)
+            assert rc == _lib.STATUS_OK, _lib.status_string(rc)
+            if i == 0:
+                ev.record(stream)
+    torch.cuda.synchronize()
+    for M, N, K, A, B, C, Cw in cases:
+        assert _run(lib.vedic_gemm, _lib.OP_TN, _lib.DT_F16, M, N, K, A, B, Cw) == _lib.STATUS_OK
+    torch.cuda.synchronize()
+    for M, N, K, A, B, C, Cw in cases:
+        assert torch.equal(C, Cw), f"{M}x{N}x{K}: C differs from vedic_gemm"
