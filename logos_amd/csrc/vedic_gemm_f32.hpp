@@ -461,14 +461,25 @@ struct CfgF32WaveK {
 
 static_assert(CfgF32Narrow::BN == 64, "f32_small_tiles assumes the narrow tile's 64 columns");
 
+// The same products in NN on the decode kernel's barrier-free pipeline
+// (vedic_gemm_skinny.hip): 32 x 64 row blocks, each wave its own K quarter
+// (512 x 1024 x 1024: 12.2-13.1 us against 15.9-16.5 us on the wave-split
+// tiles).  NT keeps the wave-split tiles (its B rows are K-contiguous).
+hipError_t launch_gemm_f32_rowblocks(const GemmArgs& a, hipStream_t s);
+#ifndef VEDIC_F32_ROWBLOCKS
+#define VEDIC_F32_ROWBLOCKS 1
+#endif
+
 // Narrow tiles when N fits one 64-wide tile column; small ones when 128 x 128
 // tiles would leave most CUs idle.
 template <int OP>
 hipError_t launch_gemm_f32_direct_op(const GemmArgs& a, hipStream_t s) {
     if (a.N <= CfgF32Narrow::BN) return launch_f32_kind<OP, CfgF32Narrow>(a, s);
     if constexpr (OP != 2) {  // (TN's A is M-contiguous: its LDS rows need at least 64 of M)
-        if (a.ksplit <= 1 && f32_wave_split(a.M, a.N, device_cu_count()))
+        if (a.ksplit <= 1 && f32_wave_split(a.M, a.N, device_cu_count())) {
+            if (OP == 0 && VEDIC_F32_ROWBLOCKS) return launch_gemm_f32_rowblocks(a, s);
             return launch_f32_kind<OP, CfgF32WaveK>(a, s);
+        }
     }
     if (f32_small_tiles(a.M, a.N, device_cu_count())) return launch_f32_kind<OP, CfgF32Small>(a, s);
     return launch_f32_kind<OP, CfgF32>(a, s);

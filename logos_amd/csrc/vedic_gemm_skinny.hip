@@ -37,8 +37,12 @@
 
 namespace vedic {
 
-constexpr int kSkStages = 4;     // stages in flight per wave
-constexpr int kSkStage = 8192;   // bytes per stage per wave: 4 KiB of A + 4 KiB of B
+// Every operand type gives: BK (contraction values per stage), L (direct-load
+// instructions per stage and wave), ST (stages in flight per wave), STAGE
+// (bytes per stage and wave), NB (32-column blocks per workgroup),
+// kUniformRounds, init() and issue() for its loads and consume() for the
+// MFMAs of one stage.  A workgroup computes rows m0 .. m0 + 31 (m0 = 32
+// blockIdx.y) of columns n0 .. n0 + 32 NB - 1.
 
 // fp16 operands, 64-deep stages.  Direct loads without branches: each lane
 // keeps its byte offset and the first contraction index of its chunk, and an
@@ -50,18 +54,19 @@ template <int NA>
 struct SkinnyF16 {
     static constexpr int BK = 64;
     static constexpr int L = NA + 4;  // direct-load instructions per stage per wave
+    static constexpr int ST = 4, STAGE = 8192, NB = 1;  // 4 KiB of A + 4 KiB of B per stage
     static constexpr bool kUniformRounds = false;
     using T = _Float16;
     uint32_t aoff[4], boff[4];
     int ak[4], bk[4];
-    __device__ __forceinline__ void init(const GemmArgs& a, int n0, int lane) {
+    __device__ __forceinline__ void init(const GemmArgs& a, int m0, int n0, int lane) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // A: 32 rows x 8 chunks of 8 k (KC layout, rows of 128 bytes)
             const int q = i * 64 + lane;
             const int row = q >> 3;
             const int c = (q & 7) ^ swz_kc<8>(row);
-            aoff[i] = row < a.M ? (uint32_t)(row * a.lda * 2 + c * 16) : kOob;
+            aoff[i] = m0 + row < a.M ? (uint32_t)(row * a.lda * 2 + c * 16) : kOob;
             ak[i] = 8 * c;
             // B: 64 k rows x 4 chunks of 8 columns (MC layout, rows of 64 bytes)
             const int k = q >> 2, cb = q & 3;
@@ -71,8 +76,8 @@ struct SkinnyF16 {
         }
     }
     // k0 < K; krem = contraction values left in the wave's range (<= 0: none)
-    __device__ __forceinline__ void issue(const GemmArgs& a, int k0, int krem, char* dst) const {
-        const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(static_cast<const T*>(a.A) + k0);
+    __device__ __forceinline__ void issue(const GemmArgs& a, int m0, int k0, int krem, char* dst) const {
+        const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(static_cast<const T*>(a.A) + (int64_t)m0 * a.lda + k0);
         const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(static_cast<const T*>(a.B) + (int64_t)k0 * a.ldb);
 #pragma unroll
         for (int i = 0; i < NA; ++i)
@@ -83,82 +88,99 @@ struct SkinnyF16 {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(dst + 4096 + i * 1024), 16,
                                                      bk[i] < krem ? boff[i] : kOob, 0, 0, 0);
     }
-    __device__ __forceinline__ static void consume(const char* la, int lane, float16_t& acc) {
+    __device__ __forceinline__ static void consume(const char* la, int lane, float16_t (&acc)[NB]) {
 #pragma unroll
         for (int kk = 0; kk < BK / 16; ++kk) {
             const half8_t af = read_frag<true, 32, BK>(la, 0, kk, lane);
             const half8_t bf = read_frag<false, 32, BK>(la + 4096, 0, kk, lane);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc, 0, 0, 0);
+            acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc[0], 0, 0, 0);
         }
     }
 };
 
-// fp32 operands, 32-deep stages; NA as for fp16.
-template <int NA>
+// fp32 operands, 32-deep stages; NA as for fp16.  NB_ 32-column blocks of B
+// per workgroup, each its own 4 KiB B region of the stage laid out as for
+// one block; the A fragment of each k step feeds all NB_ blocks' MFMAs.
+// NB_ = 1: the decode kernel (four stages in flight per wave); NB_ = 2: the
+// 32 x 64 row blocks of small fp32 products (three stages).
+template <int NA, int NB_ = 1, int ST_ = 4>
 struct SkinnyF32 {
     static constexpr int BK = 32;
-    static constexpr int L = NA + 4;
+    static constexpr int NB = NB_;
+    static constexpr int L = NA + 4 * NB;
+    static constexpr int ST = ST_, STAGE = 4096 * (1 + NB);
     static constexpr bool kUniformRounds = true;
     using T = float;
     // Instruction i of a side fills bytes [1024 i, 1024 (i + 1)) of the
     // side's 4 KiB; lane q lands at +16 q.
-    uint32_t aoff[4], boff[4];
-    int ak[4], bk[4];
-    __device__ __forceinline__ void init(const GemmArgs& a, int n0, int lane) {
+    uint32_t aoff[4], boff[4 * NB];
+    int ak[4], bk[4 * NB];
+    __device__ __forceinline__ void init(const GemmArgs& a, int m0, int n0, int lane) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = 8 * i + (lane >> 3);
             const int c = (lane & 7) ^ swz_kc<8>(row);
-            aoff[i] = row < a.M ? (uint32_t)(row * a.lda * 4 + c * 16) : kOob;
+            aoff[i] = m0 + row < a.M ? (uint32_t)(row * a.lda * 4 + c * 16) : kOob;
             ak[i] = 4 * c;
-            const int j = lane >> 3;  // LDS row 8 i + j holds k row 8 i + (j odd ? 4 + j/2 : j/2)
-            const int k = 8 * i + ((j & 1) ? 4 + (j >> 1) : (j >> 1));
-            const int col = n0 + 4 * (lane & 7);
-            boff[i] = col + 4 <= a.N ? (uint32_t)((int64_t)k * a.ldb * 4 + col * 4) : kOob;
-            bk[i] = k;
         }
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int j = lane >> 3;  // LDS row 8 i + j holds k row 8 i + (j odd ? 4 + j/2 : j/2)
+                const int k = 8 * i + ((j & 1) ? 4 + (j >> 1) : (j >> 1));
+                const int col = n0 + 32 * b + 4 * (lane & 7);
+                boff[4 * b + i] = col + 4 <= a.N ? (uint32_t)((int64_t)k * a.ldb * 4 + col * 4) : kOob;
+                bk[4 * b + i] = k;
+            }
     }
-    __device__ __forceinline__ void issue(const GemmArgs& a, int k0, int krem, char* dst) const {
-        const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(static_cast<const T*>(a.A) + k0);
+    __device__ __forceinline__ void issue(const GemmArgs& a, int m0, int k0, int krem, char* dst) const {
+        const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(static_cast<const T*>(a.A) + (int64_t)m0 * a.lda + k0);
         const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(static_cast<const T*>(a.B) + (int64_t)k0 * a.ldb);
 #pragma unroll
         for (int i = 0; i < NA; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(dst + i * 1024), 16,
                                                      ak[i] + 4 <= krem ? aoff[i] : kOob, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4 * NB; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(dst + 4096 + i * 1024), 16,
                                                      bk[i] < krem ? boff[i] : kOob, 0, 0, 0);
     }
-    __device__ __forceinline__ static void consume(const char* la, int lane, float16_t& acc) {
+    __device__ __forceinline__ static void consume(const char* la, int lane, float16_t (&acc)[NB]) {
         const int l32 = lane & 31, h = lane >> 5;
-        const char* lb = la + 4096;
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
             const float4_t av =
                 *reinterpret_cast<const float4_t*>(la + l32 * 128 + (((2 * cc + h) ^ swz_kc<8>(l32)) << 4));
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                // k = 8 cc + 4 h + s sits at LDS row 8 cc + 2 s + h
-                const float bv = *reinterpret_cast<const float*>(lb + (8 * cc + 2 * s + h) * 128 + l32 * 4);
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s], bv, acc, 0, 0, 0);
-            }
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    // k = 8 cc + 4 h + s sits at LDS row 8 cc + 2 s + h of block b's region
+                    const float bv =
+                        *reinterpret_cast<const float*>(la + 4096 * (1 + b) + (8 * cc + 2 * s + h) * 128 + l32 * 4);
+                    acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s], bv, acc[b], 0, 0, 0);
+                }
         }
     }
 };
 
 template <class Sk, int KIND>
 __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs a) {
-    constexpr int BK = Sk::BK, ST = kSkStages, STAGE = kSkStage, L = Sk::L;
+    constexpr int BK = Sk::BK, ST = Sk::ST, STAGE = Sk::STAGE, L = Sk::L, NB = Sk::NB;
+    static_assert(ST >= 2 && ST <= 4, "two to four stages");
+    static_assert((ST - 1) * L < 64, "vmcnt range");
+    static_assert(4 * NB * 16 * 64 * 4 <= 4 * STAGE, "the partial sums fit the first stage object");
     __shared__ __attribute__((aligned(1024))) char s0[4 * STAGE];
     __shared__ __attribute__((aligned(1024))) char s1[4 * STAGE];
-    __shared__ __attribute__((aligned(1024))) char s2[4 * STAGE];
-    __shared__ __attribute__((aligned(1024))) char s3[4 * STAGE];
-    char* const Ss[ST] = {s0, s1, s2, s3};
+    __shared__ __attribute__((aligned(1024))) char s2[ST > 2 ? 4 * STAGE : 16];
+    __shared__ __attribute__((aligned(1024))) char s3[ST > 3 ? 4 * STAGE : 16];
+    char* const Ss[4] = {s0, s1, s2, s3};
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int n0 = blockIdx.x * 32;
+    const int n0 = blockIdx.x * 32 * NB;
+    const int m0 = blockIdx.y * 32;
     const int K = a.K;
     // contiguous K quarter of this wave, whole stages
     const int kq = ((K + 4 * BK - 1) / (4 * BK)) * BK;
@@ -168,13 +190,15 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs a) {
     const int nround = max(1, (ke - kb + ST * BK - 1) / (ST * BK));
 
     Sk sk;
-    sk.init(a, n0, lane);
+    sk.init(a, m0, n0, lane);
     auto issue = [&](int st, char* buf) {
         const int k0 = kb + st * BK;
-        sk.issue(a, k0 < K ? k0 : 0, ke - k0, buf + wave * STAGE);
+        sk.issue(a, m0, k0 < K ? k0 : 0, ke - k0, buf + wave * STAGE);
     };
 
-    float16_t acc = float16_t{};
+    float16_t acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = float16_t{};
 #pragma unroll
     for (int st = 0; st < ST; ++st) issue(st, Ss[st]);
     // Every round but the last refills each stage after reading it.  The
@@ -200,9 +224,9 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs a) {
     } else {
 #pragma unroll
         for (int sb = 0; sb < ST; ++sb) {
-            if (sb == 0) wait_vmcnt<3 * L>();
-            else if (sb == 1) wait_vmcnt<2 * L>();
-            else if (sb == 2) wait_vmcnt<L>();
+            if (sb == ST - 4) wait_vmcnt<(ST > 3 ? 3 : 0) * L>();
+            else if (sb == ST - 3) wait_vmcnt<(ST > 2 ? 2 : 0) * L>();
+            else if (sb == ST - 2) wait_vmcnt<L>();
             else wait_vmcnt<0>();
             Sk::consume(Ss[sb] + wave * STAGE, lane, acc);
         }
@@ -212,19 +236,23 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs a) {
     __syncthreads();
     float* red = reinterpret_cast<float*>(s0);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) red[(wave * 16 + e) * 64 + lane] = acc[e];
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) red[((wave * NB + b) * 16 + e) * 64 + lane] = acc[b][e];
     __syncthreads();
     if (wave != 0) return;
-    float16_t sum[1][1];
+    float16_t sum[1][NB];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        float v = red[e * 64 + lane];
-        v += red[(16 + e) * 64 + lane];
-        v += red[(32 + e) * 64 + lane];
-        v += red[(48 + e) * 64 + lane];
-        sum[0][0][e] = v;
-    }
-    epilogue<KIND, true, 1, 1>(a, a.C, sum, 0, n0, lane);
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            float v = red[(b * 16 + e) * 64 + lane];
+            v += red[((NB + b) * 16 + e) * 64 + lane];
+            v += red[((2 * NB + b) * 16 + e) * 64 + lane];
+            v += red[((3 * NB + b) * 16 + e) * 64 + lane];
+            sum[0][b][e] = v;
+        }
+    epilogue<KIND, true, 1, NB>(a, a.C, sum, m0, n0, lane);
 }
 
 #define VEDIC_SKINNY_KERNELS(Sk)                                \
@@ -237,11 +265,19 @@ VEDIC_SKINNY_KERNELS(SkinnyF16<4>);
 VEDIC_SKINNY_KERNELS(SkinnyF32<1>);
 VEDIC_SKINNY_KERNELS(SkinnyF32<2>);
 VEDIC_SKINNY_KERNELS(SkinnyF32<4>);
+#ifndef VEDIC_F32_ROWS_NB
+#define VEDIC_F32_ROWS_NB 2
+#endif
+#ifndef VEDIC_F32_ROWS_ST
+#define VEDIC_F32_ROWS_ST 2
+#endif
+typedef SkinnyF32<4, VEDIC_F32_ROWS_NB, VEDIC_F32_ROWS_ST> SkinnyF32Rows;
+VEDIC_SKINNY_KERNELS(SkinnyF32Rows);
 #undef VEDIC_SKINNY_KERNELS
 
 template <class Sk>
 static hipError_t launch_skinny(const GemmArgs& a, hipStream_t s) {
-    const dim3 grid((a.N + 31) / 32);
+    const dim3 grid((a.N + 32 * Sk::NB - 1) / (32 * Sk::NB), (a.M + 31) / 32);
     if (a.epi_kind == EK_PLAIN)
         hipLaunchKernelGGL((gemm_skinny_kernel<Sk, EK_PLAIN>), grid, dim3(256), 0, s, a);
     else if (a.epi_kind == EK_BIAS)
@@ -265,6 +301,19 @@ hipError_t launch_gemm_f32_skinny(const GemmArgs& a, hipStream_t s) {
     if (a.M <= 8) return launch_skinny<SkinnyF32<1>>(a, s);
     if (a.M <= 16) return launch_skinny<SkinnyF32<2>>(a, s);
     return launch_skinny<SkinnyF32<4>>(a, s);
+}
+
+// fp32 NN products with few output tiles (f32_wave_split: BASELINE config 1,
+// 512 x 1024 x 1024): one 32 x 64 row block per workgroup, each wave running
+// its own K quarter through its own two LDS stages with no workgroup barrier
+// until the fixed-order sum of the four partials.  Operands as for
+// launch_gemm_f32_skinny; any M.  512 x 1024 x 1024 on one box: 12.2-13.1 us
+// against 15.9-16.5 us for the wave-split tiles with a barrier per stage;
+// three stages 13.8-14.8 us (a K quarter of eight stages then runs a ninth,
+// all-zero one: every round has the same shape), 32 x 32 blocks with two
+// workgroups per CU 12.2-13.5 us.
+hipError_t launch_gemm_f32_rowblocks(const GemmArgs& a, hipStream_t s) {
+    return launch_skinny<SkinnyF32Rows>(a, s);
 }
 
 }  // namespace vedic
