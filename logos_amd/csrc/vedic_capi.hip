@@ -347,10 +347,45 @@ __global__ void __launch_bounds__(256) colsum_reduce_kernel(const float* __restr
     colsum_reduce_block(part, nblocks, N, out, beta, blockIdx.x);
 }
 
+// The same sums with 16-byte loads, for N a multiple of 4 and 16-byte
+// aligned partials: a workgroup covers 16 columns (four chunks of four);
+// thread t takes chunk t % 4 of group g = t / 4, which adds blocks
+// [g q, (g + 1) q) in ascending order (q = ceil(nblocks / 64)); the 64 group
+// sums of each column are then added in ascending g.  Four times the
+// workgroups of colsum_reduce_kernel and every load of a thread in flight
+// together (GELU-backward's 256 x 4096 partials: 4.8 -> about 2 us).
+constexpr int kCsGroups = 64;
+__global__ void __launch_bounds__(256) colsum_reduce4_kernel(const float* __restrict__ part, int nblocks, int N,
+                                                             float* __restrict__ out, float beta) {
+    __shared__ float sh[kCsGroups][17];
+    const int c4 = threadIdx.x & 3, g = threadIdx.x >> 2;
+    const int j = blockIdx.x * 16 + 4 * c4;  // first of this thread's four columns
+    const int q = (nblocks + kCsGroups - 1) / kCsGroups;
+    const int b0 = min(nblocks, g * q), b1 = min(nblocks, b0 + q);
+    float4_t acc = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    if (j < N) {
+#pragma unroll 8
+        for (int b = b0; b < b1; ++b) acc += *reinterpret_cast<const float4_t*>(part + (int64_t)b * N + j);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sh[g][4 * c4 + e] = acc[e];
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        const int col = blockIdx.x * 16 + threadIdx.x;
+        float t = sh[0][threadIdx.x];
+        for (int k = 1; k < kCsGroups; ++k) t += sh[k][threadIdx.x];
+        if (col < N) out[col] = beta == 0.0f ? t : beta * out[col] + t;
+    }
+}
+
 static hipError_t launch_colsum_reduce(const float* part, int nblocks, int N, float* out, float beta,
                                        hipStream_t s) {
-    hipLaunchKernelGGL(colsum_reduce_kernel, dim3((unsigned)((N + 31) / 32)), dim3(256), 0, s, part, nblocks, N,
-                       out, beta);
+    if (N % 4 == 0 && ((uintptr_t)part & 15u) == 0)
+        hipLaunchKernelGGL(colsum_reduce4_kernel, dim3((unsigned)((N + 15) / 16)), dim3(256), 0, s, part, nblocks,
+                           N, out, beta);
+    else
+        hipLaunchKernelGGL(colsum_reduce_kernel, dim3((unsigned)((N + 31) / 32)), dim3(256), 0, s, part, nblocks, N,
+                           out, beta);
     return hipGetLastError();
 }
 
