@@ -72,3 +72,29 @@ def test_probability_copy_full_size_rows():
     masked = np.arange(seq)[None, :] > rows[:, None]
     assert np.all(got[masked] == 0.0)  # masked entries: zero content times 1/l
     close(got, want, "seq 8192 rows")
+
+
+@pytest.mark.parametrize("kmax", [50, 70, 17])
+def test_probability_copy_walk_width(kmax):
+    """The row maximum at key kmax and every other score 0 (Q = e0, K[kmax] =
+    3 e0, no mask), checked against the closed form of the reference's
+    16-key walk (FA_TILE = 16, cuda/VedicGEMM.cu:898): keys of 16-key tiles
+    before the one holding kmax were written with the stale maximum 0, so
+    they hold exp(0) / l; keys from that tile on hold exp(s - 3) / l, with
+    l = sum over keys of exp(s - 3).  kmax = 50 is where a 32-key walk
+    differs (it would give keys 32..47 exp(-3) / l)."""
+    seq, dh = 96, 16
+    Q = np.zeros((seq, dh), np.float32)
+    K = np.zeros((seq, dh), np.float32)
+    Q[:, 0] = 1.0
+    K[kmax, 0] = 3.0
+    S = np.zeros(seq)
+    S[kmax] = 3.0
+    l = np.exp(S - 3.0).sum()
+    t0 = kmax // 16 * 16
+    want = np.where(np.arange(seq) < t0, 1.0 / l, np.exp(S - 3.0) / l)
+    v = vedic()
+    attn = torch.zeros((seq, seq), device="cuda")
+    v.flash_attention_fwd(dev(Q), dev(K), dev(np.zeros((seq, dh), np.float32)), attn=attn, scale=1.0, causal=False)
+    got = host(attn).astype(np.float64)
+    assert np.allclose(got, want[None, :], rtol=2e-6, atol=0.0), f"kmax {kmax}: max rel {np.max(np.abs(got / want - 1)):.2e}"
