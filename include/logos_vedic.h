@@ -282,9 +282,10 @@ int vedic_gemm_f16_scatter(const void* X, int M, int K, const void* W, int N, fl
  * head_cols; out_dtype F32; epilogue NONE, alpha 1, beta 0, no colsum or
  * preact (VEDIC_STATUS_BAD_EPILOGUE otherwise); desc->A unused; desc->lda is
  * the heads' leading dimension (>= head_cols).  nheads <= 64.
- * One launch when head_cols is a multiple of 64, N > 64 and every head, B and
- * the leading dimensions are aligned as for the 16-byte-load path; otherwise
- * the per-head calls themselves (same result).  With fp32 heads and N > 1024
+ * One launch when head_cols is a multiple of 64, N > 64, M > 32 and every
+ * head, B and the leading dimensions are aligned as for the 16-byte-load path
+ * (then each per-head product is one MFMA chain per output, which the launch
+ * repeats); otherwise the per-head calls themselves (same result).  With fp32 heads and N > 1024
  * the heads are first cast into an M x K binary16 block of the stream's
  * workspace. */
 int vedic_gemm_gather(const vedic_gemm_desc_t* desc, const void* const* heads, int nheads, int head_cols);

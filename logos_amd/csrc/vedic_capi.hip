@@ -1582,7 +1582,12 @@ extern "C" int vedic_gemm_gather(const vedic_gemm_desc_t* d, const void* const* 
     bool heads_ok = head_cols % 64 == 0 && d->lda % (amp ? 4 : 8) == 0 && d->lda < (amp ? kMaxLd / 2 : kMaxLd);
     for (int h = 0; h < nheads && heads_ok; ++h) heads_ok = aligned16(a_heads[h]);
     const bool b_ok = aligned16(d->B) && d->ldb % 8 == 0 && d->N % 8 == 0 && d->ldb < kMaxLd;
-    if (!heads_ok || !b_ok || d->N <= 64) {
+    // One launch only where each per-head product runs one MFMA chain per
+    // output over its head's k range, as the head-ordered kernels do: not on
+    // the narrow tiles (N <= 64) or the decode kernel (M <= 32), whose waves
+    // split the contraction and add partials, nor split over K.
+    const bool chain = d->N > 64 && d->M > 32 && choose_ksplit(d->M, d->N, head_cols, device_cu_count(), true) == 1;
+    if (!heads_ok || !b_ok || !chain) {
         // the per-head products themselves
         const int64_t n = (int64_t)d->M * d->N;
         hipLaunchKernelGGL(zero_rows_kernel, dim3(ew_blocks(n, 4)), dim3(kEwThreads), 0, s, static_cast<float*>(d->C), d->ldc, d->M, d->N);

@@ -98,6 +98,8 @@ def test_gather_shapes(M, N, hc, nheads, amp):
     (200, 256, 32, 4, True, None),   # head_cols not a multiple of 64: per-head calls
     (200, 256, 64, 4, False, 72),    # heads with a leading dimension above head_cols (one launch)
     (200, 256, 64, 4, True, 66),     # fp32 heads whose rows are not 16-byte aligned: per-head calls
+    (3, 1032, 192, 5, True, None),   # M <= 32 (the per-head products' decode kernel splits K): per-head calls
+    (20, 512, 64, 8, False, None),
 ])
 def test_gather_strided_and_fallback(M, N, hc, nheads, amp, lda):
     _case(M, N, hc, nheads, amp, seed=3 * M + hc, lda=lda)
