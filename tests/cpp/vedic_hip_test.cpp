@@ -12,6 +12,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <stdexcept>
 #include <vector>
 
@@ -365,6 +366,58 @@ static void test_residual() {
     EXPECT(same, "fp16 residual != X + A.W");
 }
 
+// The stacked attention-output projection against the reference's loop
+// (cuda/ModelGPU.cu:889-890, 976-986): concat zeroed, then per head the
+// product of its binary16-cast output with W_O[h] added in (beta = 1), bit for
+// bit, from fp32 head outputs (cuda_amp_gemm_heads) and from binary16 ones
+// (cuda_gemm_fp16_heads); the row-stacked W_O equals the per-block casts.
+static void test_stacked_wo() {
+    Rng r(53);
+    const int M = 300, DH = 64, H = 4, D = 136;
+    std::vector<GPUTensor> ho, wo;
+    std::vector<HalfTensor> ho16;
+    std::vector<const float*> hp, wp;
+    std::vector<const __half*> hp16;
+    for (int h = 0; h < H; ++h) {
+        ho.push_back(upload(rand_vec(r, (size_t)M * DH), M, DH));
+        wo.push_back(upload(rand_vec(r, (size_t)DH * D, 0.05), DH, D));
+        ho16.push_back(half_alloc(M, DH));
+        cuda_cast_fp32_to_fp16(ho.back().data, ho16.back().data, M * DH);
+    }
+    for (int h = 0; h < H; ++h) {
+        hp.push_back(ho[h].data);
+        wp.push_back(wo[h].data);
+        hp16.push_back(ho16[h].data);
+    }
+    HalfTensor W16 = half_alloc(H * DH, D);
+    cuda_cast_stack_fp16(wp.data(), H, DH, D, W16.data);
+    HalfTensor blk = half_alloc(DH, D);
+    bool stack_ok = true;
+    for (int h = 0; h < H; ++h) {
+        cuda_cast_fp32_to_fp16(wo[h].data, blk.data, DH * D);
+        std::vector<uint16_t> a((size_t)DH * D), b((size_t)DH * D);
+        HIP_CHECK(hipMemcpy(a.data(), blk.data, a.size() * 2, hipMemcpyDeviceToHost));
+        HIP_CHECK(hipMemcpy(b.data(), W16.data + (size_t)h * DH * D, b.size() * 2, hipMemcpyDeviceToHost));
+        stack_ok = stack_ok && a == b;
+    }
+    EXPECT(stack_ok, "row-stacked W_O != per-block casts");
+    std::vector<float> zeros((size_t)M * D, 0.0f);
+    GPUTensor ref = upload(zeros, M, D);
+    for (int h = 0; h < H; ++h)
+        cuda_gemm_fp16_fp32out(ho16[h].data, M, DH, W16.data + (size_t)h * DH * D, D, ref.data, 1.0f, 1.0f);
+    GPUTensor c32 = gpu_alloc(M, D), c16 = gpu_alloc(M, D);
+    cuda_amp_gemm_heads(hp.data(), H, M, DH, W16.data, D, c32.data);
+    cuda_gemm_fp16_heads(hp16.data(), H, M, DH, W16.data, D, c16.data);
+    auto want = download(ref), g32 = download(c32), g16 = download(c16);
+    bool same32 = true, same16 = true;
+    for (size_t i = 0; i < want.size(); ++i) {
+        same32 = same32 && std::memcmp(&g32[i], &want[i], 4) == 0;
+        same16 = same16 && std::memcmp(&g16[i], &want[i], 4) == 0;
+    }
+    EXPECT(same32, "cuda_amp_gemm_heads != per-head beta = 1 products");
+    EXPECT(same16, "cuda_gemm_fp16_heads != per-head beta = 1 products");
+}
+
 // Layer normalisation: a constant row gives beta exactly; a two-valued row
 // [a, b] gives gamma (+-h) / sqrt(h^2 + eps) + beta, h = (a - b) / 2; the
 // binary16 copy equals the cast of the fp32 rows.
@@ -448,6 +501,8 @@ int main() {
         std::printf("fp16 path done\n");
         test_residual();
         std::printf("residual done\n");
+        test_stacked_wo();
+        std::printf("stacked W_O done\n");
         test_layernorm();
         std::printf("layernorm done\n");
         test_errors_and_verify();
