@@ -5,7 +5,8 @@
 // so it is bound by HBM bandwidth, not by the matrix cores; the kernels are
 // built to keep as many weight bytes in flight as possible:
 //  * one workgroup per 32 output columns (256 workgroups for N = 8192), all
-//    M <= 32 rows in one 32 x 32 MFMA block (rows past M load as zeros);
+//    M <= 32 rows in one 32 x 32 block of the MFMA C layout (rows past M
+//    load as zeros);
 //  * the four waves split K into contiguous quarters.  Each wave keeps four
 //    stages of A and B in flight in its own LDS region and refills a stage
 //    as soon as its MFMAs have read it.  A wave reads only what it loaded
@@ -23,7 +24,12 @@
 // [k][32 columns] rows of 64 bytes read with ds_read_b64_tr_b16, conflict free
 // without a swizzle).
 //
-// fp32 (v_mfma_f32_32x32x2_f32): 32-deep stages.
+// fp32, M <= 16 (SkinnyF32Small): v_mfma_f32_4x4x1_16b_f32 on one or two
+// eight-row groups, a quarter or half of the 32 x 32 x 2 MFMA's time; layouts
+// at the type.  M = 1 x 1024 x 8192 on one box: 7.3 -> 5.5 us (loads alone
+// 3.4 us, the output store and the kernel's end about 0.7 us).
+//
+// fp32, 16 < M <= 32 (v_mfma_f32_32x32x2_f32): 32-deep stages.
 //  * A: 32 rows x 32 k (128-byte rows, chunks swizzled as in the tiled
 //    kernels); lane (r, h) reads chunk 2c + h of row r with one ds_read_b128:
 //    four consecutive k, one for each of four MFMAs.
@@ -57,6 +63,8 @@ struct SkinnyF16 {
     static constexpr int ST = 4, STAGE = 8192, NB = 1;  // 4 KiB of A + 4 KiB of B per stage
     static constexpr bool kUniformRounds = false;
     using T = _Float16;
+    typedef float16_t Acc[NB];  // 32 x 32 MFMA blocks
+    __device__ __forceinline__ static void to_c(const Acc& acc, float16_t (&c)[NB]) { c[0] = acc[0]; }
     uint32_t aoff[4], boff[4];
     int ak[4], bk[4];
     __device__ __forceinline__ void init(const GemmArgs& a, int m0, int n0, int lane) {
@@ -111,6 +119,11 @@ struct SkinnyF32 {
     static constexpr int ST = ST_, STAGE = 4096 * (1 + NB);
     static constexpr bool kUniformRounds = true;
     using T = float;
+    typedef float16_t Acc[NB];
+    __device__ __forceinline__ static void to_c(const Acc& acc, float16_t (&c)[NB]) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) c[b] = acc[b];
+    }
     // Instruction i of a side fills bytes [1024 i, 1024 (i + 1)) of the
     // side's 4 KiB; lane q lands at +16 q.
     uint32_t aoff[4], boff[4 * NB];
@@ -165,6 +178,96 @@ struct SkinnyF32 {
     }
 };
 
+// fp32 operands for M <= 8 NA (NA = 1, 2), 32-deep stages, on the 4 x 4 x 1
+// MFMA (v_mfma_f32_4x4x1_16b_f32: sixteen independent 4 x 4 blocks, one k
+// each).  Blocks 0-7 take rows 0-3 and blocks 8-15 rows 4-7 of an eight-row
+// group g, block b columns 4 (b mod 8) .. + 3, all at the same k: lane l
+// supplies A[8 g + l mod 4 + 4 (l / 32)][k] and B[k][l mod 32], and holds
+// C[8 g + i + 4 (l / 32)][l mod 32] in its register i -- registers 4 g + i of
+// the 32 x 32 MFMA's C layout, so the fixed-order reduction and the
+// epilogues of the 32 x 32 blocks apply unchanged (the rows past 8 NA are
+// zero).  One instruction covers 8 x 32 outputs of one k in 8 cycles, the
+// fp32 matrix rate; the 32 x 32 x 2 MFMA computes all 32 rows whatever M is,
+// 64 cycles for 32 x 32 outputs of two k: four (NA = 1) or two (NA = 2)
+// times the matrix time.  (Measured and not kept: for M <= 4, blocks 8-15 on
+// the next k instead of rows 4-7, half the instructions, ran slower, 6.1
+// against 5.5 us; 64-deep stages, the whole K quarter in flight at once in
+// the full 160 KiB of LDS, 6.2 us.)
+//  * B: 32 k rows x 32 columns (128-byte rows, no swizzle); a lane reads one
+//    value per k with ds_read_b32 (lanes l and l + 32 read the same word).
+//  * A: 8 NA rows x 32 k (128-byte rows); a lane reads four consecutive k of
+//    its row with one ds_read_b128.  The 16-byte chunk c of row r sits at
+//    position c ^ ((r / 2) mod 4), so the eight rows of a group, which a
+//    wave reads at one chunk index, fall in eight distinct 16-byte bank
+//    groups.
+template <int NA>
+struct SkinnyF32Small {
+    static constexpr int BK = 32;
+    static constexpr int NB = 1;
+    static constexpr int L = NA + 4;
+    static constexpr int ST = 4, STAGE = 4096 + 1024 * NA;  // B, then A
+    static constexpr bool kUniformRounds = true;
+    using T = float;
+    typedef float4_t Acc[NA];
+    uint32_t aoff[NA], boff[4];
+    int ak[NA], bk[4];
+    __device__ __forceinline__ static int swz_a(int row) { return (row >> 1) & 3; }
+    __device__ __forceinline__ void init(const GemmArgs& a, int m0, int n0, int lane) {
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            // instruction i fills A rows 8 i .. 8 i + 7: lane q at row 8 i + q / 8, position q mod 8
+            const int row = 8 * i + (lane >> 3);
+            const int c = (lane & 7) ^ swz_a(row);
+            aoff[i] = m0 + row < a.M ? (uint32_t)(row * a.lda * 4 + c * 16) : kOob;
+            ak[i] = 4 * c;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int k = 8 * i + (lane >> 3);
+            const int col = n0 + 4 * (lane & 7);
+            boff[i] = col + 4 <= a.N ? (uint32_t)((int64_t)k * a.ldb * 4 + col * 4) : kOob;
+            bk[i] = k;
+        }
+    }
+    __device__ __forceinline__ void issue(const GemmArgs& a, int m0, int k0, int krem, char* dst) const {
+        const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(static_cast<const T*>(a.A) + (int64_t)m0 * a.lda + k0);
+        const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(static_cast<const T*>(a.B) + (int64_t)k0 * a.ldb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(dst + i * 1024), 16,
+                                                     bk[i] < krem ? boff[i] : kOob, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < NA; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(dst + 4096 + i * 1024), 16,
+                                                     ak[i] + 4 <= krem ? aoff[i] : kOob, 0, 0, 0);
+    }
+    __device__ __forceinline__ static void consume(const char* la, int lane, Acc& acc) {
+        const int arow = (lane & 3) + 4 * (lane >> 5);
+#pragma unroll
+        for (int c = 0; c < BK / 4; ++c) {
+            float4_t av[NA];
+#pragma unroll
+            for (int g = 0; g < NA; ++g) {
+                const int row = 8 * g + arow;
+                av[g] = *reinterpret_cast<const float4_t*>(la + 4096 + row * 128 + ((c ^ swz_a(row)) << 4));
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float bv = *reinterpret_cast<const float*>(la + (4 * c + q) * 128 + 4 * (lane & 31));
+#pragma unroll
+                for (int g = 0; g < NA; ++g) acc[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(av[g][q], bv, acc[g], 0, 0, 0);
+            }
+        }
+    }
+    __device__ __forceinline__ static void to_c(const Acc& acc, float16_t (&c)[1]) {
+        c[0] = float16_t{};
+#pragma unroll
+        for (int g = 0; g < NA; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) c[0][4 * g + i] = acc[g][i];
+    }
+};
+
 template <class Sk, int KIND>
 __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs a) {
     constexpr int BK = Sk::BK, ST = Sk::ST, STAGE = Sk::STAGE, L = Sk::L, NB = Sk::NB;
@@ -196,9 +299,8 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs a) {
         sk.issue(a, m0, k0 < K ? k0 : 0, ke - k0, buf + wave * STAGE);
     };
 
-    float16_t acc[NB];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) acc[b] = float16_t{};
+    typename Sk::Acc acc;
+    for (auto& v : acc) v = {};
 #pragma unroll
     for (int st = 0; st < ST; ++st) issue(st, Ss[st]);
     // Every round but the last refills each stage after reading it.  The
@@ -235,10 +337,12 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs a) {
     // fixed-order reduction of the four partial sums through LDS
     __syncthreads();
     float* red = reinterpret_cast<float*>(s0);
+    float16_t part[NB];
+    Sk::to_c(acc, part);
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) red[((wave * NB + b) * 16 + e) * 64 + lane] = acc[b][e];
+        for (int e = 0; e < 16; ++e) red[((wave * NB + b) * 16 + e) * 64 + lane] = part[b][e];
     __syncthreads();
     if (wave != 0) return;
     float16_t sum[1][NB];
@@ -262,9 +366,9 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs a) {
 VEDIC_SKINNY_KERNELS(SkinnyF16<1>);
 VEDIC_SKINNY_KERNELS(SkinnyF16<2>);
 VEDIC_SKINNY_KERNELS(SkinnyF16<4>);
-VEDIC_SKINNY_KERNELS(SkinnyF32<1>);
-VEDIC_SKINNY_KERNELS(SkinnyF32<2>);
 VEDIC_SKINNY_KERNELS(SkinnyF32<4>);
+VEDIC_SKINNY_KERNELS(SkinnyF32Small<1>);
+VEDIC_SKINNY_KERNELS(SkinnyF32Small<2>);
 #ifndef VEDIC_F32_ROWS_NB
 #define VEDIC_F32_ROWS_NB 2
 #endif
@@ -298,8 +402,8 @@ hipError_t launch_gemm_f16_skinny(const GemmArgs& a, hipStream_t s) {
 // fp32: A, B 16-byte aligned, lda / ldb multiples of 4 and < 2^22, N a
 // multiple of 4 (checked by the caller); M <= 32, op NN.
 hipError_t launch_gemm_f32_skinny(const GemmArgs& a, hipStream_t s) {
-    if (a.M <= 8) return launch_skinny<SkinnyF32<1>>(a, s);
-    if (a.M <= 16) return launch_skinny<SkinnyF32<2>>(a, s);
+    if (a.M <= 8) return launch_skinny<SkinnyF32Small<1>>(a, s);
+    if (a.M <= 16) return launch_skinny<SkinnyF32Small<2>>(a, s);
     return launch_skinny<SkinnyF32<4>>(a, s);
 }
 

@@ -377,11 +377,13 @@ def test_split_k_epilogues():
 
 # ------------------------------------------------------- fp32 skinny and split-K
 
-@pytest.mark.parametrize("M", [1, 3, 16, 32])
+@pytest.mark.parametrize("M", [1, 3, 5, 8, 9, 16, 17, 32])
 @pytest.mark.parametrize("K,N", [(32, 4), (100, 36), (1000, 264), (1024, 8192), (2052, 132)])
 def test_skinny_m_fp32(M, K, N):
-    """M <= 32 strict-fp32 NN products take the fp32 decode kernel: partial
-    32-deep stages, quarters past K, several rounds, column edges."""
+    """M <= 32 strict-fp32 NN products take the fp32 decode kernel (M <= 8
+    and M <= 16 on the 4 x 4 x 1 MFMA with one or two eight-row groups, the
+    rest on 32 x 32 x 2): partial 32-deep stages, quarters past K, several
+    rounds, column edges."""
     vedic = V()
     rng = np.random.default_rng(zlib.crc32(f"skinny32-{M}-{K}-{N}".encode()))
     A, B = normal(rng, (M, K)), normal(rng, (K, N), std=0.05)
