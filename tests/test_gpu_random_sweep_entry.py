@@ -10,7 +10,15 @@
     the float64 normalisation and the library's own cast;
   * the checked GEMM (its check must pass on positive data), the bias
     gradient against float64 column sums, and the allocation-free entry
-    point bit for bit against vedic_gemm (or its size error).
+    point bit for bit against vedic_gemm (or its size error);
+  * the AMP dispatch (amp_gemm: a float32 activation against a binary16
+    shadow weight, or the float32 weight when there is none) against the
+    fp64 oracle and, with a shadow weight and M > 32, bit for bit against
+    the library's own cast followed by the fp16 GEMM;
+  * the binary16 casts that pack and stack several matrices, bit for bit
+    against a clamp to +-65504 and torch's round to nearest even;
+  * the attention backward over several heads in one launch, and the
+    forward's probability copy against the restated tile walk.
 
 Every case is its own test item, seeded by its index.
 """
@@ -23,7 +31,7 @@ import pytest
 torch = pytest.importorskip("torch")
 
 from oracle import oracle as o  # noqa: E402
-from tests._gpu_helpers import dev, fp32_tol, host, normal  # noqa: E402
+from tests._gpu_helpers import FP16_TOL, check, dev, fp32_tol, host, normal  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -172,3 +180,98 @@ def test_random_noalloc_matches_gemm(case):
     assert outs[0][0] in (_lib.STATUS_OK, _lib.STATUS_TOO_LARGE), f"{label}: no-allocation status {outs[0][0]}"
     if outs[0][0] == _lib.STATUS_OK:
         assert torch.equal(outs[0][1], outs[1][1]), f"{label}: differs from vedic_gemm"
+
+
+@pytest.mark.parametrize("case", range(40))
+def test_random_amp_gemm(case):
+    v = V()
+    R = random.Random(9000 + case)
+    rng = np.random.default_rng(9000 + case)
+    M, N, K = _dims(R, 2e8)
+    shadow = R.random() < 0.75
+    form = R.choice(["plain", "bias", "bias_gelu"])
+    label = f"AMP case {case}: M {M} N {N} K {K} shadow {shadow} {form}"
+    A = normal(rng, (M, K)) * np.float32(R.choice([1.0, 1.0, 3e4]))  # some rows reach the +-65504 clamp
+    W = normal(rng, (K, N), std=0.05)
+    bias = normal(rng, (N,), std=0.1)
+    tA, tW = dev(A), dev(W)
+    W16 = v.cast_fp32_to_fp16(tW) if shadow else None
+    kw = {} if form == "plain" else dict(bias=dev(bias), gelu=form == "bias_gelu")
+    got = host(v.amp_gemm(tA, W16, None if shadow else tW, **kw))
+    Ar = o.f16_round(A) if shadow else A
+    Wr = o.f16_round(W) if shadow else W
+    tol = FP16_TOL if shadow else fp32_tol(K)
+    check(got, o.NN, Ar, Wr, tol=tol, bias=None if form == "plain" else bias, gelu=form == "bias_gelu",
+          label=label)
+    if shadow and M > 32:  # (M <= 32: the fp16 call takes the decode kernel, the AMP call the tiles)
+        epi = {"plain": v.EPI_NONE, "bias": v.EPI_BIAS, "bias_gelu": v.EPI_BIAS_GELU}[form]
+        ref = host(v.gemm(v.OP_NN, v.cast_fp32_to_fp16(tA), W16, bias=None if form == "plain" else dev(bias),
+                          epilogue=epi))
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"{label}: differs from cast + fp16 GEMM"
+
+
+def _half_clamped(x):
+    return torch.clamp(x, -65504.0, 65504.0).half()
+
+
+@pytest.mark.parametrize("case", range(20))
+def test_random_cast_pack_and_stack(case):
+    v = V()
+    R = random.Random(10000 + case)
+    rng = np.random.default_rng(10000 + case)
+    n = R.randint(1, 64)
+    rows, cols = R.randint(1, 300), R.randint(1, 300)
+    label = f"cast case {case}: {n} matrices of {rows} x {cols}"
+    srcs = [dev(normal(rng, (rows, cols)) * np.float32(R.choice([1.0, 1e3, 1e5]))) for _ in range(n)]
+    packed = v.cast_pack_fp16(srcs)
+    stacked = v.cast_stack_fp16(srcs)
+    for i, t in enumerate(srcs):
+        want = _half_clamped(t)
+        assert torch.equal(packed[:, i * cols:(i + 1) * cols], want), f"{label}: packed matrix {i}"
+        assert torch.equal(stacked[i * rows:(i + 1) * rows], want), f"{label}: stacked matrix {i}"
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_random_attention_bwd_heads(case):
+    v = V()
+    R = random.Random(11000 + case)
+    rng = np.random.default_rng(11000 + case)
+    H = R.randint(1, 8)
+    seq = R.randint(1, 300)
+    dh = R.choice([R.randint(1, 128), 64, 128])
+    m = _mask(R)
+    scale = float(1.0 / np.sqrt(dh))
+    label = f"attention backward heads case {case}: {H} heads seq {seq} DH {dh} mask {m}"
+    Qs, Ks, Vs, dOs = ([normal(rng, (seq, dh)) for _ in range(H)] for _ in range(4))
+    tQ, tK, tV, tdO = ([dev(x) for x in xs] for xs in (Qs, Ks, Vs, dOs))
+    lses = [torch.empty(seq, device="cuda") for _ in range(H)]
+    Os = [v.flash_attention_fwd(tQ[h], tK[h], tV[h], scale=scale, lse=lses[h], **_attn_kw(m)) for h in range(H)]
+    dQs, dKs, dVs = v.flash_attention_bwd_heads(tQ, tK, tV, Os, tdO, lses, scale=scale, **_attn_kw(m))
+    tol = fp32_tol(max(seq, 64 if dh <= 64 else 128))
+    for h in range(H):
+        want = o.flash_attention_bwd_f64(Qs[h], Ks[h], Vs[h], dOs[h], scale, *m)
+        err = o.grad_rel_err((host(dQs[h]), host(dKs[h]), host(dVs[h])), want)
+        assert err <= tol, f"{label}: head {h} {err:.3e}"
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_random_attention_probability_copy(case):
+    v = V()
+    R = random.Random(12000 + case)
+    rng = np.random.default_rng(12000 + case)
+    seq = R.randint(1, 260)
+    dh = R.choice([R.randint(1, 128), 64, 128])
+    m = _mask(R)
+    scale = float(1.0 / np.sqrt(dh))
+    label = f"probability copy case {case}: seq {seq} DH {dh} mask {m}"
+    Q, K, Vv = normal(rng, (seq, dh), std=1.5), normal(rng, (seq, dh), std=1.5), normal(rng, (seq, dh))
+    prior = normal(rng, (seq, seq))
+    attn = dev(prior)
+    out = v.flash_attention_fwd(dev(Q), dev(K), dev(Vv), scale=scale, attn=attn, **_attn_kw(m))
+    plain = v.flash_attention_fwd(dev(Q), dev(K), dev(Vv), scale=scale, **_attn_kw(m))
+    assert torch.equal(out, plain), f"{label}: the output changes with the copy"
+    want = o.flash_attention_probs(Q, K, scale, *m, prior=prior)
+    got = host(attn)
+    rowmax = np.max(np.abs(want), axis=1, keepdims=True)
+    bad = np.abs(got - want) > 2e-5 * np.abs(want) + 1e-6 * rowmax
+    assert not bad.any(), f"{label}: {int(bad.sum())} entries off"
