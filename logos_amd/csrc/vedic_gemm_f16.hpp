@@ -137,7 +137,7 @@ struct Side {
     // Direct loads of one stage.  `tile` points at element (mn0, k0) (KC) or
     // (k0, mn0) (MC); krem = K - k0 (<= 0 past the range: zeros, no memory
     // touched).  Branch free, so every stage's loads have the same shape.
-    __device__ __forceinline__ void load(const _Float16* tile, char* lds, int wave, int lane, int krem) const {
+    __device__ __forceinline__ void load(const _Float16* tile, char* lds, int wave, int /*lane*/, int krem) const {
         const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(tile);
 #pragma unroll
         for (int i = 0; i < NLD; ++i)
