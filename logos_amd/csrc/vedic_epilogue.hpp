@@ -52,18 +52,32 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, 0x7FFFFFFF, 0x00020000);
 }
 
+// CPOL: the store's cache-policy bits (0, or kStoreDevice below).
+template <int CPOL = 0>
 __device__ __forceinline__ void st_f32(float v, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rs, (int)voff, (int)soff, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rs, (int)voff, (int)soff, CPOL);
 }
 
 __device__ __forceinline__ float ld_f32(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)voff, (int)soff, 0));
 }
 
+template <int CPOL = 0>
 __device__ __forceinline__ void st_f16(float v, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
     _Float16 h = (_Float16)v;
-    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, h), rs, (int)voff, (int)soff, 0);
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, h), rs, (int)voff, (int)soff, CPOL);
 }
+
+// Device-scope stores (the sc1 bit of a gfx950 vector store).  A persistent
+// GEMM writes its last work item's output with them, so fewer of those lines
+// are left dirty in the XCDs' L2s for the release at the kernel's end to
+// write back (after a 256 x 256 product's last burst, about 32 MB).  Measured
+// with bench.py, same box, two repetitions each: the forward + backward block
+// 785.4-785.7 -> 776.0-778.2 us (its dW, FFN-down and GELU-backward products
+// gain most), the FFN-up and the LM head unchanged within 0.3 us; the LM head
+// gained 2 us on two other boxes.  Device-scope stores for every tile were
+// slower: the earlier bursts are written back under the next tile's K loop.
+constexpr int kStoreDevice = 16;
 
 __device__ __forceinline__ float ld_f16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
     uint16_t b = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)voff, (int)soff, 0);
@@ -84,7 +98,7 @@ __device__ __forceinline__ bool epi_wants_bias(const GemmArgs& a) {
 // guarantees (32*MI) * ld * 4 < 2^31 for ldc and ldp.
 // bias_pre: the NI bias values of this lane's columns, already loaded by the
 // caller (columns past N as 0), or null to load them here.
-template <int KIND, bool CHECK, int MI, int NI>
+template <int KIND, bool CHECK, int MI, int NI, int CPOL = 0>
 __device__ __forceinline__ void epilogue(const GemmArgs& a, void* Cp, const float16_t (&acc)[MI][NI], int row0,
                                          int col0, int lane, const float* bias_pre = nullptr) {
     const int l32 = lane & 31, h = lane >> 5;
@@ -181,44 +195,44 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, void* Cp, const floa
                 offsets(j, i, g, r, ldcb, ccol, oc, op, sc, sp);
                 float v = acc[i][j][e];
                 if constexpr (KIND == EK_PLAIN) {
-                    st_f32(v, rc, oc, sc);
+                    st_f32<CPOL>(v, rc, oc, sc);
                 } else if constexpr (KIND == EK_BIAS) {
-                    st_f32(v + bj, rc, oc, sc);
+                    st_f32<CPOL>(v + bj, rc, oc, sc);
                 } else if constexpr (KIND == EK_BIAS_GELU) {
-                    st_f32(gelu_tanh(v + bj), rc, oc, sc);
+                    st_f32<CPOL>(gelu_tanh(v + bj), rc, oc, sc);
                 } else if constexpr (KIND == EK_BIAS_GELU_PRE) {
                     v += bj;
-                    st_f32(v, rp, op, sp);
-                    st_f32(gelu_tanh(v), rc, oc, sc);
+                    st_f32<CPOL>(v, rp, op, sp);
+                    st_f32<CPOL>(gelu_tanh(v), rc, oc, sc);
                 } else if constexpr (KIND == EK_ACCUM) {
-                    st_f32(cur_c[e] + v, rc, oc, sc);
+                    st_f32<CPOL>(cur_c[e] + v, rc, oc, sc);
                 } else if constexpr (KIND == EK_GELU_BWD) {
                     v *= gelu_tanh_grad(cur_p[e]);
-                    st_f32(v, rc, oc, sc);
+                    st_f32<CPOL>(v, rc, oc, sc);
                     if (!CHECK || oc != kOob) csum += v;
                 } else if constexpr (KIND == EK_RESIDUAL) {
                     // the bias is added to the product before the residual,
                     // as the reference's GEMM + bias then residual_add_kernel
                     const float t = want_bias ? v + bj : v;
-                    if (pre) st_f32(t, rp, op, sp);
-                    st_f32(cur_c[e] + t, rc, oc, sc);
+                    if (pre) st_f32<CPOL>(t, rp, op, sp);
+                    st_f32<CPOL>(cur_c[e] + t, rc, oc, sc);
                 } else if constexpr (KIND == EK_LINEAR_CS) {
                     v = __builtin_fmaf(v, a.alpha, bj);
-                    st_f32(v, rc, oc, sc);
+                    st_f32<CPOL>(v, rc, oc, sc);
                     if (!CHECK || oc != kOob) csum += v;
                 } else {
                     const int epi = a.epi;
                     if (epi & EPI_ALPHA) v *= a.alpha;
                     if (epi & EPI_BETA) v += a.beta * cur_c[e];
                     if (!(epi & EPI_RESID) || (epi & EPI_BIAS)) v += bj;
-                    if (epi & EPI_PREACT) st_f32(v, rp, op, sp);
+                    if (epi & EPI_PREACT) st_f32<CPOL>(v, rp, op, sp);
                     if (epi & EPI_RESID) v = cur_c[e] + v;
                     if (epi & EPI_GELU) v = gelu_tanh(v);
                     if (epi & EPI_GELU_BWD) v *= gelu_tanh_grad(cur_p[e]);
                     if (f16out)
-                        st_f16(v, rc, oc, sc);
+                        st_f16<CPOL>(v, rc, oc, sc);
                     else
-                        st_f32(v, rc, oc, sc);
+                        st_f32<CPOL>(v, rc, oc, sc);
                     if (!CHECK || oc != kOob) csum += v;
                 }
             }
