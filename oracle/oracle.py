@@ -409,21 +409,27 @@ def grad_rel_err(got, want64) -> float:
 
 U32 = 2.0 ** -24  # unit roundoff of binary32
 U16 = 2.0 ** -11  # unit roundoff of binary16
+# Half the spacing of the subnormals: the absolute error of rounding to
+# nearest where the result is subnormal (binary32: 2^-150, binary16: 2^-25).
+# Below 2^-14 a binary16 result carries this absolute error, not U16 |x|.
+TINY = {U32: 2.0 ** -150, U16: 2.0 ** -25}
 
 
 def componentwise_ratio(got, want64, absdot, rounded=None, unit=U32) -> float:
-    """max over elements of (|got - want| - 2 unit |rounded|) / absdot: the
-    error of a dot product relative to its sum of |a_k b_k| (absdot), after
-    allowing two output roundings of size `unit` per element on the terms in
-    `rounded` (|want| by default; the caller adds |bias|, |beta C_old|).  A
-    K-term fp32 sum has ratio <= gamma_K = K u / (1 - K u) whatever the order
-    (recursive summation bound); random-sign data stays near sqrt(K) u.
-    Elements with absdot = 0 must be within the allowance exactly."""
+    """max over elements of (|got - want| - 2 (unit |rounded| + tiny)) /
+    absdot: the error of a dot product relative to its sum of |a_k b_k|
+    (absdot), after allowing two output roundings per element, each of size
+    `unit` on the terms in `rounded` (|want| by default; the caller adds
+    |bias|, |beta C_old|) or, where the result is subnormal, half the
+    subnormal spacing of the output format (TINY).  A K-term fp32 sum has
+    ratio <= gamma_K = K u / (1 - K u) whatever the order (recursive
+    summation bound); random-sign data stays near sqrt(K) u.  Elements with
+    absdot = 0 must be within the allowance exactly."""
     got = np.asarray(got, dtype=np.float64)
     want64 = np.asarray(want64, dtype=np.float64)
     absdot = np.asarray(absdot, dtype=np.float64)
     r = np.abs(want64) if rounded is None else np.asarray(rounded, dtype=np.float64)
-    excess = np.abs(got - want64) - 2.0 * unit * r
+    excess = np.abs(got - want64) - 2.0 * (unit * r + TINY.get(unit, 0.0))
     if not np.all(np.isfinite(excess)):
         return float("inf")
     pos = absdot > 0

@@ -12,6 +12,17 @@ Gathered products (vedic_gemm_gather) are checked bit for bit against the
 per-head beta = 1 products they replace, scattered ones (vedic_gemm_scatter)
 against the plain product's columns.
 
+A second sweep (test_random_gemm_layouts) places the operands and C inside
+wider buffers: leading dimensions padded by up to a few thousand elements,
+start offsets of 1-8 elements, operands with at most four rows at leading
+dimensions around 2^22 (the fp16 kernels' 32-bit tile offsets stop there,
+and such operands take the element-wise kernels); sizes on the tile edges
+(63-65, 127-129, ..., 1023, 1025); binary16 output; alpha and beta with
+bias, GELU alone and the saved pre-activation.  Columns of C past N must
+stay untouched.  Its first run found only the test's componentwise bound
+lacking the absolute rounding of binary16 subnormal outputs (2^-25): every
+flagged output was the correctly rounded binary16 of the exact value.
+
 Every case is its own test item, seeded by its index, so a failure names
 its case and can be run alone.  A larger run of the same sweep found that
 the gathered product once took its one-launch path for M <= 32, where the
@@ -31,7 +42,10 @@ from tests._gpu_helpers import FP16_TOL, check, dev, fp32_tol, host, normal  # n
 pytestmark = pytest.mark.gpu
 
 OPS = {0: o.NN, 1: o.NT, 2: o.TN}
-N_GEMM, N_GATHER, N_SCATTER = 240, 60, 24
+N_GEMM, N_GATHER, N_SCATTER, N_LAYOUT = 240, 60, 24, 120
+BIG_LD = 1 << 22
+EDGES = [63, 64, 65, 95, 96, 97, 127, 128, 129, 191, 192, 193, 255, 256, 257, 383, 384, 385, 511, 512, 513,
+         1023, 1025]
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -175,3 +189,87 @@ def test_random_scatter(case):
     full = host(v.gemm(v.OP_NN, X, W))
     for h in range(nh):
         assert np.array_equal(host(hs[h]), full[:, h * hc:(h + 1) * hc]), f"{label}: head {h} differs"
+
+
+def _edge_dim(R):
+    r = R.random()
+    if r < 0.25:
+        return R.randint(1, 40)
+    if r < 0.55:
+        return R.choice(EDGES)
+    if r < 0.85:
+        return R.randint(41, 900)
+    return R.choice([1024, 1536, 2048, 3072]) + R.choice([0, 0, 1, 8, 31])
+
+
+def _in_wider(v, R, x, f16, few_rows):
+    """x placed in a wider, offset buffer on the device (fp32, or binary16
+    by the library's cast); returns (view, leading dimension, offset)."""
+    r, c = x.shape
+    pad = R.choice([0, 0, 0, 1, 3, 7, 8, 64, 129, R.randint(0, 3000)])
+    if few_rows and R.random() < 0.5:
+        pad = max(R.choice([BIG_LD - 8, BIG_LD, BIG_LD + 8]) - c, 0)
+    off = R.choice([0, 0, 0, 1, 2, 4, 8])
+    ld = c + pad
+    buf = torch.zeros(r * ld + off + 8, device="cuda", dtype=torch.float16 if f16 else torch.float32)
+    view = buf[off:off + r * ld].view(r, ld)[:, :c]
+    view.copy_(v.cast_fp32_to_fp16(dev(x)) if f16 else dev(x))
+    return view, ld, off
+
+
+@pytest.mark.parametrize("case", range(N_LAYOUT))
+def test_random_gemm_layouts(case):
+    v = V()
+    R = random.Random(4000 + case)
+    rng = np.random.default_rng(4000 + case)
+    op = R.choice([0, 0, 1, 2])
+    dtype = R.choice(["f32", "f16", "f16", "amp"] if op == 0 else ["f32", "f16", "f16"])
+    M, N, K = _edge_dim(R), _edge_dim(R), _edge_dim(R)
+    while M * N * K > 3e8:
+        M, N, K = max(1, M // 2), max(1, N // 2), max(1, K // 2)
+    f16out = dtype != "f32" and R.random() < 0.25
+    epi = R.choice(["none", "bias", "bias_gelu", "bias_gelu_pre", "gelu", "alpha", "beta", "alpha_beta_bias"])
+    if f16out and epi == "bias_gelu_pre":
+        epi = "bias_gelu"
+    alpha = R.choice([1.0, 0.5, -2.0, 0.125]) if epi in ("alpha", "alpha_beta_bias") else 1.0
+    beta = R.choice([1.0, 0.5, -1.0]) if epi in ("beta", "alpha_beta_bias") else 0.0
+    A = normal(rng, (K, M) if op == 2 else (M, K))
+    B = normal(rng, (N, K) if op == 1 else (K, N), std=0.05)
+    tA, lda, offa = _in_wider(v, R, A, dtype == "f16", A.shape[0] <= 4)
+    tB, ldb, offb = _in_wider(v, R, B, dtype != "f32", B.shape[0] <= 4)
+    Ar = A if dtype == "f32" else o.f16_round(A)
+    Br = B if dtype == "f32" else o.f16_round(B)
+    tol = (fp32_tol(K) if dtype == "f32" else FP16_TOL) + (2.0 ** -11 if f16out else 0.0)
+    bias = normal(rng, (N,), std=0.1)
+    C0 = normal(rng, (M, N))
+    cpad = R.choice([0, 0, 1, 5, 64, R.randint(0, 2000)])
+    odt = torch.float16 if f16out else torch.float32
+    Cbuf = torch.zeros((M, N + cpad), device="cuda", dtype=odt)
+    C = Cbuf[:, :N]
+    if beta != 0.0:
+        C.copy_(dev(C0).to(odt))
+        C0 = host(C).astype(np.float32)
+    label = (f"layout case {case}: op {op} {dtype} M {M} N {N} K {K} epilogue {epi} alpha {alpha} beta {beta} "
+             f"f16 out {f16out} lda {lda}+{offa} ldb {ldb}+{offb} ldc {N + cpad}")
+    kw = dict(alpha=alpha, beta=beta, out_dtype=odt)
+    ref = dict(bias=None, gelu=False)
+    P = None
+    if epi in ("bias", "alpha_beta_bias"):
+        kw.update(bias=dev(bias), epilogue=v.EPI_BIAS)
+        ref["bias"] = bias
+    elif epi in ("bias_gelu", "bias_gelu_pre"):
+        kw.update(bias=dev(bias), epilogue=v.EPI_BIAS_GELU)
+        ref.update(bias=bias, gelu=True)
+        if epi == "bias_gelu_pre":
+            P = torch.empty((M, N + R.choice([0, 3, 100])), device="cuda")[:, :N]
+            kw["preact"] = P
+    elif epi == "gelu":
+        kw["epilogue"] = v.EPI_GELU
+        ref["gelu"] = True
+    got = host(v.gemm(op, tA, tB, C, **kw))
+    check(got, OPS[op], Ar, Br, tol=tol, alpha=alpha, beta=beta, C0=C0 if beta != 0.0 else None,
+          f16_out=f16out, label=label, **ref)
+    if P is not None:
+        check(host(P), OPS[op], Ar, Br, tol=tol, bias=bias, label=label + " (pre-activation)")
+    if cpad:
+        assert not np.any(host(Cbuf[:, N:])), f"{label}: values written past column N"

@@ -485,6 +485,27 @@ def test_componentwise_ratio_definition():
     assert o.componentwise_ratio(np.array([[np.nan]]), np.array([[0.0]]), np.array([[1.0]])) == float("inf")
 
 
+def test_componentwise_ratio_binary16_subnormals():
+    """A binary16 output below 2^-14 rounds with an absolute error of up to
+    2^-25 (half the subnormal spacing), which U16 |x| does not cover: products
+    with K = 1..4 and small values, rounded correctly to binary16, pass the
+    binary16 allowance; the same outputs flushed to zero (a planted mistake)
+    do not, nor do they pass without the subnormal term."""
+    rng = np.random.default_rng(5)
+    A = (rng.standard_normal((256, 2)) * 0.01).astype(np.float32)
+    B = (rng.standard_normal((2, 64)) * 0.01).astype(np.float32)
+    want, absdot = o.gemm_f64(o.NN, A, B)
+    got = want.astype(np.float16).astype(np.float64)
+    sub = np.abs(want) < 2.0 ** -14
+    assert sub.sum() > 1000
+    assert o.componentwise_ratio(got, want, absdot, unit=o.U16) <= 2 * o.U32
+    flushed = np.where(np.abs(got) < 2.0 ** -14, 0.0, got)
+    assert o.componentwise_ratio(flushed, want, absdot, unit=o.U16) > 1e-3
+    # without the subnormal term the correct outputs would fail
+    excess = np.abs(got - want) - 2.0 * o.U16 * np.abs(want)
+    assert np.max(excess / absdot) > 2 * 2 * o.U32
+
+
 # ------------------------------------------- attention probability copy (Aptr)
 
 REF_FA_TILE = 16  # `#define FA_TILE 16`, /root/reference/cuda/VedicGEMM.cu:898
