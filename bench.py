@@ -20,11 +20,12 @@ The default run prints one JSON line with the metric named in BASELINE.json plus
                 rocprofv3 FETCH_SIZE / WRITE_SIZE summary, scaled by a copy
                 kernel of known size (None when no summary is committed);
   cpu_baseline  the reference CPU path on a bounded sample of the same workload:
-                all host cores (at most 16) running the bitwise restatement in
-                oracle/ sharded by 64-row blocks as `value`, and one thread (the
+                all host cores (at most 16) as `value` and one thread beside it
+                in `single_thread`, with the CPU model.  Both run the
                 reference's own vedic_gemm built from its sources into
-                oracle/_ref where that exists, else the restatement) beside it
-                in `single_thread`, with the CPU model.
+                oracle/_ref where that exists (kind "reference"; the threads
+                take blocks of output rows), else the bitwise restatement in
+                oracle/ (kind "port", 64-row blocks).
 """
 from __future__ import annotations
 
@@ -352,15 +353,48 @@ def baseline_threads() -> int:
     return max(1, min(n, 16))
 
 
+def _ref_rows(o, g, B, bias):
+    """The reference's own path for one GEMM of the workload on a block of
+    output rows: its GEMM (vedic_gemm / vedic_gemm_bias, or the transpose +
+    vedic_gemm of gemm_backward) and the element-wise work that follows it
+    in the reference (gelu; gelu_backward + bias_backward; the residual add)."""
+    op, epi = g["op"], g["epi"]
+
+    def run(a, h=None, x=None):
+        if op == "NN":
+            C = o.ref_vedic_gemm_bias(a, B, bias) if epi in ("bias", "bias_gelu", "bias_residual") else o.ref_vedic_gemm(a, B)
+        elif op == "NT":
+            C = o.ref_gemm_nt(a, B)
+        else:
+            C = o.ref_gemm_tn(a, B)
+        if epi == "bias_gelu":
+            C = o.ref_gelu(C)
+        if epi == "gelu_bwd":  # ffn_backward's gelu_backward + bias_backward
+            C = o.ref_gelu_backward(h, C)
+            o.ref_bias_backward(C)
+        if epi == "bias_residual":  # the residual add after the FFN-down
+            C = x + C
+        return C
+
+    return run
+
+
 def _cpu_gemm_sample(w: dict, seconds: float, nthreads: int, seed: int):
     """(flops, seconds, kind, parts): the reference CPU path on row samples of
-    the workload's GEMMs, repeated until about `seconds`.  One thread runs the
-    reference's own vedic_gemm built in place when that exists (oracle/_ref),
-    else the bitwise restatement; several threads run the restatement sharded
-    by 64-row blocks (the same bits, each element summed in the same order)."""
+    the workload's GEMMs, repeated until about `seconds`.  Where the
+    reference's own CPU GEMM is built in place (oracle/_ref, kind
+    "reference") it runs on `nthreads` host threads, each taking one block of
+    output rows (the reference functions are called through ctypes, which
+    releases the interpreter lock; rows of a product are independent and each
+    element is summed in the same order whichever rows share a call, so the
+    GEMM's bits are the one-call result); else the bitwise restatement runs
+    (kind "port"), sharded by 64-row blocks on `nthreads` threads."""
+    from concurrent.futures import ThreadPoolExecutor
+
     from oracle import oracle as o
 
-    kind = "reference" if nthreads == 1 and o.ref_available() else "port"
+    kind = "reference" if o.ref_available() else "port"
+    pool = ThreadPoolExecutor(nthreads) if kind == "reference" and nthreads > 1 else None
     rng = np.random.default_rng(seed)
     per_gemm = max(seconds / len(w["gemms"]), 0.5)
     total_flops = 0.0
@@ -388,20 +422,20 @@ def _cpu_gemm_sample(w: dict, seconds: float, nthreads: int, seed: int):
         reps = 0
         while True:
             if kind == "reference":
-                if op == "NN":
-                    C = (o.ref_vedic_gemm_bias(A, B, bias) if g["epi"] in ("bias", "bias_gelu", "bias_residual")
-                         else o.ref_vedic_gemm(A, B))
-                elif op == "NT":
-                    C = o.ref_gemm_nt(A, B)
+                run = _ref_rows(o, g, B, bias)
+                if pool is None:
+                    C = run(A, Hs, Xs)
                 else:
-                    C = o.ref_gemm_tn(A, B)
-                if g["epi"] == "bias_gelu":
-                    C = o.ref_gelu(C)
-                if g["epi"] == "gelu_bwd":  # ffn_backward's gelu_backward + bias_backward
-                    C = o.ref_gelu_backward(Hs, C)
-                    o.ref_bias_backward(C)
-                if g["epi"] == "bias_residual":  # the residual add after the FFN-down
-                    C = Xs + C
+                    # output rows are A's rows (NN, NT) or A's columns (TN: A is K x rows)
+                    cuts = np.linspace(0, rows, nthreads + 1).astype(int)
+                    jobs = []
+                    for r0, r1 in zip(cuts[:-1], cuts[1:]):
+                        if r1 > r0:
+                            a = A[:, r0:r1] if op == "TN" else A[r0:r1]
+                            jobs.append(pool.submit(run, np.ascontiguousarray(a),
+                                                    None if Hs is None else Hs[r0:r1],
+                                                    None if Xs is None else Xs[r0:r1]))
+                    C = [j.result() for j in jobs]
             else:
                 if op == "NN":
                     C = (o.vedic_gemm_bias(A, B, bias, nthreads=nthreads)
@@ -425,14 +459,16 @@ def _cpu_gemm_sample(w: dict, seconds: float, nthreads: int, seed: int):
         total_flops += reps * 2.0 * rows * K * N
         total_t += dt
         parts.append(f"{op} {rows}/{M} rows x{reps}")
+    if pool is not None:
+        pool.shutdown()
     return total_flops, total_t, kind, parts
 
 
 def cpu_baseline(w: dict, seconds: float, seed: int = 7):
     """The reference CPU path on row samples of the workload's GEMMs: all host
-    cores (the restatement, sharded by 64-row blocks) as `value`, and one
-    thread (the reference's algorithm as written) beside it, each for about
-    half of `seconds`.  Rows of every GEMM are independent and cost the same,
+    cores (the reference build on blocks of rows where it is built, else the
+    restatement sharded by 64-row blocks) as `value`, and one thread beside
+    it, each for about half of `seconds`.  Rows of every GEMM are independent and cost the same,
     so TFLOP/s over a row sample is the rate of the whole GEMM."""
     n = baseline_threads()
     f1, t1, k1, p1 = _cpu_gemm_sample(w, seconds / 2, 1, seed)
@@ -443,7 +479,8 @@ def cpu_baseline(w: dict, seconds: float, seed: int = 7):
         "unit": "TFLOP/s",
         "cores": n,
         "kind": kn,
-        "sample": f"{'; '.join(pn)} ({fn / 1e9:.1f} GFLOP in {tn:.1f} s), {n} threads by 64-row blocks, {flags}",
+        "sample": (f"{'; '.join(pn)} ({fn / 1e9:.1f} GFLOP in {tn:.1f} s), {n} threads"
+                   f"{' by row blocks of the reference build' if kn == 'reference' else ' by 64-row blocks'}, {flags}"),
         "single_thread": {"value": f1 / t1 / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": k1,
                           "sample": f"{'; '.join(p1)} ({f1 / 1e9:.1f} GFLOP in {t1:.1f} s), {flags}"},
         "cpu_model": cpu_model(),
