@@ -77,6 +77,8 @@ __device__ __forceinline__ void st_f16(float v, __amdgpu_buffer_rsrc_t rs, uint3
 // gain most), the FFN-up and the LM head unchanged within 0.3 us; the LM head
 // gained 2 us on two other boxes.  Device-scope stores for every tile were
 // slower: the earlier bursts are written back under the next tile's K loop.
+// The decode and row-block kernels, whose workgroups write once, use them
+// for every store.
 constexpr int kStoreDevice = 16;
 
 __device__ __forceinline__ float ld_f16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
