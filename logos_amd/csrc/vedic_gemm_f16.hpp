@@ -648,8 +648,9 @@ __global__ void __launch_bounds__(WGM* WGN * WGK * 64) gemm_f16_kernel(GemmArgs 
         }
         const bool full = (row0 + WM <= args.M) && (col0 + WN <= args.N);
         if (WGK == 1 || wk == 0) {
-            // the last work item's output with device-scope stores (kStoreDevice)
-            if (KIND != EK_GENERIC && full && !more && args.ksplit == 1)
+            // the last work item's output (or split-K partial) with
+            // device-scope stores (kStoreDevice)
+            if (KIND != EK_GENERIC && full && !more)
                 epilogue<KIND, false, MI, NI, kStoreDevice>(args, cp, acc, row0, col0, lane,
                                                             pre_bias ? bias_pre : nullptr);
             else if (KIND != EK_GENERIC && full)
