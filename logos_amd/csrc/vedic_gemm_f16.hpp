@@ -705,7 +705,7 @@ struct CfgLarge {  // 256 x 256, eight waves of 128 x 64
 #ifndef VEDIC_F16_SMALL_ST
 #define VEDIC_F16_SMALL_ST 3
 #endif
-struct CfgSmall {  // 128 x 128, four waves of 64 x 64, two workgroups per CU (2 x 64 KiB of LDS)
+struct CfgSmall {  // 128 x 128, four waves of 64 x 64, three 32 KiB stages, one workgroup per CU
     static constexpr int BM = 128, BN = 128, BK = 64, ST = VEDIC_F16_SMALL_ST, WGM = 2, WGN = VEDIC_F16_SMALL_WGN, WGK = 1;
     static constexpr int PER_CU = VEDIC_F16_SMALL_PER_CU;
 };
